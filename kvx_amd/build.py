@@ -1,0 +1,90 @@
+"""Build libkvx_amd.so (the C-ABI library with the gfx950 HIP kernels) in-tree.
+
+Usage: python -m kvx_amd.build   (or kvx_amd.build.build() from Python)
+
+Every source is compiled with hipcc for gfx950 only.  Device-code flags:
+  -fhip-fp32-correctly-rounded-divide-sqrt  the FP8 quantizing cast divides by
+                                            the scale and must round exactly;
+  -fno-gpu-flush-denormals-to-zero          keep f32 subnormals (bit-exact
+                                            casts of tiny values);
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                            no packed-FP32 instructions.
+The library links with -Bsymbolic so its own entry points never resolve to a
+same-named symbol from another loaded library, and exports only kvx_* symbols
+(csrc/exports.map).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = REPO / "include"
+OBJ_DIR = PKG_DIR / "_build"
+LIB_PATH = PKG_DIR / "libkvx_amd.so"
+
+SOURCES = ["abi.cpp", "launch.cpp", "kernels.hip"]
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the kvx_amd build needs ROCm")
+    return path
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature;
+    # that line is expected and carries no information.
+    noise = "not a recognized feature for this target"
+    stderr = "\n".join(l for l in proc.stderr.splitlines() if noise not in l
+                       and "ignoring feature" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n"
+                           f"{proc.stdout}\n{proc.stderr}")
+    if verbose and stderr.strip():
+        print(stderr, file=sys.stderr, flush=True)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link LIB_PATH.  Always rebuilds."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    objs = []
+    for src in SOURCES:
+        obj = OBJ_DIR / (src + ".o")
+        _run([cc, *COMMON_FLAGS, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)],
+             verbose)
+        objs.append(str(obj))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs,
+          "-Wl,-Bsymbolic", "-Wl,--no-undefined",
+          f"-Wl,--version-script={CSRC / 'exports.map'}"], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,435 @@
+// Launch-path entry points of kvx_paged_kv.h and kvx_ext.h.
+//
+// Host validation reproduces the check order and status codes of the
+// reference launchers (kernels/kvx_paged_kv.cu:315-451 write, :493-716
+// prefill, :763-870 gather, :472-491 / :739-761 / :891-910 dispatch), so a
+// malformed call returns the same kvx_status_t as the reference before any
+// HIP call is made.  Checks this build adds come after every reference check
+// and only reject inputs on which the reference kernels would divide by zero
+// or dereference NULL:
+//   - block_size == 0 with a non-empty batch   -> INVALID_ARGUMENT
+//   - NULL io / cache / index data pointers     -> INVALID_ARGUMENT
+// F8_E4M3 caches (quantizing write, byte-copy gather, dequantizing gather)
+// are extensions; the reference returns UNSUPPORTED for them.
+#include <hip/hip_runtime.h>
+
+#include "kvx_ext.h"
+#include "kvx_internal.h"
+#include "kvx_paged_kv.h"
+
+namespace kvx {
+namespace {
+
+bool is_io_float(kvx_dtype_t dt) {
+  return dt == KVX_DTYPE_F16 || dt == KVX_DTYPE_BF16 || dt == KVX_DTYPE_F32;
+}
+
+// reference kvx_paged_kv.cu:269-289 (no size/dtype/data checks on this path)
+kvx_status_t check_io_3d(const kvx_tensor_desc_t *t, int32_t num_tokens,
+                         int32_t heads, int32_t head_dim) {
+  if (t->ndim != 3) return KVX_STATUS_INVALID_ARGUMENT;
+  if (t->shape[0] != num_tokens || t->shape[1] != heads ||
+      t->shape[2] != head_dim)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (t->stride[2] != 1 || t->stride[1] != (int64_t)head_dim ||
+      t->stride[0] != (int64_t)heads * head_dim)
+    return KVX_STATUS_UNSUPPORTED;
+  return KVX_STATUS_OK;
+}
+
+// reference kvx_paged_kv.cu:291-313
+kvx_status_t check_io_4d(const kvx_tensor_desc_t *t, int32_t seq_count,
+                         int32_t max_seq_len, int32_t heads,
+                         int32_t head_dim) {
+  if (t->ndim != 4) return KVX_STATUS_INVALID_ARGUMENT;
+  if (t->shape[0] != seq_count || t->shape[1] != max_seq_len ||
+      t->shape[2] != heads || t->shape[3] != head_dim)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (t->stride[3] != 1 || t->stride[2] != (int64_t)head_dim ||
+      t->stride[1] != (int64_t)heads * head_dim ||
+      t->stride[0] != (int64_t)max_seq_len * heads * head_dim)
+    return KVX_STATUS_UNSUPPORTED;
+  return KVX_STATUS_OK;
+}
+
+// Descriptor -> Geom.  Status codes as reference kvx_fill_cache_params
+// (kernels/kvx_paged_kv.cu:18-52): PACKED needs pack > 0 dividing head_dim;
+// layouts other than NHD/HND/HND_PACKED are UNSUPPORTED.  Any strides are
+// honoured.
+kvx_status_t fill_geom(const kvx_cache_desc_t *cache,
+                       const kvx_tensor_desc_t *t, Geom *g) {
+  const int64_t *s = t->stride;
+  g->s_piece = 0;
+  g->pad_ = 0;
+  switch (t->layout) {
+    case KVX_LAYOUT_BLOCK_NHD:
+      g->s_block = s[0];
+      g->s_off = s[1];
+      g->s_head = s[2];
+      g->s_inner = s[3];
+      g->pack = (int32_t)cache->head_dim;
+      return KVX_STATUS_OK;
+    case KVX_LAYOUT_BLOCK_HND:
+      g->s_block = s[0];
+      g->s_head = s[1];
+      g->s_off = s[2];
+      g->s_inner = s[3];
+      g->pack = (int32_t)cache->head_dim;
+      return KVX_STATUS_OK;
+    case KVX_LAYOUT_BLOCK_HND_PACKED: {
+      const int64_t pack = t->shape[4];
+      if (pack <= 0) return KVX_STATUS_INVALID_ARGUMENT;
+      if ((int64_t)cache->head_dim % pack != 0)
+        return KVX_STATUS_INVALID_ARGUMENT;
+      g->s_block = s[0];
+      g->s_head = s[1];
+      g->s_piece = s[2];
+      g->s_off = s[3];
+      g->s_inner = s[4];
+      g->pack = (int32_t)pack;
+      return KVX_STATUS_OK;
+    }
+    default:
+      return KVX_STATUS_UNSUPPORTED;
+  }
+}
+
+// Resolve a per-tensor F32 scale for the quantizing write
+// (KVX_SPEC.md:258-259: scale descriptor first, raw pointer as fallback).
+kvx_status_t resolve_write_scale(const kvx_scale_desc_t *desc,
+                                 const void *raw, const float **out) {
+  if (desc->data != nullptr) {
+    if (desc->size < sizeof(kvx_scale_desc_t))
+      return KVX_STATUS_INVALID_ARGUMENT;
+    if (desc->dtype != KVX_DTYPE_F32) return KVX_STATUS_UNSUPPORTED;
+    if (desc->granularity != KVX_SCALE_PER_TENSOR)
+      return KVX_STATUS_UNSUPPORTED;
+    *out = static_cast<const float *>(desc->data);
+    return KVX_STATUS_OK;
+  }
+  if (raw == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  *out = static_cast<const float *>(raw);
+  return KVX_STATUS_OK;
+}
+
+kvx_status_t resolve_gather_scale(const kvx_scale_desc_t *desc,
+                                  const float **out) {
+  if (desc->size < sizeof(kvx_scale_desc_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (desc->dtype != KVX_DTYPE_F32) return KVX_STATUS_UNSUPPORTED;
+  if (desc->granularity != KVX_SCALE_PER_TENSOR) return KVX_STATUS_UNSUPPORTED;
+  if (desc->data == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  *out = static_cast<const float *>(desc->data);
+  return KVX_STATUS_OK;
+}
+
+}  // namespace
+
+// `expected` is the payload dtype of the per-dtype helper; KVX_DTYPE_F8_E4M3
+// is this build's FP8 path, where io may be F16/BF16/F32 (quantize) or
+// F8_E4M3 (byte copy).
+kvx_status_t launch_write(const kvx_cache_desc_t *cache,
+                          const kvx_write_desc_t *write, int32_t tokens_per_seq,
+                          bool prefill, kvx_dtype_t expected, void *stream) {
+  if (cache == nullptr || write == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (prefill && tokens_per_seq <= 0) return KVX_STATUS_INVALID_ARGUMENT;
+  if (write->size < sizeof(kvx_write_desc_t)) return KVX_STATUS_INVALID_ARGUMENT;
+  if (write->io.size < sizeof(kvx_kv_io_desc_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (write->slots.size < sizeof(kvx_slot_mapping_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (prefill && (write->io.num_tokens % (uint32_t)tokens_per_seq) != 0)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != expected || cache->v.dtype != expected)
+    return KVX_STATUS_UNSUPPORTED;
+  const kvx_dtype_t io_dt = write->io.key.dtype;
+  if (expected == KVX_DTYPE_F8_E4M3) {
+    if (write->io.value.dtype != io_dt ||
+        !(is_io_float(io_dt) || io_dt == KVX_DTYPE_F8_E4M3))
+      return KVX_STATUS_UNSUPPORTED;
+  } else if (io_dt != expected || write->io.value.dtype != expected) {
+    return KVX_STATUS_UNSUPPORTED;
+  }
+  const int32_t heads = (int32_t)write->io.num_kv_heads;
+  const int32_t head_dim = (int32_t)write->io.head_dim;
+  if (heads != (int32_t)cache->num_kv_heads ||
+      head_dim != (int32_t)cache->head_dim)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  const int32_t num_tokens = (int32_t)write->io.num_tokens;
+  kvx_status_t st = check_io_3d(&write->io.key, num_tokens, heads, head_dim);
+  if (st != KVX_STATUS_OK) return st;
+  st = check_io_3d(&write->io.value, num_tokens, heads, head_dim);
+  if (st != KVX_STATUS_OK) return st;
+  if (write->slots.token_count != write->io.num_tokens)
+    return KVX_STATUS_INVALID_ARGUMENT;
+
+  WritePlan p;
+  st = fill_geom(cache, &cache->k, &p.gk);
+  if (st != KVX_STATUS_OK) return st;
+  st = fill_geom(cache, &cache->v, &p.gv);
+  if (st != KVX_STATUS_OK) return st;
+
+  const bool quant = expected == KVX_DTYPE_F8_E4M3 && io_dt != KVX_DTYPE_F8_E4M3;
+  p.k_scale = nullptr;
+  p.v_scale = nullptr;
+  if (quant) {
+    st = resolve_write_scale(&write->k_scale_desc, write->k_scale, &p.k_scale);
+    if (st != KVX_STATUS_OK) return st;
+    st = resolve_write_scale(&write->v_scale_desc, write->v_scale, &p.v_scale);
+    if (st != KVX_STATUS_OK) return st;
+  }
+
+  const int64_t total = (int64_t)num_tokens * heads * head_dim;
+  if (total == 0) return KVX_STATUS_OK;
+  if (write->slots.dtype != KVX_DTYPE_S32 && write->slots.dtype != KVX_DTYPE_S64)
+    return KVX_STATUS_INVALID_ARGUMENT;
+
+  // Checks added by this build (see file comment).
+  if (cache->block_size == 0) return KVX_STATUS_INVALID_ARGUMENT;
+  if (write->io.key.data == nullptr || write->io.value.data == nullptr ||
+      cache->k.data == nullptr || cache->v.data == nullptr ||
+      write->slots.slots == nullptr)
+    return KVX_STATUS_INVALID_ARGUMENT;
+
+  p.src_k = write->io.key.data;
+  p.src_v = write->io.value.data;
+  p.dst_k = cache->k.data;
+  p.dst_v = cache->v.data;
+  p.slots = write->slots.slots;
+  p.num_tokens = num_tokens;
+  p.slot_is64 = write->slots.dtype == KVX_DTYPE_S64;
+  p.heads = heads;
+  p.head_dim = head_dim;
+  p.block_size = (int32_t)cache->block_size;
+  p.num_blocks = (int32_t)cache->num_blocks;
+  p.conv = quant ? kConvQuant : kConvCopy;
+  p.io_dtype = io_dt;
+  p.cache_dtype = cache->k.dtype;
+  return enqueue_write(p, stream);
+}
+
+kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
+                           const kvx_gather_desc_t *gather,
+                           const kvx_scale_desc_t *k_scale,
+                           const kvx_scale_desc_t *v_scale, bool dequant,
+                           kvx_dtype_t expected, void *stream) {
+  if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (dequant && (k_scale == nullptr || v_scale == nullptr))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (gather->size < sizeof(kvx_gather_desc_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (gather->io.size < sizeof(kvx_kv_io_desc_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (gather->block_table.size < sizeof(kvx_block_table_t) ||
+      gather->seq_lens.size < sizeof(kvx_seq_lens_t))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != expected || cache->v.dtype != expected)
+    return KVX_STATUS_UNSUPPORTED;
+  const kvx_dtype_t io_dt = gather->io.key.dtype;
+  if (dequant) {
+    if (gather->io.value.dtype != io_dt || !is_io_float(io_dt))
+      return KVX_STATUS_UNSUPPORTED;
+  } else if (io_dt != expected || gather->io.value.dtype != expected) {
+    return KVX_STATUS_UNSUPPORTED;
+  }
+  if (gather->block_table.format != KVX_BLOCK_TABLE_PACKED)
+    return KVX_STATUS_UNSUPPORTED;
+  const int32_t heads = (int32_t)gather->io.num_kv_heads;
+  const int32_t head_dim = (int32_t)gather->io.head_dim;
+  if (heads != (int32_t)cache->num_kv_heads ||
+      head_dim != (int32_t)cache->head_dim)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if (gather->seq_lens.seq_count != gather->block_table.seq_count)
+    return KVX_STATUS_INVALID_ARGUMENT;
+  const int32_t seq_count = (int32_t)gather->block_table.seq_count;
+  const int32_t max_seq_len = (int32_t)gather->max_seq_len;
+  kvx_status_t st =
+      check_io_4d(&gather->io.key, seq_count, max_seq_len, heads, head_dim);
+  if (st != KVX_STATUS_OK) return st;
+  st = check_io_4d(&gather->io.value, seq_count, max_seq_len, heads, head_dim);
+  if (st != KVX_STATUS_OK) return st;
+
+  GatherPlan p;
+  st = fill_geom(cache, &cache->k, &p.gk);
+  if (st != KVX_STATUS_OK) return st;
+  st = fill_geom(cache, &cache->v, &p.gv);
+  if (st != KVX_STATUS_OK) return st;
+
+  p.k_scale = nullptr;
+  p.v_scale = nullptr;
+  if (dequant) {
+    st = resolve_gather_scale(k_scale, &p.k_scale);
+    if (st != KVX_STATUS_OK) return st;
+    st = resolve_gather_scale(v_scale, &p.v_scale);
+    if (st != KVX_STATUS_OK) return st;
+  }
+
+  const int64_t total = (int64_t)seq_count * max_seq_len * heads * head_dim;
+  if (total == 0) return KVX_STATUS_OK;
+  const kvx_dtype_t idx_dt = gather->block_table.index_dtype;
+  const kvx_dtype_t len_dt = gather->seq_lens.dtype;
+  const bool s32 = idx_dt == KVX_DTYPE_S32 && len_dt == KVX_DTYPE_S32;
+  const bool s64 = idx_dt == KVX_DTYPE_S64 && len_dt == KVX_DTYPE_S64;
+  if (!s32 && !s64) return KVX_STATUS_INVALID_ARGUMENT;
+
+  // Checks added by this build (see file comment).
+  if (cache->block_size == 0) return KVX_STATUS_INVALID_ARGUMENT;
+  if (gather->io.key.data == nullptr || gather->io.value.data == nullptr ||
+      cache->k.data == nullptr || cache->v.data == nullptr ||
+      gather->seq_lens.lengths == nullptr ||
+      (gather->block_table.max_blocks_per_seq > 0 &&
+       gather->block_table.indices == nullptr))
+    return KVX_STATUS_INVALID_ARGUMENT;
+
+  p.src_k = cache->k.data;
+  p.src_v = cache->v.data;
+  p.dst_k = gather->io.key.data;
+  p.dst_v = gather->io.value.data;
+  p.block_table = gather->block_table.indices;
+  p.seq_lens = gather->seq_lens.lengths;
+  p.index_is64 = s64;
+  p.seq_count = seq_count;
+  p.max_blocks_per_seq = (int32_t)gather->block_table.max_blocks_per_seq;
+  p.max_seq_len = max_seq_len;
+  p.heads = heads;
+  p.head_dim = head_dim;
+  p.block_size = (int32_t)cache->block_size;
+  p.num_blocks = (int32_t)cache->num_blocks;
+  p.conv = dequant ? kConvDequant : kConvCopy;
+  p.io_dtype = io_dt;
+  p.cache_dtype = cache->k.dtype;
+  return enqueue_gather(p, stream);
+}
+
+}  // namespace kvx
+
+using kvx::launch_gather;
+using kvx::launch_write;
+
+// ---------------------------------------------------------------------------
+// Exported C ABI.
+
+extern "C" {
+
+KVX_API kvx_status_t kvx_launch_write_kv_f32(const kvx_cache_desc_t *cache,
+                                             const kvx_write_desc_t *write,
+                                             void *stream) {
+  return launch_write(cache, write, 0, false, KVX_DTYPE_F32, stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_f16(const kvx_cache_desc_t *cache,
+                                             const kvx_write_desc_t *write,
+                                             void *stream) {
+  return launch_write(cache, write, 0, false, KVX_DTYPE_F16, stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_bf16(const kvx_cache_desc_t *cache,
+                                              const kvx_write_desc_t *write,
+                                              void *stream) {
+  return launch_write(cache, write, 0, false, KVX_DTYPE_BF16, stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv(const kvx_cache_desc_t *cache,
+                                         const kvx_write_desc_t *write,
+                                         void *stream) {
+  if (cache == nullptr || write == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
+  switch (cache->k.dtype) {
+    case KVX_DTYPE_F16:
+    case KVX_DTYPE_BF16:
+    case KVX_DTYPE_F32:
+    case KVX_DTYPE_F8_E4M3:
+      return launch_write(cache, write, 0, false, cache->k.dtype, stream);
+    default:
+      return KVX_STATUS_UNSUPPORTED;
+  }
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_prefill_f32(
+    const kvx_cache_desc_t *cache, const kvx_write_desc_t *write,
+    int32_t tokens_per_seq, void *stream) {
+  return launch_write(cache, write, tokens_per_seq, true, KVX_DTYPE_F32,
+                      stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_prefill_f16(
+    const kvx_cache_desc_t *cache, const kvx_write_desc_t *write,
+    int32_t tokens_per_seq, void *stream) {
+  return launch_write(cache, write, tokens_per_seq, true, KVX_DTYPE_F16,
+                      stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_prefill_bf16(
+    const kvx_cache_desc_t *cache, const kvx_write_desc_t *write,
+    int32_t tokens_per_seq, void *stream) {
+  return launch_write(cache, write, tokens_per_seq, true, KVX_DTYPE_BF16,
+                      stream);
+}
+
+KVX_API kvx_status_t kvx_launch_write_kv_prefill(
+    const kvx_cache_desc_t *cache, const kvx_write_desc_t *write,
+    int32_t tokens_per_seq, void *stream) {
+  if (cache == nullptr || write == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
+  switch (cache->k.dtype) {
+    case KVX_DTYPE_F16:
+    case KVX_DTYPE_BF16:
+    case KVX_DTYPE_F32:
+    case KVX_DTYPE_F8_E4M3:
+      return launch_write(cache, write, tokens_per_seq, true, cache->k.dtype,
+                          stream);
+    default:
+      return KVX_STATUS_UNSUPPORTED;
+  }
+}
+
+KVX_API kvx_status_t kvx_launch_gather_kv_f32(const kvx_cache_desc_t *cache,
+                                              const kvx_gather_desc_t *gather,
+                                              void *stream) {
+  return launch_gather(cache, gather, nullptr, nullptr, false, KVX_DTYPE_F32,
+                       stream);
+}
+
+KVX_API kvx_status_t kvx_launch_gather_kv_f16(const kvx_cache_desc_t *cache,
+                                              const kvx_gather_desc_t *gather,
+                                              void *stream) {
+  return launch_gather(cache, gather, nullptr, nullptr, false, KVX_DTYPE_F16,
+                       stream);
+}
+
+KVX_API kvx_status_t kvx_launch_gather_kv_bf16(const kvx_cache_desc_t *cache,
+                                               const kvx_gather_desc_t *gather,
+                                               void *stream) {
+  return launch_gather(cache, gather, nullptr, nullptr, false, KVX_DTYPE_BF16,
+                       stream);
+}
+
+KVX_API kvx_status_t kvx_launch_gather_kv(const kvx_cache_desc_t *cache,
+                                          const kvx_gather_desc_t *gather,
+                                          void *stream) {
+  if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
+  switch (cache->k.dtype) {
+    case KVX_DTYPE_F16:
+    case KVX_DTYPE_BF16:
+    case KVX_DTYPE_F32:
+    case KVX_DTYPE_F8_E4M3:
+      return launch_gather(cache, gather, nullptr, nullptr, false,
+                           cache->k.dtype, stream);
+    default:
+      return KVX_STATUS_UNSUPPORTED;
+  }
+}
+
+KVX_API kvx_status_t kvx_launch_gather_kv_dequant(
+    const kvx_cache_desc_t *cache, const kvx_gather_desc_t *gather,
+    const kvx_scale_desc_t *k_scale, const kvx_scale_desc_t *v_scale,
+    void *stream) {
+  if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != KVX_DTYPE_F8_E4M3) return KVX_STATUS_UNSUPPORTED;
+  return launch_gather(cache, gather, k_scale, v_scale, true,
+                       KVX_DTYPE_F8_E4M3, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+"""Torch-facing host helpers over the KVX C ABI.
+
+These build kvx_abi.h descriptors from torch tensors (shape, element strides,
+data pointer, memory type) and call libkvx_amd.so through ctypes.  torch is
+only the source of device memory and streams here; every byte is moved by the
+library's HIP kernels.  There is no fallback: if libkvx_amd.so is missing,
+``abi.load()`` raises.
+
+The calls mirror the reference's launch API (kernels/kvx_paged_kv.h:11-21):
+``write_kv`` -> kvx_launch_write_kv / kvx_launch_write_kv_prefill,
+``gather_kv`` -> kvx_launch_gather_kv / kvx_launch_gather_kv_dequant, and
+return the kvx_status_t as ``abi.Status``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import abi
+from .abi import DType, Layout, Memory, Status
+
+_TORCH_DTYPE = {
+    torch.float16: DType.F16,
+    torch.bfloat16: DType.BF16,
+    torch.float32: DType.F32,
+    torch.float8_e4m3fn: DType.F8_E4M3,
+    torch.int32: DType.S32,
+    torch.int64: DType.S64,
+}
+
+
+def dtype_code(t: torch.Tensor | torch.dtype) -> DType:
+    dt = t.dtype if isinstance(t, torch.Tensor) else t
+    if dt not in _TORCH_DTYPE:
+        raise ValueError(f"unsupported dtype {dt}")
+    return _TORCH_DTYPE[dt]
+
+
+def memory_of(t: torch.Tensor) -> Memory:
+    return Memory.DEVICE if t.is_cuda else Memory.HOST
+
+
+def tensor_desc(t: torch.Tensor, layout: Layout = Layout.BLOCK_CUSTOM,
+                dtype: DType | None = None) -> abi.TensorDesc:
+    """Descriptor of `t` as laid out in memory (its own shape and strides)."""
+    d = abi.TensorDesc()
+    d.size = C.sizeof(abi.TensorDesc)
+    d.dtype = int(dtype if dtype is not None else dtype_code(t))
+    d.layout = int(layout)
+    d.memory = int(memory_of(t))
+    d.ndim = t.dim()
+    for i in range(t.dim()):
+        d.shape[i] = t.shape[i]
+        d.stride[i] = t.stride(i)
+    d.data = t.data_ptr()
+    return d
+
+
+def cache_shape(layout: Layout, num_blocks: int, block_size: int, heads: int,
+                head_dim: int, pack: int = 8) -> tuple:
+    """Canonical shape of a cache tensor in `layout` (KVX_SPEC.md:50-56)."""
+    layout = Layout(layout)
+    if layout == Layout.BLOCK_NHD:
+        return (num_blocks, block_size, heads, head_dim)
+    if layout == Layout.BLOCK_HND:
+        return (num_blocks, heads, block_size, head_dim)
+    if layout == Layout.BLOCK_HND_PACKED:
+        return (num_blocks, heads, head_dim // pack, block_size, pack)
+    raise ValueError(layout)
+
+
+@dataclass
+class PagedCache:
+    """K and V cache tensors and the kvx_cache_desc_t describing them."""
+
+    key_cache: torch.Tensor
+    value_cache: torch.Tensor
+    k_layout: Layout
+    v_layout: Layout
+    num_blocks: int
+    block_size: int
+    heads: int
+    head_dim: int
+
+    def desc(self) -> abi.CacheDesc:
+        k = tensor_desc(self.key_cache, self.k_layout)
+        v = tensor_desc(self.value_cache, self.v_layout)
+        return abi.cache_desc(self.num_blocks, self.block_size, self.heads,
+                              self.head_dim, k, v)
+
+
+def alloc_cache(num_blocks: int, block_size: int, heads: int, head_dim: int,
+                dtype: torch.dtype, device, k_layout=Layout.BLOCK_NHD,
+                v_layout=None, pack: int = 8) -> PagedCache:
+    v_layout = k_layout if v_layout is None else v_layout
+    k = torch.empty(cache_shape(k_layout, num_blocks, block_size, heads, head_dim, pack),
+                    dtype=dtype, device=device)
+    v = torch.empty(cache_shape(v_layout, num_blocks, block_size, heads, head_dim, pack),
+                    dtype=dtype, device=device)
+    return PagedCache(k, v, Layout(k_layout), Layout(v_layout), num_blocks, block_size,
+                      heads, head_dim)
+
+
+def _stream_handle(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+    if isinstance(stream, torch.cuda.Stream):
+        return stream.cuda_stream
+    return int(stream)
+
+
+def build_write(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
+                slot_mapping: torch.Tensor, k_scale: torch.Tensor | None = None,
+                v_scale: torch.Tensor | None = None) -> abi.WriteDesc:
+    """kvx_write_desc_t for [T, H, D] key/value rows and [T] slots.  FP8
+    scales are one-element F32 device tensors, passed as PER_TENSOR scale
+    descriptors."""
+    T = key.shape[0]
+    w = abi.WriteDesc()
+    w.size = C.sizeof(abi.WriteDesc)
+    w.io.size = C.sizeof(abi.KvIoDesc)
+    w.io.key = tensor_desc(key)
+    w.io.value = tensor_desc(value)
+    w.io.num_tokens = T
+    w.io.num_kv_heads = key.shape[1] if key.dim() == 3 else 0
+    w.io.head_dim = key.shape[2] if key.dim() == 3 else 0
+    w.slots.size = C.sizeof(abi.SlotMapping)
+    w.slots.dtype = int(dtype_code(slot_mapping))
+    w.slots.token_count = slot_mapping.numel()
+    w.slots.invalid_slot = -1
+    w.slots.slots = slot_mapping.data_ptr()
+    if k_scale is not None:
+        w.k_scale_desc = abi.scale_desc(k_scale.data_ptr())
+    if v_scale is not None:
+        w.v_scale_desc = abi.scale_desc(v_scale.data_ptr())
+    return w
+
+
+def build_gather(key_out: torch.Tensor, value_out: torch.Tensor,
+                 block_table: torch.Tensor, seq_lens: torch.Tensor,
+                 max_seq_len: int) -> abi.GatherDesc:
+    S, mbps = block_table.shape
+    g = abi.GatherDesc()
+    g.size = C.sizeof(abi.GatherDesc)
+    g.io.size = C.sizeof(abi.KvIoDesc)
+    g.io.key = tensor_desc(key_out)
+    g.io.value = tensor_desc(value_out)
+    g.io.num_tokens = S * max_seq_len
+    g.io.num_kv_heads = key_out.shape[2]
+    g.io.head_dim = key_out.shape[3]
+    g.block_table = abi.make_block_table_packed(S, mbps, dtype_code(block_table),
+                                                block_table.data_ptr())
+    g.seq_lens = abi.make_seq_lens(seq_lens.numel(), dtype_code(seq_lens),
+                                   seq_lens.data_ptr())
+    g.max_seq_len = max_seq_len
+    return g
+
+
+def write_kv(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
+             slot_mapping: torch.Tensor, *, tokens_per_seq: int | None = None,
+             k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+             stream=None, entry: str = "launch") -> Status:
+    """Scatter rows into the paged cache.  entry = "launch" (kvx_paged_kv.h)
+    or "abi" (kvx_write_kv of kvx_abi.h)."""
+    lib = abi.load()
+    cd = cache.desc()
+    wd = build_write(cache, key, value, slot_mapping, k_scale, v_scale)
+    s = _stream_handle(stream)
+    if entry == "abi":
+        return Status(lib.kvx_write_kv(C.byref(cd), C.byref(wd), s))
+    if tokens_per_seq is not None:
+        return Status(lib.kvx_launch_write_kv_prefill(C.byref(cd), C.byref(wd),
+                                                      tokens_per_seq, s))
+    return Status(lib.kvx_launch_write_kv(C.byref(cd), C.byref(wd), s))
+
+
+def gather_kv(cache: PagedCache, key_out: torch.Tensor, value_out: torch.Tensor,
+              block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int, *,
+              k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+              stream=None, entry: str = "launch") -> Status:
+    """Gather sequences into contiguous [S, max_seq_len, H, D] buffers.
+    With k_scale/v_scale the FP8 cache is dequantized
+    (kvx_launch_gather_kv_dequant)."""
+    lib = abi.load()
+    cd = cache.desc()
+    gd = build_gather(key_out, value_out, block_table, seq_lens, max_seq_len)
+    s = _stream_handle(stream)
+    if entry == "abi":
+        return Status(lib.kvx_gather_kv(C.byref(cd), C.byref(gd), s))
+    if k_scale is not None or v_scale is not None:
+        ks = abi.scale_desc(k_scale.data_ptr())
+        vs = abi.scale_desc(v_scale.data_ptr())
+        return Status(lib.kvx_launch_gather_kv_dequant(C.byref(cd), C.byref(gd),
+                                                       C.byref(ks), C.byref(vs), s))
+    return Status(lib.kvx_launch_gather_kv(C.byref(cd), C.byref(gd), s))

@@ -1,0 +1,202 @@
+"""Seeded synthetic workloads for the five BASELINE configurations.
+
+Each function returns a `Workload` that holds only the index metadata
+(slot mapping, block table, sequence lengths) as numpy arrays plus the shapes
+and dtypes; payload data is generated on the device by the caller.  All
+randomness comes from numpy PCG64 with the seed recorded in the workload.
+
+  c1  TinyLlama-1.1B prefill write + gather, f16, H=4, D=64, bs=16,
+      8 seqs x 128 tokens, blocks from a seeded permutation of a 512 pool.
+  c2  Llama-3-8B decode write + full-context gather, bf16, H=8, D=128,
+      bs=16, 256 seqs, ctx ~ U[512, 8192], 5% of slots = -1.
+  c3  Llama-3-8B chunked prefill write, bf16, 16 x 2048 tokens, K in the
+      x-packed layout (x = 8), V plain NHD, random block assignment.
+  c4  c2 with an FP8 E4M3 cache: 128 decode tokens quantized with per-tensor
+      scales amax/448 from a seeded calibration batch, dequantizing gather.
+  c5  Llama-3-70B-shaped, bs=32, 64 seqs, ctx ~ U[16384, 32768], 32 prefill
+      tokens per seq written, full gather, blocks scattered over a pool of
+      about 200 GB of K+V.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .abi import DType, Layout
+
+
+@dataclass
+class Workload:
+    name: str
+    seed: int
+    heads: int
+    head_dim: int
+    block_size: int
+    num_blocks: int
+    cache_dtype: DType
+    io_dtype: DType
+    k_layout: Layout
+    v_layout: Layout
+    pack: int
+    # write
+    slots: np.ndarray            # [T] int64 or int32
+    tokens_per_seq: int | None   # prefill entry when set
+    # gather
+    block_table: np.ndarray      # [S, max_blocks_per_seq]
+    seq_lens: np.ndarray         # [S], same dtype as block_table
+    max_seq_len: int
+    layers: int = 1
+    notes: dict = field(default_factory=dict)
+
+    @property
+    def num_tokens(self) -> int:
+        return int(self.slots.size)
+
+    @property
+    def seq_count(self) -> int:
+        return int(self.block_table.shape[0])
+
+    @property
+    def max_blocks_per_seq(self) -> int:
+        return int(self.block_table.shape[1])
+
+    @property
+    def row_elems(self) -> int:
+        return self.heads * self.head_dim
+
+    def gathered_tokens(self) -> int:
+        n = np.minimum(self.seq_lens.astype(np.int64), self.max_seq_len)
+        n = np.minimum(n, self.max_blocks_per_seq * self.block_size)
+        return int(np.maximum(n, 0).sum())
+
+    def valid_write_tokens(self) -> int:
+        s = self.slots.astype(np.int64)
+        ok = (s >= 0) & (s // self.block_size < self.num_blocks)
+        return int(ok.sum())
+
+
+def dtype_bytes(dt: DType) -> int:
+    return {DType.F16: 2, DType.BF16: 2, DType.F32: 4, DType.F8_E4M3: 1}[DType(dt)]
+
+
+def write_bytes(w: Workload) -> int:
+    """Algorithmic bytes of one write: every valid row of K and V read from
+    io and written to the cache, plus the slot array (and two f32 scales
+    when quantizing)."""
+    e = w.row_elems
+    b = w.valid_write_tokens() * 2 * e * (dtype_bytes(w.io_dtype) + dtype_bytes(w.cache_dtype))
+    b += w.num_tokens * w.slots.itemsize
+    if w.cache_dtype != w.io_dtype:
+        b += 8
+    return int(b)
+
+
+def gather_bytes(w: Workload) -> int:
+    """Algorithmic bytes of one gather: gathered rows of K and V read from the
+    cache and written out, plus the block-table entries used and seq_lens."""
+    e = w.row_elems
+    n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
+    n = np.minimum(n, w.max_blocks_per_seq * w.block_size)
+    blocks = (n + w.block_size - 1) // w.block_size
+    b = int(n.sum()) * 2 * e * (dtype_bytes(w.cache_dtype) + dtype_bytes(w.io_dtype))
+    b += int(blocks.sum()) * w.block_table.itemsize + w.seq_count * w.seq_lens.itemsize
+    if w.cache_dtype != w.io_dtype:
+        b += 8
+    return int(b)
+
+
+def _slots_for(positions: np.ndarray, table_row: np.ndarray, bs: int) -> np.ndarray:
+    return table_row[positions // bs].astype(np.int64) * bs + positions % bs
+
+
+def c1_tinyllama(seed: int = 1) -> Workload:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    S, L, bs, pool = 8, 128, 16, 512
+    mbps = L // bs
+    table = rng.permutation(pool)[: S * mbps].reshape(S, mbps).astype(np.int32)
+    pos = np.arange(L)
+    slots = np.concatenate([_slots_for(pos, table[s], bs) for s in range(S)])
+    return Workload("c1_tinyllama_f16_prefill", seed, 4, 64, bs, pool, DType.F16,
+                    DType.F16, Layout.BLOCK_NHD, Layout.BLOCK_NHD, 8,
+                    slots.astype(np.int64), L, table,
+                    np.full(S, L, np.int32), L, layers=22)
+
+
+def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None):
+    lens = rng.integers(lo, hi, size=S, endpoint=True).astype(np.int64)
+    need = (lens + bs - 1) // bs
+    mbps = (max_len + bs - 1) // bs
+    used = int(need.sum())
+    pool = used if pool_blocks is None else int(pool_blocks)
+    if pool_blocks is None:
+        ids = rng.permutation(pool)
+    else:
+        ids = rng.choice(pool, size=used, replace=False)
+    table = np.full((S, mbps), -1, np.int64)
+    at = 0
+    for s in range(S):
+        table[s, : need[s]] = ids[at: at + need[s]]
+        at += need[s]
+    return lens, table, pool
+
+
+def c2_llama8b_decode(seed: int = 2, batch: int = 256) -> Workload:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    bs, L = 16, 8192
+    lens, table, pool = _decode_tables(rng, batch, 512, 8192, bs, L)
+    pos = lens - 1  # the new token is the last position of each context
+    slots = table[np.arange(batch), pos // bs] * bs + pos % bs
+    pad = rng.choice(batch, size=int(round(0.05 * batch)), replace=False)
+    slots[pad] = -1
+    return Workload("c2_llama3_8b_decode_bf16", seed, 8, 128, bs, pool, DType.BF16,
+                    DType.BF16, Layout.BLOCK_NHD, Layout.BLOCK_NHD, 8,
+                    slots.astype(np.int64), None, table.astype(np.int32),
+                    lens.astype(np.int32), L, layers=32,
+                    notes={"padded_slots": int(pad.size)})
+
+
+def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD) -> Workload:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    S, chunk, bs, pool = 16, 2048, 16, 8192
+    mbps = chunk // bs
+    table = rng.permutation(pool)[: S * mbps].reshape(S, mbps).astype(np.int32)
+    pos = np.arange(chunk)
+    slots = np.concatenate([_slots_for(pos, table[s], bs) for s in range(S)])
+    return Workload("c3_llama3_8b_prefill_packedK_bf16", seed, 8, 128, bs, pool,
+                    DType.BF16, DType.BF16, Layout.BLOCK_HND_PACKED, Layout(v_layout), 8,
+                    slots.astype(np.int64), chunk, table, np.full(S, chunk, np.int32),
+                    chunk)
+
+
+def c4_llama8b_fp8(seed: int = 4, batch: int = 128) -> Workload:
+    w = c2_llama8b_decode(seed, batch)
+    w.name = "c4_llama3_8b_decode_fp8_e4m3"
+    w.cache_dtype = DType.F8_E4M3
+    w.notes["calibration_seed"] = seed + 1000
+    w.notes["io_sigma"] = 2.0
+    return w
+
+
+def c5_llama70b_long(seed: int = 5, pool_blocks: int = 1_530_000,
+                     batch: int = 64) -> Workload:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    bs, L, tps = 32, 32768, 32
+    lens, table, pool = _decode_tables(rng, batch, 16384, 32768, bs, L, pool_blocks)
+    slots = []
+    for s in range(batch):
+        pos = np.arange(lens[s] - tps, lens[s])
+        slots.append(table[s, pos // bs] * bs + pos % bs)
+    return Workload("c5_llama3_70b_bs32_long_bf16", seed, 8, 128, bs, pool, DType.BF16,
+                    DType.BF16, Layout.BLOCK_NHD, Layout.BLOCK_NHD, 8,
+                    np.concatenate(slots).astype(np.int64), tps, table.astype(np.int32),
+                    lens.astype(np.int32), L)
+
+
+CONFIGS = {
+    "c1": c1_tinyllama,
+    "c2": c2_llama8b_decode,
+    "c3": c3_llama8b_prefill,
+    "c4": c4_llama8b_fp8,
+    "c5": c5_llama70b_long,
+}

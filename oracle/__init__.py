@@ -1,0 +1,151 @@
+"""Python access to the CPU oracle (oracle/kvx_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker and the timed CPU baseline.  The
+product (kvx_amd) never imports it.
+
+Buffers are numpy arrays (C-contiguous, any element type: they are passed as
+raw bytes).  Layout and dtype codes are the kvx_abi.h enum values.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from . import build as _build
+
+_LIB = None
+_I64P = C.POINTER(C.c_int64)
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not _build.ORACLE_LIB.exists():
+            _build.build_oracle()
+        L = C.CDLL(str(_build.ORACLE_LIB))
+        vp, i32, i64, f32, i = C.c_void_p, C.c_int32, C.c_int64, C.c_float, C.c_int
+        geom = [i, _I64P, i64]
+        L.oracle_cache_offset.argtypes = [i, _I64P, i64, i64, i64, i64, i64]
+        L.oracle_cache_offset.restype = i64
+        L.oracle_write_kv.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, i32, i32,
+                                                    i32, i32, i, i, f32, f32]
+        L.oracle_gather_kv.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32, i32,
+                                                     i32, i32, i32, i32, i32, i, i, f32,
+                                                     f32]
+        L.oracle_write_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, i32,
+                                                         i32, i32, i32, i]
+        L.oracle_write_kv_fast.restype = i
+        L.oracle_gather_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32,
+                                                          i32, i32, i32, i32, i32, i32, i]
+        L.oracle_gather_kv_fast.restype = i
+        L.oracle_f32_to_e4m3.argtypes = [f32]
+        L.oracle_f32_to_e4m3.restype = C.c_uint8
+        L.oracle_e4m3_to_f32.argtypes = [C.c_uint8]
+        L.oracle_e4m3_to_f32.restype = f32
+        L.oracle_f32_to_bf16.argtypes = [f32]
+        L.oracle_f32_to_bf16.restype = C.c_uint16
+        L.oracle_f32_to_f16.argtypes = [f32]
+        L.oracle_f32_to_f16.restype = C.c_uint16
+        L.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        L.oracle_f16_to_f32.restype = f32
+        L.oracle_quantize_e4m3.argtypes = [vp, i, i64, f32, vp]
+        L.oracle_dequantize_e4m3.argtypes = [vp, i64, f32, i, vp]
+        _LIB = L
+    return _LIB
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("oracle buffers must be C-contiguous")
+    return a.ctypes.data
+
+
+def _strides(s) -> C.Array:
+    arr = (C.c_int64 * 5)(*([int(x) for x in s] + [0] * (5 - len(s))))
+    return arr
+
+
+class Geometry:
+    """Layout, element strides and pack of one cache tensor."""
+
+    def __init__(self, layout: int, stride, pack: int = 1):
+        self.layout = int(layout)
+        self.stride = tuple(int(x) for x in stride)
+        self.pack = int(pack)
+
+    def args(self):
+        return [self.layout, C.cast(_strides(self.stride), _I64P), self.pack]
+
+
+def cache_offset(g: Geometry, block, offset, head, dim) -> int:
+    return lib().oracle_cache_offset(*g.args(), block, offset, head, dim)
+
+
+def write_kv(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache, slots,
+             *, heads, head_dim, block_size, num_blocks, io_dtype, cache_dtype,
+             k_scale=1.0, v_scale=1.0) -> None:
+    """Element-wise write (kernels/kvx_paged_kv.cu:93-124), in place."""
+    slots = np.ascontiguousarray(slots)
+    lib().oracle_write_kv(*gk.args(), *gv.args(), _ptr(key), _ptr(value),
+                          _ptr(key_cache), _ptr(value_cache), _ptr(slots),
+                          int(slots.dtype == np.int64), int(slots.size), heads,
+                          head_dim, block_size, num_blocks, int(io_dtype),
+                          int(cache_dtype), float(k_scale), float(v_scale))
+
+
+def gather_kv(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value_out,
+              block_table, seq_lens, *, seq_count, max_blocks_per_seq, max_seq_len,
+              heads, head_dim, block_size, num_blocks, cache_dtype, io_dtype,
+              k_scale=1.0, v_scale=1.0) -> None:
+    """Element-wise gather (kernels/kvx_paged_kv.cu:226-267), in place."""
+    block_table = np.ascontiguousarray(block_table)
+    seq_lens = np.ascontiguousarray(seq_lens)
+    if block_table.dtype != seq_lens.dtype:
+        raise ValueError("block table and seq_lens share one index dtype")
+    lib().oracle_gather_kv(*gk.args(), *gv.args(), _ptr(key_cache), _ptr(value_cache),
+                           _ptr(key_out), _ptr(value_out), _ptr(block_table),
+                           _ptr(seq_lens), int(block_table.dtype == np.int64),
+                           seq_count, max_blocks_per_seq, max_seq_len, heads, head_dim,
+                           block_size, num_blocks, int(cache_dtype), int(io_dtype),
+                           float(k_scale), float(v_scale))
+
+
+def write_kv_fast(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache, slots,
+                  *, heads, head_dim, block_size, num_blocks, elem_size) -> int:
+    slots = np.ascontiguousarray(slots)
+    return lib().oracle_write_kv_fast(*gk.args(), *gv.args(), _ptr(key), _ptr(value),
+                                      _ptr(key_cache), _ptr(value_cache), _ptr(slots),
+                                      int(slots.dtype == np.int64), int(slots.size),
+                                      heads, head_dim, block_size, num_blocks, elem_size)
+
+
+def gather_kv_fast(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out,
+                   value_out, block_table, seq_lens, *, seq_count, max_blocks_per_seq,
+                   max_seq_len, heads, head_dim, block_size, num_blocks,
+                   elem_size) -> int:
+    return lib().oracle_gather_kv_fast(*gk.args(), *gv.args(), _ptr(key_cache),
+                                       _ptr(value_cache), _ptr(key_out), _ptr(value_out),
+                                       _ptr(block_table), _ptr(seq_lens),
+                                       int(block_table.dtype == np.int64), seq_count,
+                                       max_blocks_per_seq, max_seq_len, heads, head_dim,
+                                       block_size, num_blocks, elem_size)
+
+
+def quantize_e4m3(x: np.ndarray, io_dtype: int, scale: float) -> np.ndarray:
+    """e4m3(sat(x / scale)) of a raw io buffer (f32 / f16 / bf16 bits)."""
+    x = np.ascontiguousarray(x)
+    n = x.size
+    out = np.empty(n, np.uint8)
+    lib().oracle_quantize_e4m3(_ptr(x), int(io_dtype), n, float(scale), _ptr(out))
+    return out
+
+
+def dequantize_e4m3(q: np.ndarray, scale: float, io_dtype: int) -> np.ndarray:
+    """io(f32(q) * scale) as raw bits (uint32 for F32, uint16 otherwise)."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    out = np.empty(q.size, np.uint32 if int(io_dtype) == 3 else np.uint16)
+    lib().oracle_dequantize_e4m3(_ptr(q), q.size, float(scale), int(io_dtype), _ptr(out))
+    return out

@@ -1,0 +1,91 @@
+/*
+ * CPU oracle for the KVX paged KV write / gather path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (libkvx_amd.so, the
+ * kvx_amd package) links, loads or calls this code; only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the
+ * checker and as the timed CPU baseline.
+ *
+ * The reference ships no CPU implementation of write/gather (kvx_abi.c only
+ * validates), so this is a restatement of the reference kernel semantics:
+ *   oracle_cache_offset  kernels/kvx_paged_kv.cu:54-75
+ *   oracle_write_kv      kernels/kvx_paged_kv.cu:93-124
+ *   oracle_gather_kv     kernels/kvx_paged_kv.cu:226-267
+ * plus the FP8 E4M3 cast this build adds (OCP FP8 definition).
+ */
+#ifndef KVX_ORACLE_H
+#define KVX_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Layout codes and dtype codes are the kvx_abi.h enum values. */
+
+int64_t oracle_cache_offset(int layout, const int64_t *stride, int64_t pack,
+                            int64_t block, int64_t offset, int64_t head,
+                            int64_t dim);
+
+/* Element-wise write.  io and cache dtypes are equal (bit copy) or the cache
+ * is F8_E4M3 and io is F16/BF16/F32 (quantize with k_scale / v_scale). */
+void oracle_write_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                     int v_layout, const int64_t *v_stride, int64_t v_pack,
+                     const void *key, const void *value, void *key_cache,
+                     void *value_cache, const void *slots, int slot_is64,
+                     int64_t num_tokens, int32_t heads, int32_t head_dim,
+                     int32_t block_size, int32_t num_blocks, int io_dtype,
+                     int cache_dtype, float k_scale, float v_scale);
+
+/* Element-wise gather into [seq_count, max_seq_len, H, D].  Rows not
+ * written by the reference semantics are left untouched.  Dequantizes when
+ * the cache is F8_E4M3 and io is F16/BF16/F32. */
+void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                      int v_layout, const int64_t *v_stride, int64_t v_pack,
+                      const void *key_cache, const void *value_cache,
+                      void *key_out, void *value_out, const void *block_table,
+                      const void *seq_lens, int index_is64, int32_t seq_count,
+                      int32_t max_blocks_per_seq, int32_t max_seq_len,
+                      int32_t heads, int32_t head_dim, int32_t block_size,
+                      int32_t num_blocks, int cache_dtype, int io_dtype,
+                      float k_scale, float v_scale);
+
+/* Same results as the element-wise functions for bit-copy calls, with one
+ * memcpy per contiguous run and OpenMP over tokens / (sequence, block); the
+ * timed CPU baseline.  Returns the number of OpenMP threads used. */
+int oracle_write_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                         int v_layout, const int64_t *v_stride, int64_t v_pack,
+                         const void *key, const void *value, void *key_cache,
+                         void *value_cache, const void *slots, int slot_is64,
+                         int64_t num_tokens, int32_t heads, int32_t head_dim,
+                         int32_t block_size, int32_t num_blocks, int elem_size);
+
+int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                          int v_layout, const int64_t *v_stride, int64_t v_pack,
+                          const void *key_cache, const void *value_cache,
+                          void *key_out, void *value_out,
+                          const void *block_table, const void *seq_lens,
+                          int index_is64, int32_t seq_count,
+                          int32_t max_blocks_per_seq, int32_t max_seq_len,
+                          int32_t heads, int32_t head_dim, int32_t block_size,
+                          int32_t num_blocks, int elem_size);
+
+/* Scalar casts (OCP E4M3, bf16, f16), by nearest-value search. */
+uint8_t oracle_f32_to_e4m3(float v);
+float oracle_e4m3_to_f32(uint8_t q);
+uint16_t oracle_f32_to_bf16(float v);
+uint16_t oracle_f32_to_f16(float v);
+float oracle_f16_to_f32(uint16_t h);
+
+/* Array versions for tests: out[i] = cast(in[i] / scale) etc. */
+void oracle_quantize_e4m3(const void *in, int io_dtype, int64_t n, float scale,
+                          uint8_t *out);
+void oracle_dequantize_e4m3(const uint8_t *in, int64_t n, float scale,
+                            int io_dtype, void *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVX_ORACLE_H */

@@ -1,0 +1,114 @@
+"""Helpers shared by the GPU parity tests: device buffers for a paged cache
+(optionally padded, i.e. with non-canonical strides), and the calls that run
+the same write / gather through libkvx_amd.so and through the CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+from kvx_amd import paged
+from kvx_amd.abi import DType, Layout, Status
+
+TORCH_DT = {DType.F32: torch.float32, DType.F16: torch.float16,
+            DType.BF16: torch.bfloat16, DType.F8_E4M3: torch.float8_e4m3fn}
+
+
+def np_bytes(t: torch.Tensor) -> np.ndarray:
+    """Host copy of a tensor's bytes (the tensor must be contiguous)."""
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy().reshape(-1).copy()
+
+
+def random_fill(t: torch.Tensor, gen: torch.Generator) -> torch.Tensor:
+    """Fill any tensor with random bytes (NaN/Inf patterns included)."""
+    b = t.view(torch.uint8)
+    b.copy_(torch.randint(0, 256, b.shape, dtype=torch.uint8, generator=gen,
+                          device="cpu").to(b.device))
+    return t
+
+
+class CacheBuf:
+    """A K or V cache tensor: `base` owns the storage, `view` is the shaped
+    (possibly padded) tensor handed to the library."""
+
+    def __init__(self, layout, dtype, nb, bs, H, D, pack, device, gen, pad_axis=None,
+                 pad=3):
+        self.layout = Layout(layout)
+        self.pack = pack
+        shape = paged.cache_shape(layout, nb, bs, H, D, pack)
+        big = list(shape)
+        if pad_axis is not None:
+            big[pad_axis] += pad
+        self.base = torch.empty(big, dtype=TORCH_DT[dtype], device=device)
+        random_fill(self.base, gen)
+        self.view = self.base[tuple(slice(0, n) for n in shape)]
+
+    def geometry(self) -> oracle.Geometry:
+        return oracle.Geometry(self.layout, self.view.stride(),
+                               self.pack if self.layout == Layout.BLOCK_HND_PACKED else 1)
+
+
+def make_cache(k_layout, v_layout, dtype, nb, bs, H, D, pack=8, device="cuda",
+               gen=None, k_pad=None, v_pad=None):
+    gen = gen or torch.Generator().manual_seed(0)
+    k = CacheBuf(k_layout, dtype, nb, bs, H, D, pack, device, gen, k_pad)
+    v = CacheBuf(v_layout, dtype, nb, bs, H, D, pack, device, gen, v_pad)
+    pc = paged.PagedCache(k.view, v.view, k.layout, v.layout, nb, bs, H, D)
+    return pc, k, v
+
+
+def check_write(pc, kbuf, vbuf, key, value, slots, *, io_dtype, cache_dtype,
+                tokens_per_seq=None, k_scale=None, v_scale=None, entry="launch",
+                stream=None):
+    """Run the write on the GPU and in the oracle from identical inputs and
+    require bit-identical caches (touched and untouched bytes alike)."""
+    kb0, vb0 = np_bytes(kbuf.base), np_bytes(vbuf.base)
+    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
+                                                   device=key.device)
+    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
+                                                   device=key.device)
+    st = paged.write_kv(pc, key, value, slots, tokens_per_seq=tokens_per_seq,
+                        k_scale=ks, v_scale=vs, entry=entry, stream=stream)
+    assert st == Status.OK, st
+    torch.cuda.synchronize()
+    oracle.write_kv(kbuf.geometry(), vbuf.geometry(), np_bytes(key), np_bytes(value),
+                    kb0, vb0, slots.cpu().numpy(), heads=pc.heads, head_dim=pc.head_dim,
+                    block_size=pc.block_size, num_blocks=pc.num_blocks,
+                    io_dtype=io_dtype, cache_dtype=cache_dtype,
+                    k_scale=1.0 if k_scale is None else k_scale,
+                    v_scale=1.0 if v_scale is None else v_scale)
+    got_k, got_v = np_bytes(kbuf.base), np_bytes(vbuf.base)
+    assert np.array_equal(got_k, kb0), _first_diff(got_k, kb0)
+    assert np.array_equal(got_v, vb0), _first_diff(got_v, vb0)
+
+
+def check_gather(pc, kbuf, vbuf, key_out, value_out, table, lens, max_seq_len, *,
+                 cache_dtype, io_dtype, k_scale=None, v_scale=None, entry="launch",
+                 stream=None):
+    """Run the gather on the GPU and in the oracle from identical inputs (the
+    outputs pre-filled with random bytes) and require bit-identical outputs."""
+    ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
+    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
+                                                   device=key_out.device)
+    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
+                                                   device=key_out.device)
+    st = paged.gather_kv(pc, key_out, value_out, table, lens, max_seq_len, k_scale=ks,
+                         v_scale=vs, entry=entry, stream=stream)
+    assert st == Status.OK, st
+    torch.cuda.synchronize()
+    S, mbps = table.shape
+    oracle.gather_kv(kbuf.geometry(), vbuf.geometry(), np_bytes(kbuf.base),
+                     np_bytes(vbuf.base), ko0, vo0, table.cpu().numpy(), lens.cpu().numpy(),
+                     seq_count=S, max_blocks_per_seq=mbps, max_seq_len=max_seq_len,
+                     heads=pc.heads, head_dim=pc.head_dim, block_size=pc.block_size,
+                     num_blocks=pc.num_blocks, cache_dtype=cache_dtype, io_dtype=io_dtype,
+                     k_scale=1.0 if k_scale is None else k_scale,
+                     v_scale=1.0 if v_scale is None else v_scale)
+    got_k, got_v = np_bytes(key_out), np_bytes(value_out)
+    assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
+    assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)
+
+
+def _first_diff(a: np.ndarray, b: np.ndarray) -> str:
+    idx = np.flatnonzero(a != b)
+    return f"{idx.size} bytes differ, first at {idx[:8].tolist()}"

@@ -1,0 +1,297 @@
+"""Status codes of the kvx_paged_kv.h / kvx_ext.h launch path (CPU only).
+
+The reference launchers (kernels/kvx_paged_kv.cu) need nvcc and cannot be
+built here, so each case below is one injected fault (or a pair, to pin the
+check order) with the code the cited reference line returns.  Every case
+returns before a kernel would be enqueued (a validation error, or an empty
+batch, which the reference returns OK for without launching), so no GPU is
+touched.
+"""
+import ctypes as C
+
+import pytest
+
+from kvx_amd import abi
+from kvx_amd.abi import DType, Layout, Memory, ScaleGranularity, Status, TableFormat
+
+D_ = Memory.DEVICE
+FAKE = 0x20000  # never dereferenced: every case returns before a launch
+
+INV, UNS, OK = Status.INVALID_ARGUMENT, Status.UNSUPPORTED, Status.OK
+
+
+def base_write(dt=DType.BF16, io_dt=None, T=4, layout=Layout.BLOCK_NHD, v_layout=None,
+               slot_dt=DType.S64, H=2, D=8, nb=4, bs=4, pack=4):
+    io_dt = dt if io_dt is None else io_dt
+    cache = abi.make_cache(layout, dt, D_, nb, bs, H, D, FAKE, FAKE, pack=pack,
+                           v_layout=v_layout)
+    w = abi.make_write(T, H, D, io_dt, D_, FAKE, FAKE, slot_dt, FAKE)
+    return cache, w
+
+
+def base_gather(dt=DType.BF16, io_dt=None, S=2, L=8, H=2, D=8, nb=4, bs=4,
+                idx=DType.S32, lens=DType.S32, layout=Layout.BLOCK_NHD):
+    io_dt = dt if io_dt is None else io_dt
+    cache = abi.make_cache(layout, dt, D_, nb, bs, H, D, FAKE, FAKE)
+    tb = abi.make_block_table_packed(S, 2, idx, FAKE)
+    sl = abi.make_seq_lens(S, lens, FAKE)
+    g = abi.make_gather(S, L, H, D, io_dt, D_, FAKE, FAKE, tb, sl)
+    return cache, g
+
+
+def W(lib, cache, w, fn="kvx_launch_write_kv"):
+    return Status(getattr(lib, fn)(abi.ref(cache), abi.ref(w), None))
+
+
+def WP(lib, cache, w, tps, fn="kvx_launch_write_kv_prefill"):
+    return Status(getattr(lib, fn)(abi.ref(cache), abi.ref(w), tps, None))
+
+
+def G(lib, cache, g, fn="kvx_launch_gather_kv"):
+    return Status(getattr(lib, fn)(abi.ref(cache), abi.ref(g), None))
+
+
+# ---------------------------------------------------------------------------
+# write: kvx_paged_kv.cu:315-451 (per dtype), :472-491 (dispatch)
+
+def test_write_dispatch(kvx_lib):
+    c, w = base_write()
+    assert W(kvx_lib, None, w) == INV                       # :475
+    assert W(kvx_lib, c, None) == INV
+    c.v.dtype = DType.F16
+    assert W(kvx_lib, c, w) == INV                          # :478 k != v dtype
+    for dt in (DType.U8, DType.S32, DType.F8_E5M2, DType.INVALID):
+        c, w = base_write()
+        c.k.dtype = c.v.dtype = dt
+        assert W(kvx_lib, c, w) == UNS, dt                  # :488
+
+
+@pytest.mark.parametrize("fn", ["kvx_launch_write_kv", "kvx_launch_write_kv_bf16"])
+def test_write_single_faults(kvx_lib, fn):
+    cases = []
+
+    def case(expect, mutate, **kw):
+        c, w = base_write(**kw)
+        mutate(c, w)
+        cases.append((expect, c, w))
+
+    case(INV, lambda c, w: setattr(w, "size", C.sizeof(w) - 1))             # :323
+    case(INV, lambda c, w: setattr(w.io, "size", 8))                        # :326
+    case(INV, lambda c, w: setattr(w.slots, "size", 0))                     # :329
+    case(UNS, lambda c, w: (setattr(w.io.key, "dtype", DType.F16)))         # :335
+    case(UNS, lambda c, w: (setattr(w.io.value, "dtype", DType.F32)))       # :336
+    case(INV, lambda c, w: setattr(w.io, "num_kv_heads", 3))                # :339
+    case(INV, lambda c, w: setattr(w.io, "head_dim", 16))                   # :340
+    case(INV, lambda c, w: setattr(w.io.key, "ndim", 4))                    # :276
+    case(INV, lambda c, w: w.io.key.shape.__setitem__(0, 5))                # :279
+    case(UNS, lambda c, w: w.io.key.stride.__setitem__(0, 17))              # :283
+    case(UNS, lambda c, w: w.io.value.stride.__setitem__(2, 2))             # :350
+    case(INV, lambda c, w: setattr(w.slots, "token_count", 3))              # :357
+    case(UNS, lambda c, w: setattr(c.k, "layout", Layout.BLOCK_CUSTOM))     # :49
+    case(UNS, lambda c, w: setattr(c.v, "layout", Layout.INVALID))          # :367
+    case(INV, lambda c, w: (setattr(c.k, "layout", Layout.BLOCK_HND_PACKED),
+                            c.k.shape.__setitem__(4, 0)))                   # :40
+    case(INV, lambda c, w: (setattr(c.k, "layout", Layout.BLOCK_HND_PACKED),
+                            c.k.shape.__setitem__(4, 3)))                   # :43
+    case(INV, lambda c, w: setattr(w.slots, "dtype", DType.U32))            # :443
+    case(INV, lambda c, w: setattr(w.slots, "dtype", DType.S32 - 6))        # :443
+    for expect, c, w in cases:
+        assert W(kvx_lib, c, w, fn) == expect
+
+
+def test_write_check_order(kvx_lib):
+    # size checks come before dtype checks (:323 before :332)
+    c, w = base_write()
+    w.size = 0
+    c.k.dtype = c.v.dtype = DType.F32
+    assert W(kvx_lib, c, w, "kvx_launch_write_kv_bf16") == INV
+    # io dtype (UNSUPPORTED) before the head check (INVALID): :335 before :339
+    c, w = base_write()
+    w.io.key.dtype = DType.F32
+    w.io.num_kv_heads = 7
+    assert W(kvx_lib, c, w) == UNS
+    # key io tensor before value io tensor: INVALID shape beats UNSUPPORTED stride
+    c, w = base_write()
+    w.io.key.ndim = 2
+    w.io.value.stride[0] = 99
+    assert W(kvx_lib, c, w) == INV
+    # params (UNSUPPORTED layout) before the slot dtype (INVALID): :363 before :443
+    c, w = base_write()
+    c.k.layout = Layout.BLOCK_CUSTOM
+    w.slots.dtype = DType.U64
+    assert W(kvx_lib, c, w) == UNS
+
+
+def test_write_empty_batch_is_ok_without_launch(kvx_lib):
+    # total == 0 returns OK before the slot-dtype check (:374 before :398)
+    c, w = base_write(T=0)
+    w.slots.dtype = DType.U32
+    assert W(kvx_lib, c, w) == OK
+    # mixed K/V layouts and non-canonical cache strides pass launch validation
+    c, w = base_write(T=0, layout=Layout.BLOCK_HND_PACKED, v_layout=Layout.BLOCK_NHD)
+    c.v.stride[0] += 64
+    assert W(kvx_lib, c, w) == OK
+    # ... while the strict ABI entry point rejects the mixed layouts
+    c.k.memory = c.v.memory = Memory.HOST
+    w.io.key.memory = w.io.value.memory = Memory.HOST
+    assert Status(kvx_lib.kvx_write_kv(abi.ref(c), abi.ref(w), None)) == INV
+
+
+def test_prefill_validation(kvx_lib):
+    c, w = base_write()
+    assert WP(kvx_lib, c, w, 0) == INV                       # :500
+    assert WP(kvx_lib, c, w, -3) == INV
+    # reference test run_write_prefill_invalid (kvx_kernel_test.cu:607-618)
+    c0, w0 = abi.CacheDesc(), abi.WriteDesc()
+    c0.k.dtype = c0.v.dtype = DType.F16
+    assert WP(kvx_lib, c0, w0, 0) == INV
+    # num_tokens % tps checked after sizes and before dtypes (:512)
+    c, w = base_write(T=6)
+    c.k.dtype = c.v.dtype = DType.F32
+    assert WP(kvx_lib, c, w, 4, "kvx_launch_write_kv_prefill_bf16") == INV
+    c, w = base_write(T=6)
+    w.size = 1
+    assert WP(kvx_lib, c, w, 4) == INV
+    c, w = base_write(T=0)
+    assert WP(kvx_lib, c, w, 4) == OK
+    c, w = base_write(T=8)
+    w.io.key.dtype = DType.F16
+    assert WP(kvx_lib, c, w, 4) == UNS
+
+
+def test_write_safety_checks_added_by_this_build(kvx_lib):
+    """Inputs the reference would launch on and then divide by zero or fault."""
+    c, w = base_write()
+    c.block_size = 0
+    assert W(kvx_lib, c, w) == INV
+    for field in ("key", "value"):
+        c, w = base_write()
+        getattr(w.io, field).data = None
+        assert W(kvx_lib, c, w) == INV
+    c, w = base_write()
+    w.slots.slots = None
+    assert W(kvx_lib, c, w) == INV
+    c, w = base_write()
+    c.k.data = None
+    assert W(kvx_lib, c, w) == INV
+
+
+def test_fp8_write_validation(kvx_lib):
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    assert W(kvx_lib, c, w) == INV                           # no scale at all
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    w.k_scale_desc = abi.scale_desc(FAKE, dtype=DType.F16)
+    w.v_scale = FAKE
+    assert W(kvx_lib, c, w) == UNS
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    w.k_scale_desc = abi.scale_desc(FAKE, granularity=ScaleGranularity.PER_HEAD)
+    w.v_scale = FAKE
+    assert W(kvx_lib, c, w) == UNS
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    w.k_scale = FAKE
+    w.v_scale_desc = abi.scale_desc(FAKE)
+    w.v_scale_desc.size = 8
+    assert W(kvx_lib, c, w) == INV
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.U8)
+    assert W(kvx_lib, c, w) == UNS
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    w.io.value.dtype = DType.F16
+    assert W(kvx_lib, c, w) == UNS
+    # per-dtype helpers never take an FP8 cache
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    assert W(kvx_lib, c, w, "kvx_launch_write_kv_bf16") == UNS
+    # empty FP8 batch with valid scales
+    c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16, T=0)
+    w.k_scale = w.v_scale = FAKE
+    assert W(kvx_lib, c, w) == OK
+
+
+# ---------------------------------------------------------------------------
+# gather: kvx_paged_kv.cu:763-870 (per dtype), :891-910 (dispatch)
+
+def test_gather_single_faults(kvx_lib):
+    cases = []
+
+    def case(expect, mutate, **kw):
+        c, g = base_gather(**kw)
+        mutate(c, g)
+        cases.append((expect, c, g))
+
+    case(INV, lambda c, g: setattr(g, "size", 4))                             # :771
+    case(INV, lambda c, g: setattr(g.io, "size", 4))                          # :774
+    case(INV, lambda c, g: setattr(g.block_table, "size", 4))                 # :777
+    case(INV, lambda c, g: setattr(g.seq_lens, "size", 4))                    # :778
+    case(UNS, lambda c, g: setattr(g.io.key, "dtype", DType.F32))             # :784
+    case(UNS, lambda c, g: setattr(g.block_table, "format", TableFormat.RAGGED))  # :788
+    case(UNS, lambda c, g: setattr(g.block_table, "format", TableFormat.KV_OFFSETS))
+    case(INV, lambda c, g: setattr(g.io, "num_kv_heads", 1))                  # :791
+    case(INV, lambda c, g: setattr(g.seq_lens, "seq_count", 1))               # :795
+    case(INV, lambda c, g: g.io.key.shape.__setitem__(1, 7))                  # :302
+    case(UNS, lambda c, g: g.io.value.stride.__setitem__(1, 3))               # :306
+    case(UNS, lambda c, g: setattr(c.k, "layout", Layout.BLOCK_CUSTOM))       # :816
+    case(INV, lambda c, g: setattr(g.block_table, "index_dtype", DType.S64))  # :861
+    case(INV, lambda c, g: setattr(g.seq_lens, "dtype", DType.U32))           # :861
+    for expect, c, g in cases:
+        assert G(kvx_lib, c, g) == expect
+    c, g = base_gather()
+    assert G(kvx_lib, None, g) == INV
+    c.v.dtype = DType.F16
+    assert G(kvx_lib, c, g) == INV                                            # :897
+    c, g = base_gather()
+    c.k.dtype = c.v.dtype = DType.F8_E5M2
+    assert G(kvx_lib, c, g) == UNS                                            # :907
+    c, g = base_gather()
+    assert G(kvx_lib, c, g, "kvx_launch_gather_kv_f16") == UNS               # :781
+
+
+def test_gather_check_order_and_empty(kvx_lib):
+    # format (UNSUPPORTED) before heads (INVALID): :788 before :791
+    c, g = base_gather()
+    g.block_table.format = TableFormat.RAGGED
+    g.io.num_kv_heads = 5
+    assert G(kvx_lib, c, g) == UNS
+    # total == 0 (max_seq_len 0) is OK before the index dtype check
+    c, g = base_gather(L=0)
+    g.block_table.index_dtype = DType.U64
+    assert G(kvx_lib, c, g) == OK
+    # block_table.indices_count is not checked on the launch path
+    c, g = base_gather(L=0)
+    g.block_table.indices_count = 12345
+    assert G(kvx_lib, c, g) == OK
+
+
+def test_dequant_gather_validation(kvx_lib):
+    f = kvx_lib.kvx_launch_gather_kv_dequant
+    ks = abi.scale_desc(FAKE)
+    vs = abi.scale_desc(FAKE)
+
+    def call(c, g, k=ks, v=vs):
+        return Status(f(abi.ref(c), abi.ref(g), abi.ref(k), abi.ref(v), None))
+
+    c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.BF16, L=0)
+    assert call(c, g) == OK
+    assert call(c, g, k=None) == INV
+    c, g = base_gather(dt=DType.BF16)
+    assert call(c, g) == UNS
+    c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.F8_E4M3)
+    assert call(c, g) == UNS
+    c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    bad = abi.scale_desc(FAKE, granularity=ScaleGranularity.PER_BLOCK)
+    assert call(c, g, v=bad) == UNS
+    bad = abi.scale_desc(None)
+    assert call(c, g, k=bad) == INV
+    c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.BF16)
+    g.block_table.format = TableFormat.RAGGED
+    assert call(c, g) == UNS
+
+
+def test_gather_safety_checks_added_by_this_build(kvx_lib):
+    c, g = base_gather()
+    c.block_size = 0
+    assert G(kvx_lib, c, g) == INV
+    c, g = base_gather()
+    g.seq_lens.lengths = None
+    assert G(kvx_lib, c, g) == INV
+    c, g = base_gather()
+    g.io.value.data = None
+    assert G(kvx_lib, c, g) == INV
