@@ -57,8 +57,23 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU baseline sampling budget")
     p.add_argument("--profile-only", action="store_true",
-                   help="skip the CPU baseline and print a shorter line (profiler runs)")
+                   help="skip the CPU baseline (profiler runs)")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="only run three plain 1 GiB device copies: the known-size "
+                        "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return p.parse_args()
+
+
+def copy_probe() -> None:
+    import torch
+
+    a = torch.ones(1024**3 // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print("copy probe: 3 x 1 GiB device copies", flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -287,6 +302,10 @@ def main():
               "(the paged write/gather shards by KV head or by sequence with no "
               "exchange; see DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe:
+        copy_probe()
+        return
 
     import torch
 

@@ -29,8 +29,21 @@ constexpr int kWavesPerBlock = kBlockThreads / kWave;
 // Chunk offsets each lane keeps in registers; rows with more chunks per lane
 // compute the rest on the fly.
 constexpr int kMaxChunksPerLane = 4;
-// Chunks per lane in flight in the flat (contiguous block) gather loop.
-constexpr int kFlatUnroll = 4;
+// Compile-time tuning knobs of the contiguous-block gather (defaults are the
+// measured best on MI355X): chunks per lane in flight, and non-temporal
+// (streaming) loads of the cache / stores of the output.
+#ifndef KVX_FLAT_UNROLL
+#define KVX_FLAT_UNROLL 8
+#endif
+#ifndef KVX_GATHER_NT_LOAD
+#define KVX_GATHER_NT_LOAD 1
+#endif
+#ifndef KVX_GATHER_NT_STORE
+#define KVX_GATHER_NT_STORE 1
+#endif
+constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
+constexpr bool kGatherNtLoad = KVX_GATHER_NT_LOAD != 0;
+constexpr bool kGatherNtStore = KVX_GATHER_NT_STORE != 0;
 
 // Cache geometry with strides pre-multiplied by the cache element size.
 struct GeomBytes {
@@ -46,62 +59,105 @@ struct GeomBytes {
 // ---------------------------------------------------------------------------
 // Raw storage of one chunk.
 
+// A chunk lives in 32-bit registers: B bytes in B/4 words (B < 4: the low
+// bits of one word).  Elements are read and written with shifts, never
+// through byte arrays, so a 16-byte chunk stays four VGPRs.
 template <int B>
-struct alignas(B < 16 ? B : 16) Raw {
-  uint8_t u8[B];
+struct Raw {
+  static constexpr int kWords = B >= 4 ? B / 4 : 1;
+  uint32_t w[kWords];
 };
 
 // Load/store one chunk with the widest naturally aligned access: B = 16 is
-// one global_load_dwordx4 / global_store_dwordx4 per lane.
-template <int B>
+// one global_load_dwordx4 / global_store_dwordx4 per lane.  NT selects the
+// non-temporal (streaming) form.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename V, bool NT>
+__device__ __forceinline__ V ld_one(const char *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const V *>(p));
+  return *reinterpret_cast<const V *>(p);
+}
+
+template <typename V, bool NT>
+__device__ __forceinline__ void st_one(char *p, V v) {
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, reinterpret_cast<V *>(p));
+  } else {
+    *reinterpret_cast<V *>(p) = v;
+  }
+}
+
+template <int B, bool NT = false>
 __device__ __forceinline__ Raw<B> ld(const char *p) {
   Raw<B> r;
   if constexpr (B == 1) {
-    r.u8[0] = *reinterpret_cast<const uint8_t *>(p);
+    r.w[0] = ld_one<uint8_t, NT>(p);
   } else if constexpr (B == 2) {
-    const uint16_t v = *reinterpret_cast<const uint16_t *>(p);
-    __builtin_memcpy(r.u8, &v, 2);
+    r.w[0] = ld_one<uint16_t, NT>(p);
   } else if constexpr (B == 4) {
-    const uint32_t v = *reinterpret_cast<const uint32_t *>(p);
-    __builtin_memcpy(r.u8, &v, 4);
+    r.w[0] = ld_one<uint32_t, NT>(p);
   } else if constexpr (B == 8) {
-    const uint2 v = *reinterpret_cast<const uint2 *>(p);
-    __builtin_memcpy(r.u8, &v, 8);
+    const u32x2 v = ld_one<u32x2, NT>(p);
+    r.w[0] = v[0];
+    r.w[1] = v[1];
   } else {
     static_assert(B % 16 == 0, "chunk bytes");
 #pragma unroll
     for (int i = 0; i < B / 16; ++i) {
-      const uint4 v = reinterpret_cast<const uint4 *>(p)[i];
-      __builtin_memcpy(r.u8 + 16 * i, &v, 16);
+      const u32x4 v = ld_one<u32x4, NT>(p + 16 * i);
+      r.w[4 * i + 0] = v[0];
+      r.w[4 * i + 1] = v[1];
+      r.w[4 * i + 2] = v[2];
+      r.w[4 * i + 3] = v[3];
     }
   }
   return r;
 }
 
-template <int B>
+template <int B, bool NT = false>
 __device__ __forceinline__ void st(char *p, const Raw<B> &r) {
   if constexpr (B == 1) {
-    *reinterpret_cast<uint8_t *>(p) = r.u8[0];
+    st_one<uint8_t, NT>(p, (uint8_t)r.w[0]);
   } else if constexpr (B == 2) {
-    uint16_t v;
-    __builtin_memcpy(&v, r.u8, 2);
-    *reinterpret_cast<uint16_t *>(p) = v;
+    st_one<uint16_t, NT>(p, (uint16_t)r.w[0]);
   } else if constexpr (B == 4) {
-    uint32_t v;
-    __builtin_memcpy(&v, r.u8, 4);
-    *reinterpret_cast<uint32_t *>(p) = v;
+    st_one<uint32_t, NT>(p, r.w[0]);
   } else if constexpr (B == 8) {
-    uint2 v;
-    __builtin_memcpy(&v, r.u8, 8);
-    *reinterpret_cast<uint2 *>(p) = v;
+    u32x2 v;
+    v[0] = r.w[0];
+    v[1] = r.w[1];
+    st_one<u32x2, NT>(p, v);
   } else {
 #pragma unroll
     for (int i = 0; i < B / 16; ++i) {
-      uint4 v;
-      __builtin_memcpy(&v, r.u8 + 16 * i, 16);
-      reinterpret_cast<uint4 *>(p)[i] = v;
+      u32x4 v;
+      v[0] = r.w[4 * i + 0];
+      v[1] = r.w[4 * i + 1];
+      v[2] = r.w[4 * i + 2];
+      v[3] = r.w[4 * i + 3];
+      st_one<u32x4, NT>(p + 16 * i, v);
     }
   }
+}
+
+// Element i of a chunk (i is a compile-time constant after unrolling).
+template <int B>
+__device__ __forceinline__ uint32_t get8(const Raw<B> &r, int i) {
+  return (r.w[i >> 2] >> ((i & 3) * 8)) & 0xFFu;
+}
+template <int B>
+__device__ __forceinline__ uint32_t get16(const Raw<B> &r, int i) {
+  return (r.w[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu;
+}
+template <int B>
+__device__ __forceinline__ void put8(Raw<B> &r, int i, uint32_t v) {
+  r.w[i >> 2] |= v << ((i & 3) * 8);
+}
+template <int B>
+__device__ __forceinline__ void put16(Raw<B> &r, int i, uint32_t v) {
+  r.w[i >> 1] |= v << ((i & 1) * 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -132,29 +188,25 @@ struct IoType<KVX_DTYPE_BF16> {
   static constexpr int kBytes = 2;
 };
 
-template <int IO>
-__device__ __forceinline__ float io_to_f32(const uint8_t *bytes, int i) {
+template <int IO, int B>
+__device__ __forceinline__ float io_to_f32(const Raw<B> &x, int i) {
   if constexpr (IO == KVX_DTYPE_F32) {
-    uint32_t u;
-    __builtin_memcpy(&u, bytes + 4 * i, 4);
-    return bits_f32(u);
+    return bits_f32(x.w[i]);
+  } else if constexpr (IO == KVX_DTYPE_BF16) {
+    return bf16_to_f32((uint16_t)get16(x, i));
   } else {
-    uint16_t h;
-    __builtin_memcpy(&h, bytes + 2 * i, 2);
-    if constexpr (IO == KVX_DTYPE_BF16) return bf16_to_f32(h);
-    return f16_to_f32(h);
+    return f16_to_f32((uint16_t)get16(x, i));
   }
 }
 
-template <int IO>
-__device__ __forceinline__ void f32_to_io(float v, uint8_t *bytes, int i) {
+template <int IO, int B>
+__device__ __forceinline__ void f32_to_io(float v, Raw<B> &y, int i) {
   if constexpr (IO == KVX_DTYPE_F32) {
-    const uint32_t u = f32_bits(canon_nan_f32(v));
-    __builtin_memcpy(bytes + 4 * i, &u, 4);
+    y.w[i] = f32_bits(canon_nan_f32(v));
+  } else if constexpr (IO == KVX_DTYPE_BF16) {
+    put16(y, i, f32_to_bf16(v));
   } else {
-    const uint16_t h =
-        (IO == KVX_DTYPE_BF16) ? f32_to_bf16(v) : f32_to_f16(v);
-    __builtin_memcpy(bytes + 2 * i, &h, 2);
+    put16(y, i, f32_to_f16(v));
   }
 }
 
@@ -168,8 +220,10 @@ struct QuantOp {
                                                     float scale) {
     Raw<kDst> y;
 #pragma unroll
+    for (int k = 0; k < Raw<kDst>::kWords; ++k) y.w[k] = 0;
+#pragma unroll
     for (int i = 0; i < G; ++i) {
-      y.u8[i] = f32_to_e4m3(io_to_f32<IO>(x.u8, i) / scale);
+      put8(y, i, f32_to_e4m3(io_to_f32<IO>(x, i) / scale));
     }
     return y;
   }
@@ -186,8 +240,10 @@ struct DequantOp {
                                                     float scale) {
     Raw<kDst> y;
 #pragma unroll
+    for (int k = 0; k < Raw<kDst>::kWords; ++k) y.w[k] = 0;
+#pragma unroll
     for (int i = 0; i < G; ++i) {
-      f32_to_io<IO>(e4m3_to_f32(x.u8[i]) * scale, y.u8, i);
+      f32_to_io<IO>(e4m3_to_f32((uint8_t)get8(x, i)) * scale, y, i);
     }
     return y;
   }
@@ -295,6 +351,22 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
     int64_t mine = -1;
     const int64_t tl = g * tpw + lane;
     if (lane < tpw && tl < a.num_tokens) mine = load_index(a.slots, tl, a.slot_is64);
+    // The token rows do not depend on the slot: issue their loads before
+    // waiting for it, so the slot and row latencies overlap.
+    const char *sk = a.src_k + t * a.row_bytes;
+    const char *sv = a.src_v + t * a.row_bytes;
+    Raw<Op::kSrc> xk[kMaxChunksPerLane];
+    Raw<Op::kSrc> xv[kMaxChunksPerLane];
+    if (t < a.num_tokens) {
+#pragma unroll
+      for (int k = 0; k < kMaxChunksPerLane; ++k) {
+        const int c = l + k * lpt;
+        if (c < a.nchunks) {
+          xk[k] = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
+          xv[k] = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
+        }
+      }
+    }
     int64_t slot;
     if (tpw == 1) {
       slot = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(
@@ -310,22 +382,8 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
     int64_t b, o;
     split_slot(slot, a.block_size, b, o);
     if (b >= a.num_blocks) continue;
-
-    const char *sk = a.src_k + t * a.row_bytes;
-    const char *sv = a.src_v + t * a.row_bytes;
     char *dk = a.dst_k + b * a.gk.s_block + o * a.gk.s_off;
     char *dv = a.dst_v + b * a.gv.s_block + o * a.gv.s_off;
-
-    Raw<Op::kSrc> xk[kMaxChunksPerLane];
-    Raw<Op::kSrc> xv[kMaxChunksPerLane];
-#pragma unroll
-    for (int k = 0; k < kMaxChunksPerLane; ++k) {
-      const int c = l + k * lpt;
-      if (c < a.nchunks) {
-        xk[k] = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
-        xv[k] = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
-      }
-    }
 #pragma unroll
     for (int k = 0; k < kMaxChunksPerLane; ++k) {
       const int c = l + k * lpt;
@@ -347,14 +405,168 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Block write (prefill into a layout that is not row-major in the block).
+//
+// When the `bs` consecutive tokens of a group fill one cache block in order
+// (slot = b * bs + o for o = 0..bs-1, the usual prefill pattern), the
+// group's source rows are one contiguous io region and each cache tensor's
+// destination is one contiguous block region, only permuted: a dense block
+// stores chunks in (run, offset, chunk-in-run) order,
+//   unit u = (a * bs + o) * Bc + w,   row chunk c = a * Bc + w,
+// where Bc is the chunks per contiguous per-token run: the whole row for
+// NHD, head_dim / G for HND, pack / G for HND_PACKED.  A row-dense tensor
+// (Bc = row chunks) is copied straight through; any other is staged in LDS
+// (rows padded by one chunk so the strided LDS reads are bank-conflict
+// free) so that both the HBM reads and the HBM writes are fully coalesced.
+// Groups that do not fill a block take the per-token path.
+
+struct BlockWriteArgs {
+  int32_t bs_log2;
+  int32_t nchunks_log2;  // row chunks
+  int32_t k_bc_log2;     // K chunks per contiguous per-token run
+  int32_t v_bc_log2;
+  int32_t pitch;         // LDS row pitch in chunks (row chunks + 1)
+  int32_t pad_;
+};
+
+constexpr int kBlockUnroll = 4;
+
+// One tensor of a full block: src = the group's io rows, dst = the block.
+template <class Op>
+__device__ __forceinline__ void write_dense_block(const char *src, char *dst,
+                                                  int bc_log2,
+                                                  const BlockWriteArgs &bw,
+                                                  float scale, char *lds) {
+  const int n_log2 = bw.nchunks_log2;
+  const int total = 1 << (bw.bs_log2 + n_log2);
+  const int tid = (int)threadIdx.x;
+  if (bc_log2 == n_log2) {  // row-dense: destination order == source order
+    int f = tid;
+    for (; f + (kBlockUnroll - 1) * kBlockThreads < total;
+         f += kBlockUnroll * kBlockThreads) {
+      Raw<Op::kSrc> x[kBlockUnroll];
+#pragma unroll
+      for (int u = 0; u < kBlockUnroll; ++u)
+        x[u] = ld<Op::kSrc>(src + (int64_t)(f + u * kBlockThreads) * Op::kSrc);
+#pragma unroll
+      for (int u = 0; u < kBlockUnroll; ++u)
+        st<Op::kDst>(dst + (int64_t)(f + u * kBlockThreads) * Op::kDst,
+                     Op::apply(x[u], scale));
+    }
+    for (; f < total; f += kBlockThreads)
+      st<Op::kDst>(dst + (int64_t)f * Op::kDst,
+                   Op::apply(ld<Op::kSrc>(src + (int64_t)f * Op::kSrc), scale));
+    return;
+  }
+  // Stage the rows in LDS: chunk c of row o at lds[o * pitch + c].
+  const int nmask = (1 << n_log2) - 1;
+  int f = tid;
+  for (; f + (kBlockUnroll - 1) * kBlockThreads < total;
+       f += kBlockUnroll * kBlockThreads) {
+    Raw<Op::kSrc> x[kBlockUnroll];
+#pragma unroll
+    for (int u = 0; u < kBlockUnroll; ++u)
+      x[u] = ld<Op::kSrc>(src + (int64_t)(f + u * kBlockThreads) * Op::kSrc);
+#pragma unroll
+    for (int u = 0; u < kBlockUnroll; ++u) {
+      const int g = f + u * kBlockThreads;
+      st<Op::kSrc>(lds + ((g >> n_log2) * bw.pitch + (g & nmask)) * Op::kSrc, x[u]);
+    }
+  }
+  for (; f < total; f += kBlockThreads)
+    st<Op::kSrc>(lds + ((f >> n_log2) * bw.pitch + (f & nmask)) * Op::kSrc,
+                 ld<Op::kSrc>(src + (int64_t)f * Op::kSrc));
+  __syncthreads();
+  const int bcmask = (1 << bc_log2) - 1;
+  const int bsmask = (1 << bw.bs_log2) - 1;
+  for (int u = tid; u < total; u += kBlockThreads) {
+    const int w = u & bcmask;
+    const int q = u >> bc_log2;
+    const int o = q & bsmask;
+    const int c = ((q >> bw.bs_log2) << bc_log2) + w;
+    st<Op::kDst>(dst + (int64_t)u * Op::kDst,
+                 Op::apply(ld<Op::kSrc>(lds + (o * bw.pitch + c) * Op::kSrc), scale));
+  }
+  __syncthreads();  // the LDS tile is reused by the next tensor
+}
+
+template <class Op>
+__global__ __launch_bounds__(kBlockThreads) void write_blocks_kernel(WriteArgs a,
+                                                                     BlockWriteArgs bw) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ int64_t s_block;
+  __shared__ int32_t s_full;
+  const int bs = 1 << bw.bs_log2;
+  const int64_t t0 = (int64_t)blockIdx.x << bw.bs_log2;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & (kWave - 1);
+
+  float ks = 1.0f;
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = *a.k_scale;
+    vs = *a.v_scale;
+  }
+
+  if (tid < kWave) {  // wave 0 checks that the group fills one block in order
+    const int64_t t = t0 + lane;
+    int64_t slot = -1;
+    if (lane < bs && t < a.num_tokens) slot = load_index(a.slots, t, a.slot_is64);
+    const int64_t first =
+        (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32))
+                   << 32) |
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)slot));
+    const bool in_order = lane >= bs || (t < a.num_tokens && slot == first + lane);
+    const uint64_t all = __ballot(in_order);
+    if (lane == 0) {
+      const bool base = first >= 0 && (first & (bs - 1)) == 0 &&
+                        (first >> bw.bs_log2) < a.num_blocks;
+      s_full = (all == ~0ull) && base;
+      s_block = first >> bw.bs_log2;
+    }
+  }
+  __syncthreads();
+
+  if (s_full) {
+    const int64_t b = s_block;
+    const int64_t src0 = t0 * a.row_bytes;
+    write_dense_block<Op>(a.src_k + src0, a.dst_k + b * a.gk.s_block, bw.k_bc_log2, bw,
+                          ks, lds);
+    write_dense_block<Op>(a.src_v + src0, a.dst_v + b * a.gv.s_block, bw.v_bc_log2, bw,
+                          vs, lds);
+    return;
+  }
+
+  // Per-token path: wave w takes tokens w, w + 4, ... of the group.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  for (int o = wave; o < bs; o += kWavesPerBlock) {
+    const int64_t t = t0 + o;
+    if (t >= a.num_tokens) break;
+    const int64_t slot = load_index(a.slots, t, a.slot_is64);
+    if (slot < 0) continue;
+    int64_t b, off;
+    split_slot(slot, a.block_size, b, off);
+    if (b >= a.num_blocks) continue;
+    const char *sk = a.src_k + t * a.row_bytes;
+    const char *sv = a.src_v + t * a.row_bytes;
+    char *dk = a.dst_k + b * a.gk.s_block + off * a.gk.s_off;
+    char *dv = a.dst_v + b * a.gv.s_block + off * a.gv.s_off;
+    for (int c = lane; c < a.nchunks; c += kWave) {
+      const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      const Raw<Op::kSrc> xk = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
+      const Raw<Op::kSrc> xv = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
+      st<Op::kDst>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim), Op::apply(xk, ks));
+      st<Op::kDst>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim), Op::apply(xv, vs));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Gather.
 //
-// One workgroup per (sequence, logical block).  seq_len and the block id are
-// wave-uniform scalar loads, read once per workgroup.  When the cache rows of
-// a block are contiguous (canonical NHD), the valid rows of the block are one
-// contiguous run in the cache and in the output, so the workgroup streams it
-// as a flat copy.  Other layouts map rows to (wave, lane group) and use the
-// per-lane chunk offsets as the write kernel does.
+// One workgroup per (sequence, logical block).  When the cache rows of a
+// block are contiguous (canonical NHD) gather_flat_kernel streams the block
+// as one flat copy; other layouts use gather_rows_kernel.
 
 struct GatherArgs {
   const char *src_k;
@@ -381,64 +593,88 @@ struct GatherArgs {
   int32_t flat;  // cache rows of a block are contiguous for K and V
 };
 
+// The (sequence, logical block) job of one workgroup: cache block and
+// output rows, or false when the block is skipped (past seq_len or
+// max_seq_len, beyond max_blocks_per_seq, or a block id outside
+// [0, num_blocks)).  seq_len and the block id are wave-uniform scalar loads.
+struct BlockJob {
+  const char *ck;
+  const char *cv;
+  char *ok;
+  char *ov;
+  int32_t rows;
+  float ks;
+  float vs;
+};
+
 template <class Op>
-__global__ __launch_bounds__(kBlockThreads) void gather_kernel(GatherArgs a) {
+__device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
   const int64_t wg = blockIdx.x;
   const int64_t s = wg / a.blocks_per_seq;
   const int32_t lb = (int32_t)(wg - s * a.blocks_per_seq);
-  if (lb >= a.max_blocks_per_seq) return;
+  if (lb >= a.max_blocks_per_seq) return false;
   const int64_t seq_len = load_index(a.seq_lens, s, a.index_is64);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int64_t t0 = (int64_t)lb * a.block_size;
-  if (t0 >= n) return;
+  if (t0 >= n) return false;
   const int64_t bid =
       load_index(a.table, s * a.max_blocks_per_seq + lb, a.index_is64);
-  if (bid < 0 || bid >= a.num_blocks) return;
+  if (bid < 0 || bid >= a.num_blocks) return false;
   const int64_t rem = n - t0;
-  const int32_t rows = rem < a.block_size ? (int32_t)rem : a.block_size;
-
-  float ks = 1.0f;
-  float vs = 1.0f;
+  j.rows = rem < a.block_size ? (int32_t)rem : a.block_size;
+  j.ks = 1.0f;
+  j.vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    j.ks = *a.k_scale;
+    j.vs = *a.v_scale;
   }
-
-  const char *ck = a.src_k + bid * a.gk.s_block;
-  const char *cv = a.src_v + bid * a.gv.s_block;
+  j.ck = a.src_k + bid * a.gk.s_block;
+  j.cv = a.src_v + bid * a.gv.s_block;
   const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
-  char *ok = a.dst_k + out0;
-  char *ov = a.dst_v + out0;
+  j.ok = a.dst_k + out0;
+  j.ov = a.dst_v + out0;
+  return true;
+}
 
-  if (a.flat) {
-    const int64_t total = (int64_t)rows * a.nchunks;
-    int64_t i = threadIdx.x;
-    for (; i + (kFlatUnroll - 1) * kBlockThreads < total;
-         i += kFlatUnroll * kBlockThreads) {
-      Raw<Op::kSrc> xk[kFlatUnroll];
-      Raw<Op::kSrc> xv[kFlatUnroll];
+// Canonical-NHD gather: the block's valid rows are one contiguous run in
+// the cache and in the output, streamed as a flat copy.
+template <class Op>
+__global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a) {
+  BlockJob j;
+  if (!gather_job<Op>(a, j)) return;
+  const int64_t total = (int64_t)j.rows * a.nchunks;
+  int64_t i = threadIdx.x;
+  for (; i + (kFlatUnroll - 1) * kBlockThreads < total;
+       i += kFlatUnroll * kBlockThreads) {
+    Raw<Op::kSrc> xk[kFlatUnroll];
+    Raw<Op::kSrc> xv[kFlatUnroll];
 #pragma unroll
-      for (int u = 0; u < kFlatUnroll; ++u) {
-        xk[u] = ld<Op::kSrc>(ck + (i + u * kBlockThreads) * Op::kSrc);
-        xv[u] = ld<Op::kSrc>(cv + (i + u * kBlockThreads) * Op::kSrc);
-      }
+    for (int u = 0; u < kFlatUnroll; ++u) {
+      xk[u] = ld<Op::kSrc, kGatherNtLoad>(j.ck + (i + u * kBlockThreads) * Op::kSrc);
+      xv[u] = ld<Op::kSrc, kGatherNtLoad>(j.cv + (i + u * kBlockThreads) * Op::kSrc);
+    }
 #pragma unroll
-      for (int u = 0; u < kFlatUnroll; ++u) {
-        st<Op::kDst>(ok + (i + u * kBlockThreads) * Op::kDst,
-                     Op::apply(xk[u], ks));
-        st<Op::kDst>(ov + (i + u * kBlockThreads) * Op::kDst,
-                     Op::apply(xv[u], vs));
-      }
+    for (int u = 0; u < kFlatUnroll; ++u) {
+      st<Op::kDst, kGatherNtStore>(j.ok + (i + u * kBlockThreads) * Op::kDst,
+                                   Op::apply(xk[u], j.ks));
+      st<Op::kDst, kGatherNtStore>(j.ov + (i + u * kBlockThreads) * Op::kDst,
+                                   Op::apply(xv[u], j.vs));
     }
-    for (; i < total; i += kBlockThreads) {
-      const Raw<Op::kSrc> yk = ld<Op::kSrc>(ck + i * Op::kSrc);
-      const Raw<Op::kSrc> yv = ld<Op::kSrc>(cv + i * Op::kSrc);
-      st<Op::kDst>(ok + i * Op::kDst, Op::apply(yk, ks));
-      st<Op::kDst>(ov + i * Op::kDst, Op::apply(yv, vs));
-    }
-    return;
   }
+  for (; i < total; i += kBlockThreads) {
+    const Raw<Op::kSrc> yk = ld<Op::kSrc, kGatherNtLoad>(j.ck + i * Op::kSrc);
+    const Raw<Op::kSrc> yv = ld<Op::kSrc, kGatherNtLoad>(j.cv + i * Op::kSrc);
+    st<Op::kDst, kGatherNtStore>(j.ok + i * Op::kDst, Op::apply(yk, j.ks));
+    st<Op::kDst, kGatherNtStore>(j.ov + i * Op::kDst, Op::apply(yv, j.vs));
+  }
+}
 
+// Any other layout: rows go to (wave, lane group), each lane keeps the
+// cache offsets of its chunks in registers.
+template <class Op>
+__global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a) {
+  BlockJob j;
+  if (!gather_job<Op>(a, j)) return;
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
   const int lpt = 1 << a.lpt_log2;
@@ -460,11 +696,11 @@ __global__ __launch_bounds__(kBlockThreads) void gather_kernel(GatherArgs a) {
     }
   }
 
-  for (int r = wave * tpw + sub; r < rows; r += kWavesPerBlock * tpw) {
-    const char *rk = ck + (int64_t)r * a.gk.s_off;
-    const char *rv = cv + (int64_t)r * a.gv.s_off;
-    char *wk = ok + (int64_t)r * a.out_row_bytes;
-    char *wv = ov + (int64_t)r * a.out_row_bytes;
+  for (int r = wave * tpw + sub; r < j.rows; r += kWavesPerBlock * tpw) {
+    const char *rk = j.ck + (int64_t)r * a.gk.s_off;
+    const char *rv = j.cv + (int64_t)r * a.gv.s_off;
+    char *wk = j.ok + (int64_t)r * a.out_row_bytes;
+    char *wv = j.ov + (int64_t)r * a.out_row_bytes;
     Raw<Op::kSrc> xk[kMaxChunksPerLane];
     Raw<Op::kSrc> xv[kMaxChunksPerLane];
 #pragma unroll
@@ -479,8 +715,8 @@ __global__ __launch_bounds__(kBlockThreads) void gather_kernel(GatherArgs a) {
     for (int k = 0; k < kMaxChunksPerLane; ++k) {
       const int c = l + k * lpt;
       if (c < a.nchunks) {
-        st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(xk[k], ks));
-        st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(xv[k], vs));
+        st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(xk[k], j.ks));
+        st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(xv[k], j.vs));
       }
     }
     for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
@@ -489,8 +725,8 @@ __global__ __launch_bounds__(kBlockThreads) void gather_kernel(GatherArgs a) {
           ld<Op::kSrc>(rk + chunk_off(a.gk, e, (uint32_t)a.head_dim));
       const Raw<Op::kSrc> yv =
           ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim));
-      st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(yk, ks));
-      st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(yv, vs));
+      st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(yk, j.ks));
+      st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(yv, j.vs));
     }
   }
 }
@@ -552,25 +788,44 @@ int lpt_log2_for(int nchunks) {
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// How a write launches: the per-token kernel, or the block kernel with its
+// LDS tile size and one workgroup per `bs` tokens.
+struct WriteLaunch {
+  int grid;
+  bool blocks;
+  BlockWriteArgs bw;
+  int64_t block_grid;
+  uint32_t lds_bytes;
+};
+
 template <class Op>
-void launch_write_op(const WriteArgs &a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL(write_kernel<Op>, dim3(grid), dim3(kBlockThreads), 0, s,
-                     a);
+void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
+  if (w.blocks) {
+    hipLaunchKernelGGL(write_blocks_kernel<Op>, dim3((uint32_t)w.block_grid),
+                       dim3(kBlockThreads), w.lds_bytes, s, a, w.bw);
+  } else {
+    hipLaunchKernelGGL(write_kernel<Op>, dim3(w.grid), dim3(kBlockThreads), 0, s, a);
+  }
 }
 
 template <class Op>
 void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
-  hipLaunchKernelGGL(gather_kernel<Op>, dim3((uint32_t)grid),
-                     dim3(kBlockThreads), 0, s, a);
+  if (a.flat) {
+    hipLaunchKernelGGL(gather_flat_kernel<Op>, dim3((uint32_t)grid),
+                       dim3(kBlockThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(gather_rows_kernel<Op>, dim3((uint32_t)grid),
+                       dim3(kBlockThreads), 0, s, a);
+  }
 }
 
 template <int IO>
-void dispatch_quant(int ge, const WriteArgs &a, int grid, hipStream_t s) {
+void dispatch_quant(int ge, const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   switch (ge) {
-    case 8: launch_write_op<QuantOp<8, IO>>(a, grid, s); break;
-    case 4: launch_write_op<QuantOp<4, IO>>(a, grid, s); break;
-    case 2: launch_write_op<QuantOp<2, IO>>(a, grid, s); break;
-    default: launch_write_op<QuantOp<1, IO>>(a, grid, s); break;
+    case 8: launch_write_op<QuantOp<8, IO>>(a, w, s); break;
+    case 4: launch_write_op<QuantOp<4, IO>>(a, w, s); break;
+    case 2: launch_write_op<QuantOp<2, IO>>(a, w, s); break;
+    default: launch_write_op<QuantOp<1, IO>>(a, w, s); break;
   }
 }
 
@@ -583,6 +838,52 @@ void dispatch_dequant(int ge, const GatherArgs &a, int64_t grid,
     case 2: launch_gather_op<DequantOp<2, IO>>(a, grid, s); break;
     default: launch_gather_op<DequantOp<1, IO>>(a, grid, s); break;
   }
+}
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int lg = 0;
+  while ((int64_t(1) << lg) < v) ++lg;
+  return lg;
+}
+
+// Chunks per contiguous per-token run when `g` is a dense block (the layout's
+// canonical in-block strides, any block stride), else -1.
+int64_t dense_run_chunks(const Geom &g, int64_t bs, int64_t H, int64_t D, int ge) {
+  if (g.s_inner != 1) return -1;
+  const int64_t E = H * D;
+  const int64_t p = g.pack;
+  if (p == D && g.s_piece == 0 && g.s_head == D && g.s_off == E) return E / ge;  // NHD
+  if (p == D && g.s_piece == 0 && g.s_off == D && g.s_head == bs * D) return D / ge;  // HND
+  if (p < D && g.s_off == p && g.s_piece == bs * p && g.s_head == (D / p) * bs * p)
+    return p / ge;  // HND_PACKED
+  return -1;
+}
+
+// Use the block kernel when some tensor is not row-dense (it needs the
+// in-block permutation), both are dense blocks with power-of-two shapes, and
+// the LDS tile fits in 64 KiB.
+bool plan_block_write(const WritePlan &p, int ge, int nchunks, int src_chunk_bytes,
+                      BlockWriteArgs *bw, int64_t *grid, uint32_t *lds_bytes) {
+  const int64_t bs = p.block_size;
+  if (bs > kWave || p.num_tokens < bs) return false;
+  const int64_t kbc = dense_run_chunks(p.gk, bs, p.heads, p.head_dim, ge);
+  const int64_t vbc = dense_run_chunks(p.gv, bs, p.heads, p.head_dim, ge);
+  if (kbc < 0 || vbc < 0) return false;
+  if (kbc == nchunks && vbc == nchunks) return false;  // both row-major: per-token kernel
+  bw->bs_log2 = log2_exact(bs);
+  bw->nchunks_log2 = log2_exact(nchunks);
+  bw->k_bc_log2 = log2_exact(kbc);
+  bw->v_bc_log2 = log2_exact(vbc);
+  if (bw->bs_log2 < 0 || bw->nchunks_log2 < 0 || bw->k_bc_log2 < 0 || bw->v_bc_log2 < 0)
+    return false;
+  bw->pitch = nchunks + 1;
+  bw->pad_ = 0;
+  const int64_t lds = bs * (int64_t)bw->pitch * src_chunk_bytes;
+  if (lds > 64 * 1024) return false;
+  *lds_bytes = (uint32_t)lds;
+  *grid = (p.num_tokens + bs - 1) / bs;
+  return *grid <= 0x7FFFFFFF;
 }
 
 }  // namespace
@@ -628,22 +929,25 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int tpw = kWave >> a.lpt_log2;
   a.num_groups = (p.num_tokens + tpw - 1) / tpw;
   const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
-  const int grid = (int)(want < 2048 ? want : 2048);
+  WriteLaunch wl;
+  wl.grid = (int)(want < 2048 ? want : 2048);
+  wl.blocks = plan_block_write(p, ge, a.nchunks, (p.conv == kConvQuant) ? ge * is : ge * cs,
+                               &wl.bw, &wl.block_grid, &wl.lds_bytes);
   hipStream_t s = as_stream(stream);
 
   if (p.conv == kConvCopy) {
     switch (ge * cs) {
-      case 16: launch_write_op<CopyOp<16>>(a, grid, s); break;
-      case 8: launch_write_op<CopyOp<8>>(a, grid, s); break;
-      case 4: launch_write_op<CopyOp<4>>(a, grid, s); break;
-      case 2: launch_write_op<CopyOp<2>>(a, grid, s); break;
-      default: launch_write_op<CopyOp<1>>(a, grid, s); break;
+      case 16: launch_write_op<CopyOp<16>>(a, wl, s); break;
+      case 8: launch_write_op<CopyOp<8>>(a, wl, s); break;
+      case 4: launch_write_op<CopyOp<4>>(a, wl, s); break;
+      case 2: launch_write_op<CopyOp<2>>(a, wl, s); break;
+      default: launch_write_op<CopyOp<1>>(a, wl, s); break;
     }
   } else {
     switch (p.io_dtype) {
-      case KVX_DTYPE_F32: dispatch_quant<KVX_DTYPE_F32>(ge, a, grid, s); break;
-      case KVX_DTYPE_F16: dispatch_quant<KVX_DTYPE_F16>(ge, a, grid, s); break;
-      default: dispatch_quant<KVX_DTYPE_BF16>(ge, a, grid, s); break;
+      case KVX_DTYPE_F32: dispatch_quant<KVX_DTYPE_F32>(ge, a, wl, s); break;
+      case KVX_DTYPE_F16: dispatch_quant<KVX_DTYPE_F16>(ge, a, wl, s); break;
+      default: dispatch_quant<KVX_DTYPE_BF16>(ge, a, wl, s); break;
     }
   }
   return hipGetLastError() == hipSuccess ? KVX_STATUS_OK

@@ -285,3 +285,51 @@ def test_c4_fp8_reduced():
 def test_c5_long_context_reduced():
     w = workloads.c5_llama70b_long(pool_blocks=3000, batch=3)
     _run_workload(w, torch.Generator().manual_seed(15))
+
+
+# ---------------------------------------------------------------------------
+# Block write (prefill groups that fill whole blocks, staged through LDS).
+
+def _block_slots(rng, nb, bs, groups):
+    """Slots for `groups` groups of bs tokens: most fill one block in order;
+    some have a -1, a swapped pair, an out-of-range block, or are cut short."""
+    blocks = rng.permutation(nb)[:groups]
+    slots = []
+    for gi, b in enumerate(blocks):
+        g = list(range(b * bs, b * bs + bs))
+        kind = gi % 6
+        if kind == 1:
+            g[bs // 2] = -1
+        elif kind == 2 and bs > 1:
+            g[0], g[1] = g[1], g[0]
+        elif kind == 3:
+            g = list(range((nb + 1) * bs, (nb + 2) * bs))  # block past num_blocks
+        slots += g
+    return np.array(slots[: len(slots) - bs // 2], dtype=np.int64)  # partial tail
+
+
+@pytest.mark.parametrize("kl,vl", [(PK, NHD), (HND, PK), (PK, PK), (HND, HND), (NHD, HND)])
+@pytest.mark.parametrize("dt,pack", [(DType.BF16, 8), (DType.F32, 4), (DType.F32, 8),
+                                     (DType.F8_E4M3, 16), (DType.F16, 16)])
+def test_block_write_paths(kl, vl, dt, pack):
+    rng = np.random.default_rng(hash((kl, vl, dt, pack)) % 1000)
+    gen = torch.Generator().manual_seed(21)
+    H, D, bs, nb = 8, 128, 16, 64
+    pc, kb, vb = make_cache(kl, vl, dt, nb, bs, H, D, pack, gen=gen)
+    slots = torch.tensor(_block_slots(rng, nb, bs, 24), device=DEV)
+    T = slots.numel()
+    key, val = rows(T, H, D, dt, gen), rows(T, H, D, dt, gen)
+    check_write(pc, kb, vb, key, val, slots, io_dtype=dt, cache_dtype=dt)
+
+
+@pytest.mark.parametrize("io", [DType.BF16, DType.F32])
+def test_block_write_quantizing_into_packed(io):
+    rng = np.random.default_rng(3)
+    gen = torch.Generator().manual_seed(22)
+    H, D, bs, nb = 8, 128, 16, 48
+    pc, kb, vb = make_cache(PK, NHD, DType.F8_E4M3, nb, bs, H, D, 16, gen=gen)
+    slots = torch.tensor(_block_slots(rng, nb, bs, 20), device=DEV)
+    T = slots.numel()
+    key, val = normal_rows(T, H, D, io, gen, 3.0), normal_rows(T, H, D, io, gen, 0.5)
+    check_write(pc, kb, vb, key, val, slots, io_dtype=io, cache_dtype=DType.F8_E4M3,
+                k_scale=0.011, v_scale=0.002)
