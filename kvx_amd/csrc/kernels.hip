@@ -33,13 +33,20 @@ constexpr int kMaxChunksPerLane = 4;
 // measured best on MI355X): chunks per lane in flight, and non-temporal
 // (streaming) loads of the cache / stores of the output.
 #ifndef KVX_FLAT_UNROLL
-#define KVX_FLAT_UNROLL 8
+#define KVX_FLAT_UNROLL 1
 #endif
 #ifndef KVX_GATHER_NT_LOAD
 #define KVX_GATHER_NT_LOAD 1
 #endif
 #ifndef KVX_GATHER_NT_STORE
 #define KVX_GATHER_NT_STORE 1
+#endif
+// Cache bytes per tensor one contiguous-block gather workgroup copies: a
+// block is split into power-of-two row ranges of about this size (at least
+// one row).  Many small tiles keep the set of HBM addresses being written
+// at any moment compact, which measures faster than fewer large tiles.
+#ifndef KVX_GATHER_TILE_BYTES
+#define KVX_GATHER_TILE_BYTES 4096
 #endif
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
 constexpr bool kGatherNtLoad = KVX_GATHER_NT_LOAD != 0;
@@ -230,20 +237,55 @@ struct QuantOp {
 };
 
 // E4M3 -> io (F16/BF16/F32): y = io(f32(q) * scale); any NaN result is the
-// canonical quiet NaN of the io type.
+// canonical quiet NaN of the io type.  gfx950 decodes two OCP E4M3 codes
+// exactly with v_cvt_pk_f32_fp8, multiplies in f32, and narrows two values
+// with round-to-nearest-even (v_cvt_pk_bf16_f32 / v_cvt_f16_f32); the result
+// equals fp_convert.h's e4m3_to_f32 / f32_to_bf16 / f32_to_f16, which the
+// GPU tests check for every code.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t canon_nan16(uint32_t h, uint32_t inf, uint32_t qnan) {
+  return ((h & 0x7FFFu) > inf) ? qnan : h;
+}
+
+template <int IO>
+__device__ __forceinline__ uint32_t pack_pair(f32x2 f) {
+  if constexpr (IO == KVX_DTYPE_BF16) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    return canon_nan16(u & 0xFFFFu, 0x7F80u, 0x7FC0u) |
+           (canon_nan16(u >> 16, 0x7F80u, 0x7FC0u) << 16);
+  } else {
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+    return canon_nan16(u & 0xFFFFu, 0x7C00u, 0x7E00u) |
+           (canon_nan16(u >> 16, 0x7C00u, 0x7E00u) << 16);
+  }
+}
+
 template <int G, int IO>
 struct DequantOp {
   static constexpr int kSrc = G;
   static constexpr int kDst = G * IoType<IO>::kBytes;
   static constexpr bool kScaled = true;
-  __device__ __forceinline__ static Raw<kDst> apply(const Raw<kSrc> &x,
-                                                    float scale) {
+  __device__ __forceinline__ static Raw<kDst> apply(const Raw<kSrc> &x, float scale) {
     Raw<kDst> y;
 #pragma unroll
     for (int k = 0; k < Raw<kDst>::kWords; ++k) y.w[k] = 0;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      f32_to_io<IO>(e4m3_to_f32((uint8_t)get8(x, i)) * scale, y, i);
+    for (int p = 0; p < (G + 1) / 2; ++p) {
+      // codes 2p, 2p+1 sit in halfword (p & 1) of word p / 2
+      const int word = (int)x.w[p >> 1];
+      const f32x2 f = ((p & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8(word, true)
+                               : __builtin_amdgcn_cvt_pk_f32_fp8(word, false)) * scale;
+      if constexpr (IO == KVX_DTYPE_F32) {
+        y.w[2 * p] = f32_bits(canon_nan_f32(f[0]));
+        if (2 * p + 1 < G) y.w[2 * p + 1] = f32_bits(canon_nan_f32(f[1]));
+      } else if constexpr (G == 1) {
+        y.w[0] = pack_pair<IO>(f) & 0xFFFFu;
+      } else {
+        y.w[p] = pack_pair<IO>(f);
+      }
     }
     return y;
   }
@@ -582,7 +624,7 @@ struct GatherArgs {
   int64_t out_row_bytes;  // bytes of one output row (H * D * io size)
   int32_t index_is64;
   int32_t max_blocks_per_seq;
-  int32_t blocks_per_seq;  // logical blocks launched per sequence
+  int32_t blocks_per_seq;  // workgroups per sequence
   int32_t max_seq_len;
   int32_t block_size;
   int32_t num_blocks;
@@ -591,6 +633,8 @@ struct GatherArgs {
   int32_t chunk_elems;
   int32_t lpt_log2;
   int32_t flat;  // cache rows of a block are contiguous for K and V
+  int32_t split_log2;  // flat only: workgroups per block = 1 << split_log2
+  int32_t pad_;
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -636,37 +680,69 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
   return true;
 }
 
-// Canonical-NHD gather: the block's valid rows are one contiguous run in
-// the cache and in the output, streamed as a flat copy.
+// Canonical-NHD gather: the valid rows of a block are one contiguous run in
+// the cache and in the output, streamed as a flat copy.  A workgroup copies
+// one power-of-two row range of a block (KVX_GATHER_TILE_BYTES).
+// Copy `total` chunks of K and of V: flat index f < 2 * total, K for
+// f < total, V above, so a one-row tile still gives every thread a chunk.
+template <class Op>
+__device__ __forceinline__ void flat_copy(const char *ck, const char *cv, char *ok,
+                                          char *ov, int64_t total, float ks, float vs) {
+  const int64_t both = 2 * total;
+  int64_t f = threadIdx.x;
+  for (; f + (kFlatUnroll - 1) * kBlockThreads < both; f += kFlatUnroll * kBlockThreads) {
+    Raw<Op::kSrc> x[kFlatUnroll];
+#pragma unroll
+    for (int u = 0; u < kFlatUnroll; ++u) {
+      const int64_t g = f + u * kBlockThreads;
+      const bool v = g >= total;
+      x[u] = ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + (g - (v ? total : 0)) * Op::kSrc);
+    }
+#pragma unroll
+    for (int u = 0; u < kFlatUnroll; ++u) {
+      const int64_t g = f + u * kBlockThreads;
+      const bool v = g >= total;
+      st<Op::kDst, kGatherNtStore>((v ? ov : ok) + (g - (v ? total : 0)) * Op::kDst,
+                                   Op::apply(x[u], v ? vs : ks));
+    }
+  }
+  for (; f < both; f += kBlockThreads) {
+    const bool v = f >= total;
+    const int64_t i = f - (v ? total : 0);
+    st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst,
+                                 Op::apply(ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + i * Op::kSrc),
+                                           v ? vs : ks));
+  }
+}
+
 template <class Op>
 __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a) {
-  BlockJob j;
-  if (!gather_job<Op>(a, j)) return;
-  const int64_t total = (int64_t)j.rows * a.nchunks;
-  int64_t i = threadIdx.x;
-  for (; i + (kFlatUnroll - 1) * kBlockThreads < total;
-       i += kFlatUnroll * kBlockThreads) {
-    Raw<Op::kSrc> xk[kFlatUnroll];
-    Raw<Op::kSrc> xv[kFlatUnroll];
-#pragma unroll
-    for (int u = 0; u < kFlatUnroll; ++u) {
-      xk[u] = ld<Op::kSrc, kGatherNtLoad>(j.ck + (i + u * kBlockThreads) * Op::kSrc);
-      xv[u] = ld<Op::kSrc, kGatherNtLoad>(j.cv + (i + u * kBlockThreads) * Op::kSrc);
-    }
-#pragma unroll
-    for (int u = 0; u < kFlatUnroll; ++u) {
-      st<Op::kDst, kGatherNtStore>(j.ok + (i + u * kBlockThreads) * Op::kDst,
-                                   Op::apply(xk[u], j.ks));
-      st<Op::kDst, kGatherNtStore>(j.ov + (i + u * kBlockThreads) * Op::kDst,
-                                   Op::apply(xv[u], j.vs));
-    }
+  const int64_t wg = blockIdx.x;
+  const int64_t s = wg / a.blocks_per_seq;
+  const int32_t w = (int32_t)(wg - s * a.blocks_per_seq);
+  const int32_t lb = w >> a.split_log2;
+  const int32_t part = w & ((1 << a.split_log2) - 1);
+  if (lb >= a.max_blocks_per_seq) return;
+  // seq_len and the block id do not depend on each other: load both at once.
+  const int64_t seq_len = load_index(a.seq_lens, s, a.index_is64);
+  const int64_t bid = load_index(a.table, s * a.max_blocks_per_seq + lb, a.index_is64);
+  const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  const int32_t rows_per_part = a.block_size >> a.split_log2;
+  const int64_t t0 = (int64_t)lb * a.block_size + (int64_t)part * rows_per_part;
+  if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
+  const int64_t rem = n - t0;
+  const int32_t rows = rem < rows_per_part ? (int32_t)rem : rows_per_part;
+  float ks = 1.0f;
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = *a.k_scale;
+    vs = *a.v_scale;
   }
-  for (; i < total; i += kBlockThreads) {
-    const Raw<Op::kSrc> yk = ld<Op::kSrc, kGatherNtLoad>(j.ck + i * Op::kSrc);
-    const Raw<Op::kSrc> yv = ld<Op::kSrc, kGatherNtLoad>(j.cv + i * Op::kSrc);
-    st<Op::kDst, kGatherNtStore>(j.ok + i * Op::kDst, Op::apply(yk, j.ks));
-    st<Op::kDst, kGatherNtStore>(j.ov + i * Op::kDst, Op::apply(yv, j.vs));
-  }
+  const int64_t row0 = (int64_t)part * rows_per_part;
+  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
+  flat_copy<Op>(a.src_k + bid * a.gk.s_block + row0 * a.gk.s_off,
+                a.src_v + bid * a.gv.s_block + row0 * a.gv.s_off, a.dst_k + out0,
+                a.dst_v + out0, (int64_t)rows * a.nchunks, ks, vs);
 }
 
 // Any other layout: rows go to (wave, lane group), each lane keeps the
@@ -976,6 +1052,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.out_row_bytes = row_elems * is;
   a.index_is64 = p.index_is64;
   a.max_blocks_per_seq = p.max_blocks_per_seq;
+  a.pad_ = 0;
   const int64_t by_len =
       ((int64_t)p.max_seq_len + p.block_size - 1) / p.block_size;
   a.blocks_per_seq =
@@ -994,6 +1071,15 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
            g.s_off == row_elems;
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
+  a.split_log2 = 0;
+  if (a.flat) {
+    // split a block into power-of-two row ranges of about TILE_BYTES per tensor
+    const int64_t row_bytes = row_elems * cs;
+    while ((int64_t)(p.block_size >> a.split_log2) * row_bytes > KVX_GATHER_TILE_BYTES &&
+           ((p.block_size >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == p.block_size)
+      ++a.split_log2;
+    a.blocks_per_seq <<= a.split_log2;  // workgroups per sequence
+  }
   if (a.blocks_per_seq <= 0 || p.seq_count <= 0) return KVX_STATUS_OK;
   const int64_t grid = (int64_t)p.seq_count * a.blocks_per_seq;
   if (grid > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;  // one workgroup per block
