@@ -1,0 +1,217 @@
+"""Full-size BASELINE configurations on the GPU, checked through properties
+that do not need the CPU oracle to run at that size:
+
+  - write -> gather round trip: every written row comes back bit-exact at its
+    sequence position;
+  - the whole gather equals an independent implementation (torch advanced
+    indexing of the paged cache on int16 views), row by row, and rows past
+    seq_len keep the output's prior contents;
+  - cache blocks the write does not address keep their prior contents;
+  - FP8 (c4): the quantized rows match the oracle (they are few), and the
+    full dequantizing gather equals torch's own float8_e4m3fn -> f32 * scale
+    -> bf16 chain with NaNs canonicalised.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kvx_amd import paged, workloads
+from kvx_amd.abi import DType, Layout, Status
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _release_device_memory():
+    """Full-size tests hold up to ~220 GB; return it to the device between
+    tests so the next large allocation is not fragmented."""
+    torch.cuda.empty_cache()
+    yield
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def i16(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.uint8)
+
+
+def block_view(cache: torch.Tensor, layout: Layout, pack: int) -> torch.Tensor:
+    """[nb, bs, H, D] view (element order) of a canonical cache tensor."""
+    if layout == Layout.BLOCK_NHD:
+        return cache
+    if layout == Layout.BLOCK_HND:
+        return cache.permute(0, 2, 1, 3)
+    nb, H, dx, bs, x = cache.shape
+    return cache.permute(0, 3, 1, 2, 4).reshape(nb, bs, H, dx * x)
+
+
+def check_gather_against_indexing(pc, w, ko, vo, ko_before, vo_before, seqs_per_chunk=16):
+    """Compare every gathered row with cache[block_table] and every padding
+    row with the output's previous contents."""
+    bs, L = w.block_size, w.max_seq_len
+    table = torch.tensor(w.block_table, device=DEV).long()
+    lens = torch.tensor(w.seq_lens, device=DEV).long().clamp(min=0, max=L)
+    kv = [block_view(pc.key_cache, pc.k_layout, w.pack), block_view(pc.value_cache, pc.v_layout, w.pack)]
+    pos = torch.arange(L, device=DEV)
+    for s0 in range(0, w.seq_count, seqs_per_chunk):
+        s1 = min(s0 + seqs_per_chunk, w.seq_count)
+        lb = (pos // bs).clamp(max=w.max_blocks_per_seq - 1)
+        bid = table[s0:s1][:, lb]                                   # [n, L]
+        valid = (pos[None, :] < lens[s0:s1, None]) & (pos[None, :] // bs < w.max_blocks_per_seq)
+        valid &= (bid >= 0) & (bid < w.num_blocks)
+        for src, out, before in zip(kv, (ko, vo), (ko_before, vo_before)):
+            ref = i16(src)[bid.clamp(min=0, max=w.num_blocks - 1), pos[None, :] % bs]  # [n, L, H, D]
+            got = i16(out[s0:s1])
+            old = i16(before[s0:s1])
+            m = valid[:, :, None, None]
+            assert torch.equal(torch.where(m, ref, old), got), f"sequences {s0}..{s1}"
+            del ref
+
+
+def sentinel_like(shape, dtype, fill=-5):
+    t = torch.empty(shape, dtype=dtype, device=DEV)
+    i16(t).fill_(fill)
+    return t
+
+
+def test_c2_full_decode_write_then_gather():
+    w = workloads.c2_llama8b_decode()
+    H, D, bs = w.heads, w.head_dim, w.block_size
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.bfloat16, DEV)
+    pc.key_cache.normal_()
+    pc.value_cache.normal_()
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    k0, v0 = pc.key_cache.clone(), pc.value_cache.clone()
+    assert paged.write_kv(pc, key, val, slots) == Status.OK
+    torch.cuda.synchronize()
+    # only the addressed rows changed, and they hold the new tokens
+    ok = slots >= 0
+    blk, off = slots[ok] // bs, slots[ok] % bs
+    assert torch.equal(i16(pc.key_cache[blk, off]), i16(key[ok]))
+    assert torch.equal(i16(pc.value_cache[blk, off]), i16(val[ok]))
+    k0[blk, off] = pc.key_cache[blk, off]
+    v0[blk, off] = pc.value_cache[blk, off]
+    assert torch.equal(i16(k0), i16(pc.key_cache)) and torch.equal(i16(v0), i16(pc.value_cache))
+    del k0, v0
+
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16, 3)
+    kb, vb = ko.clone(), vo.clone()
+    table = torch.tensor(w.block_table, device=DEV)
+    lens = torch.tensor(w.seq_lens, device=DEV)
+    assert paged.gather_kv(pc, ko, vo, table, lens, L) == Status.OK
+    torch.cuda.synchronize()
+    # round trip: the new token of every non-padded sequence is at position len - 1
+    seqs = torch.nonzero(ok).flatten()
+    last = lens.long()[seqs] - 1
+    assert torch.equal(i16(ko[seqs, last]), i16(key[seqs]))
+    assert torch.equal(i16(vo[seqs, last]), i16(val[seqs]))
+    check_gather_against_indexing(pc, w, ko, vo, kb, vb)
+
+
+@pytest.mark.parametrize("v_layout", [Layout.BLOCK_NHD, Layout.BLOCK_HND])
+def test_c3_full_prefill_packed_write_roundtrip(v_layout):
+    w = workloads.c3_llama8b_prefill(v_layout=v_layout)
+    H, D, bs = w.heads, w.head_dim, w.block_size
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.bfloat16, DEV, w.k_layout, w.v_layout,
+                           w.pack)
+    i16(pc.key_cache).fill_(-7)
+    i16(pc.value_cache).fill_(-7)
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots, tokens_per_seq=w.tokens_per_seq) == Status.OK
+    torch.cuda.synchronize()
+    # every written row is in place (through the layout's own indexing)
+    kview = block_view(pc.key_cache, pc.k_layout, w.pack)
+    vview = block_view(pc.value_cache, pc.v_layout, w.pack)
+    blk, off = slots // bs, slots % bs
+    assert torch.equal(i16(kview[blk, off]), i16(key))
+    assert torch.equal(i16(vview[blk, off]), i16(val))
+    # blocks outside the table are untouched
+    used = torch.zeros(w.num_blocks, dtype=torch.bool, device=DEV)
+    used[torch.tensor(w.block_table, device=DEV).long().flatten()] = True
+    assert bool((i16(pc.key_cache[~used]) == -7).all()) and bool((i16(pc.value_cache[~used]) == -7).all())
+    # gather back: the contiguous output equals the input rows
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16)
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV),
+                           torch.tensor(w.seq_lens, device=DEV), L) == Status.OK
+    torch.cuda.synchronize()
+    assert torch.equal(i16(ko.reshape(-1, H, D)), i16(key))
+    assert torch.equal(i16(vo.reshape(-1, H, D)), i16(val))
+
+
+def test_c4_full_fp8_quantize_and_dequant_gather():
+    w = workloads.c4_llama8b_fp8()
+    H, D, bs = w.heads, w.head_dim, w.block_size
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.float8_e4m3fn, DEV)
+    pc.key_cache.view(torch.uint8).random_(0, 256)
+    pc.value_cache.view(torch.uint8).random_(0, 256)
+    g = torch.Generator(device=DEV).manual_seed(w.notes["calibration_seed"])
+    cal = torch.randn((w.num_tokens, H, D), generator=g, device=DEV) * 2.0
+    ks = (cal.abs().max() / 448.0).reshape(1).float()
+    vs = (ks * 0.75).contiguous()
+    key = (torch.randn((w.num_tokens, H, D), device=DEV) * 2.0).to(torch.bfloat16)
+    val = (torch.randn((w.num_tokens, H, D), device=DEV) * 2.0).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots, k_scale=ks, v_scale=vs) == Status.OK
+    torch.cuda.synchronize()
+    ok = slots >= 0
+    blk, off = slots[ok] // bs, slots[ok] % bs
+    for src, cache, sc in ((key, pc.key_cache, ks), (val, pc.value_cache, vs)):
+        want = oracle.quantize_e4m3(src[ok].view(torch.int16).cpu().numpy().view(np.uint16),
+                                    DType.BF16, float(sc))
+        got = cache[blk, off].view(torch.uint8).cpu().numpy().reshape(-1)
+        assert np.array_equal(got, want)
+
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16)
+    kb, vb = ko.clone(), vo.clone()
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV),
+                           torch.tensor(w.seq_lens, device=DEV), L, k_scale=ks,
+                           v_scale=vs) == Status.OK
+    torch.cuda.synchronize()
+    # reference caches: torch's own float8 -> f32 * scale -> bf16, NaN canonical
+    def deq(c, sc):
+        y = (c.float() * sc).to(torch.bfloat16)
+        bits = y.view(torch.int16).clone()
+        bits[torch.isnan(y)] = 0x7FC0
+        return bits.view(torch.bfloat16)
+    ref = paged.PagedCache(deq(pc.key_cache, ks), deq(pc.value_cache, vs), pc.k_layout,
+                           pc.v_layout, pc.num_blocks, bs, H, D)
+    check_gather_against_indexing(ref, w, ko, vo, kb, vb)
+
+
+def test_c5_full_long_context_200gb_pool():
+    w = workloads.c5_llama70b_long()
+    H, D, bs = w.heads, w.head_dim, w.block_size
+    free, _ = torch.cuda.mem_get_info()
+    need = 2 * w.num_blocks * bs * H * D * 2 + 4 * w.seq_count * w.max_seq_len * H * D * 2
+    if free < need * 1.05:
+        pytest.skip(f"needs {need / 1e9:.0f} GB of free device memory, {free / 1e9:.0f} GB free")
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.bfloat16, DEV)
+    pc.key_cache.normal_()
+    pc.value_cache.normal_()
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots, tokens_per_seq=w.tokens_per_seq) == Status.OK
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16)
+    kb, vb = ko.clone(), vo.clone()
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV),
+                           torch.tensor(w.seq_lens, device=DEV), L) == Status.OK
+    torch.cuda.synchronize()
+    # the 32 written tokens of each sequence are its last 32 rows
+    lens = torch.tensor(w.seq_lens, device=DEV).long()
+    tps = w.tokens_per_seq
+    idx = (lens[:, None] - tps + torch.arange(tps, device=DEV)[None, :])
+    srow = torch.arange(S, device=DEV)[:, None].expand(-1, tps)
+    assert torch.equal(i16(ko[srow, idx]).reshape(-1, H, D), i16(key))
+    assert torch.equal(i16(vo[srow, idx]).reshape(-1, H, D), i16(val))
+    check_gather_against_indexing(pc, w, ko, vo, kb, vb, seqs_per_chunk=4)
