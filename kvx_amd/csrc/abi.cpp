@@ -2,8 +2,10 @@
 //
 // Validation restates reference kvx_abi.c:5-466 check for check: the same
 // status codes in the same order (strict canonical strides, equal K/V layout
-// and dtype, non-NULL data, table counts per format, PACKED-only gather
-// checked last).  After validation succeeds the call executes:
+// and dtype, non-NULL data, table counts per format).  The one difference is
+// the reference's last gather check, PACKED-only (kvx_abi.c:462-464): RAGGED
+// and KV_OFFSETS tables are executed here.  After validation succeeds the
+// call executes:
 //   - every payload buffer KVX_MEMORY_HOST  -> validation only, OK (this is
 //     all the reference does for any memory type, kvx_abi.c:354-466);
 //   - DEVICE / UNIFIED                       -> HIP kernels on `stream`;
@@ -204,13 +206,28 @@ bool device_accessible(const void *p) {
          (attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr);
 }
 
-Exec classify(const kvx_tensor_desc_t *const *ts, int n) {
+// Buffers of one call: all HOST -> validation only; a mix of HOST and
+// device memory -> UNSUPPORTED; UNKNOWN memory is asked of the runtime.
+// `pool` (KV_OFFSETS gathers) adds the pool pointers to the set.
+Exec classify(const kvx_tensor_desc_t *const *ts, int n,
+              const kvx_pool_desc_t *pool = nullptr) {
+  struct Buf {
+    kvx_memory_type_t memory;
+    const void *data;
+  } bufs[7];
+  int m = 0;
+  for (int i = 0; i < n; ++i) bufs[m++] = {ts[i]->memory, ts[i]->data};
+  if (pool != nullptr) {
+    bufs[m++] = {pool->memory, pool->primary};
+    if (pool->secondary != nullptr) bufs[m++] = {pool->memory, pool->secondary};
+  }
   int host = 0;
-  for (int i = 0; i < n; ++i) host += ts[i]->memory == KVX_MEMORY_HOST;
-  if (host == n) return Exec::kValidateOnly;
+  for (int i = 0; i < m; ++i) host += bufs[i].memory == KVX_MEMORY_HOST;
+  if (host == m) return Exec::kValidateOnly;
   if (host != 0) return Exec::kUnsupported;
-  for (int i = 0; i < n; ++i) {
-    if (ts[i]->memory == KVX_MEMORY_UNKNOWN && !device_accessible(ts[i]->data))
+  for (int i = 0; i < m; ++i) {
+    if (bufs[i].memory == KVX_MEMORY_UNKNOWN && bufs[i].data != nullptr &&
+        !device_accessible(bufs[i].data))
       return Exec::kUnsupported;
   }
   return Exec::kDevice;
@@ -306,11 +323,14 @@ KVX_API kvx_status_t kvx_gather_kv(const kvx_cache_desc_t *cache,
   st = check_io_4d(&io.value, gather->block_table.seq_count,
                    gather->max_seq_len, io.num_kv_heads, io.head_dim);
   if (st != KVX_STATUS_OK) return st;
-  if (gather->block_table.format != KVX_BLOCK_TABLE_PACKED)
-    return KVX_STATUS_UNSUPPORTED;
+  // The reference ends with "format != PACKED -> UNSUPPORTED" (kvx_abi.c:462);
+  // this build gathers RAGGED and KV_OFFSETS tables too.
 
-  const kvx_tensor_desc_t *ts[4] = {&cache->k, &cache->v, &io.key, &io.value};
-  switch (classify(ts, 4)) {
+  // KV_OFFSETS blocks live in the pool: the cache tensors only describe the
+  // in-block layout and their data pointers are not read.
+  const bool offsets = gather->block_table.format == KVX_BLOCK_TABLE_KV_OFFSETS;
+  const kvx_tensor_desc_t *ts[4] = {&io.key, &io.value, &cache->k, &cache->v};
+  switch (classify(ts, offsets ? 2 : 4, offsets ? &cache->pool : nullptr)) {
     case Exec::kValidateOnly: return KVX_STATUS_OK;
     case Exec::kUnsupported: return KVX_STATUS_UNSUPPORTED;
     case Exec::kDevice: break;

@@ -619,10 +619,17 @@ struct GatherArgs {
   const void *seq_lens;
   const float *k_scale;
   const float *v_scale;
+  const void *indptr;        // RAGGED
+  int64_t table_count;       // RAGGED: entries of `table`
+  const char *pool[2];       // KV_OFFSETS primary / secondary
+  int64_t bytes_per_block;   // KV_OFFSETS
   GeomBytes gk;
   GeomBytes gv;
   int64_t out_row_bytes;  // bytes of one output row (H * D * io size)
   int32_t index_is64;
+  int32_t lens_is64;
+  int32_t indptr_is64;
+  int32_t rows_per_wg;    // RAGGED / KV_OFFSETS: output rows per workgroup
   int32_t max_blocks_per_seq;
   int32_t blocks_per_seq;  // workgroups per sequence
   int32_t max_seq_len;
@@ -634,7 +641,7 @@ struct GatherArgs {
   int32_t lpt_log2;
   int32_t flat;  // cache rows of a block are contiguous for K and V
   int32_t split_log2;  // flat only: workgroups per block = 1 << split_log2
-  int32_t pad_;
+  int32_t format;      // kvx_block_table_format_t
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -657,7 +664,7 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
   const int64_t s = wg / a.blocks_per_seq;
   const int32_t lb = (int32_t)(wg - s * a.blocks_per_seq);
   if (lb >= a.max_blocks_per_seq) return false;
-  const int64_t seq_len = load_index(a.seq_lens, s, a.index_is64);
+  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int64_t t0 = (int64_t)lb * a.block_size;
   if (t0 >= n) return false;
@@ -724,7 +731,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a
   const int32_t part = w & ((1 << a.split_log2) - 1);
   if (lb >= a.max_blocks_per_seq) return;
   // seq_len and the block id do not depend on each other: load both at once.
-  const int64_t seq_len = load_index(a.seq_lens, s, a.index_is64);
+  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
   const int64_t bid = load_index(a.table, s * a.max_blocks_per_seq + lb, a.index_is64);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int32_t rows_per_part = a.block_size >> a.split_log2;
@@ -803,6 +810,117 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
           ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim));
       st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(yk, j.ks));
       st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(yv, j.vs));
+    }
+  }
+}
+
+// RAGGED and KV_OFFSETS gathers (KVX_SPEC.md:99-122).  A workgroup covers
+// `rows_per_wg` output rows of one sequence; every row resolves its own
+// source, so K and V rows come from wherever the table points:
+//   RAGGED      row t of sequence s is token i = indptr[s] + t, valid for
+//               t < indptr[s+1] - indptr[s]; block id = indices[i] (skipped
+//               when < 0 or >= num_blocks), block offset = t % block_size.
+//   KV_OFFSETS  table [seq, beam = 1, {K, V}, max_blocks_per_seq] of
+//               KVCacheIndex values: bit 31 selects the secondary pool,
+//               bits 0..30 are the block index (skipped when >= num_blocks or
+//               when the selected pool is NULL); block address = pool +
+//               index * bytes_per_block, offset t % block_size.  K and V rows
+//               are resolved independently.
+// Rows t >= min(seq_len, max_seq_len) are untouched, as in the PACKED gather.
+template <class Op, int FMT>
+__global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArgs a) {
+  const int64_t wg = blockIdx.x;
+  const int64_t s = wg / a.blocks_per_seq;
+  const int64_t t0 = (wg - s * a.blocks_per_seq) * (int64_t)a.rows_per_wg;
+  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
+  int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  int64_t start = 0;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    start = load_index(a.indptr, s, a.indptr_is64);
+    if (start < 0) return;
+    int64_t cnt = load_index(a.indptr, s + 1, a.indptr_is64) - start;
+    const int64_t left = a.table_count - start;  // entries the table holds
+    cnt = left < cnt ? left : cnt;
+    n = cnt < n ? cnt : n;
+  } else {
+    const int64_t cap = (int64_t)a.max_blocks_per_seq * a.block_size;
+    n = cap < n ? cap : n;
+  }
+  if (t0 >= n) return;
+
+  float ks = 1.0f;
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = *a.k_scale;
+    vs = *a.v_scale;
+  }
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int lpt = 1 << a.lpt_log2;
+  const int tpw = kWave >> a.lpt_log2;
+  const int sub = lane >> a.lpt_log2;
+  const int l = lane & (lpt - 1);
+
+  int64_t koff[kMaxChunksPerLane];
+  int64_t voff[kMaxChunksPerLane];
+#pragma unroll
+  for (int k = 0; k < kMaxChunksPerLane; ++k) {
+    const int c = l + k * lpt;
+    koff[k] = 0;
+    voff[k] = 0;
+    if (c < a.nchunks) {
+      const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      koff[k] = chunk_off(a.gk, e, (uint32_t)a.head_dim);
+      voff[k] = chunk_off(a.gv, e, (uint32_t)a.head_dim);
+    }
+  }
+
+  for (int r = wave * tpw + sub; r < a.rows_per_wg; r += kWavesPerBlock * tpw) {
+    const int64_t t = t0 + r;
+    if (t >= n) break;
+    const char *rk = nullptr;
+    const char *rv = nullptr;
+    if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+      const int64_t bid = load_index(a.table, start + t, a.index_is64);
+      if (bid >= 0 && bid < a.num_blocks) {
+        const int64_t o = t % a.block_size;
+        rk = a.src_k + bid * a.gk.s_block + o * a.gk.s_off;
+        rv = a.src_v + bid * a.gv.s_block + o * a.gv.s_off;
+      }
+    } else {
+      const int64_t lb = t / a.block_size;
+      const int64_t o = t - lb * a.block_size;
+      const int32_t *row = reinterpret_cast<const int32_t *>(a.table) +
+                           s * 2 * (int64_t)a.max_blocks_per_seq;
+      const uint32_t kidx = (uint32_t)row[lb];
+      const uint32_t vidx = (uint32_t)row[a.max_blocks_per_seq + lb];
+      const char *kp = a.pool[kidx >> 31];
+      const char *vp = a.pool[vidx >> 31];
+      const int64_t kb = kidx & 0x7FFFFFFFu;
+      const int64_t vb = vidx & 0x7FFFFFFFu;
+      if (kp != nullptr && kb < a.num_blocks) rk = kp + kb * a.bytes_per_block + o * a.gk.s_off;
+      if (vp != nullptr && vb < a.num_blocks) rv = vp + vb * a.bytes_per_block + o * a.gv.s_off;
+    }
+    char *wk = a.dst_k + (s * a.max_seq_len + t) * a.out_row_bytes;
+    char *wv = a.dst_v + (s * a.max_seq_len + t) * a.out_row_bytes;
+#pragma unroll
+    for (int k = 0; k < kMaxChunksPerLane; ++k) {
+      const int c = l + k * lpt;
+      if (c < a.nchunks) {
+        if (rk != nullptr)
+          st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(ld<Op::kSrc>(rk + koff[k]), ks));
+        if (rv != nullptr)
+          st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(ld<Op::kSrc>(rv + voff[k]), vs));
+      }
+    }
+    for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
+      const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      if (rk != nullptr)
+        st<Op::kDst>(wk + (int64_t)c * Op::kDst,
+                     Op::apply(ld<Op::kSrc>(rk + chunk_off(a.gk, e, (uint32_t)a.head_dim)), ks));
+      if (rv != nullptr)
+        st<Op::kDst>(wv + (int64_t)c * Op::kDst,
+                     Op::apply(ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim)), vs));
     }
   }
 }
@@ -886,7 +1004,13 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
 
 template <class Op>
 void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
-  if (a.flat) {
+  if (a.format == KVX_BLOCK_TABLE_RAGGED) {
+    hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_RAGGED>), dim3((uint32_t)grid),
+                       dim3(kBlockThreads), 0, s, a);
+  } else if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS>),
+                       dim3((uint32_t)grid), dim3(kBlockThreads), 0, s, a);
+  } else if (a.flat) {
     hipLaunchKernelGGL(gather_flat_kernel<Op>, dim3((uint32_t)grid),
                        dim3(kBlockThreads), 0, s, a);
   } else {
@@ -1034,7 +1158,16 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   const int cs = dtype_size((kvx_dtype_t)p.cache_dtype);
   const int is = dtype_size((kvx_dtype_t)p.io_dtype);
   const int max_bytes = (p.conv == kConvDequant) ? 8 : 16;
-  const int ge = pick_chunk(p.gk, p.gv, p.src_k, p.src_v, cs, p.dst_k,
+  const void *base_k = p.src_k;
+  const void *base_v = p.src_v;
+  if (p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    // Blocks start at pool + index * bytes_per_block: every such address is
+    // as aligned as the OR of both pool pointers and the block pitch.
+    base_k = base_v = reinterpret_cast<const void *>(
+        reinterpret_cast<uintptr_t>(p.pool[0]) | reinterpret_cast<uintptr_t>(p.pool[1]) |
+        (uintptr_t)p.bytes_per_block);
+  }
+  const int ge = pick_chunk(p.gk, p.gv, base_k, base_v, cs, p.dst_k,
                             p.dst_v, is, p.head_dim, max_bytes);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
 
@@ -1051,8 +1184,16 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.gv = to_bytes(p.gv, cs);
   a.out_row_bytes = row_elems * is;
   a.index_is64 = p.index_is64;
+  a.lens_is64 = p.lens_is64;
+  a.indptr = p.indptr;
+  a.indptr_is64 = p.indptr_is64;
+  a.table_count = p.table_count;
+  a.pool[0] = p.pool[0];
+  a.pool[1] = p.pool[1];
+  a.bytes_per_block = p.bytes_per_block;
+  a.format = p.format;
+  a.rows_per_wg = 0;
   a.max_blocks_per_seq = p.max_blocks_per_seq;
-  a.pad_ = 0;
   const int64_t by_len =
       ((int64_t)p.max_seq_len + p.block_size - 1) / p.block_size;
   a.blocks_per_seq =
@@ -1072,7 +1213,16 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
-  if (a.flat) {
+  if (p.format != KVX_BLOCK_TABLE_PACKED) {
+    // indexed formats: tiles of rows, about 4 KiB of each tensor's cache rows,
+    // at least one full pass of the workgroup's row groups
+    const int64_t per_pass = (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
+    int64_t rows = KVX_GATHER_TILE_BYTES / (row_elems * cs);
+    rows = rows < per_pass ? per_pass : rows;
+    a.rows_per_wg = (int32_t)rows;
+    a.flat = 0;
+    a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
+  } else if (a.flat) {
     // split a block into power-of-two row ranges of about TILE_BYTES per tensor
     const int64_t row_bytes = row_elems * cs;
     while ((int64_t)(p.block_size >> a.split_log2) * row_bytes > KVX_GATHER_TILE_BYTES &&

@@ -67,9 +67,16 @@ struct GatherPlan {
   const void *seq_lens;
   const float *k_scale;  // device pointers; only for kConvDequant
   const float *v_scale;
+  const void *indptr;       // RAGGED: [seq_count + 1] token prefix sums
+  int64_t table_count;      // entries of block_table
+  const char *pool[2];      // KV_OFFSETS: primary / secondary pool bases
+  int64_t bytes_per_block;  // KV_OFFSETS
   Geom gk;
   Geom gv;
-  int32_t index_is64;  // block table and seq_lens share one dtype
+  int32_t format;      // kvx_block_table_format_t
+  int32_t indptr_is64;
+  int32_t index_is64;  // block table (PACKED, RAGGED) / seq_lens dtype
+  int32_t lens_is64;
   int32_t seq_count;
   int32_t max_blocks_per_seq;
   int32_t max_seq_len;

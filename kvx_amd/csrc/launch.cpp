@@ -10,7 +10,8 @@
 //   - block_size == 0 with a non-empty batch   -> INVALID_ARGUMENT
 //   - NULL io / cache / index data pointers     -> INVALID_ARGUMENT
 // F8_E4M3 caches (quantizing write, byte-copy gather, dequantizing gather)
-// are extensions; the reference returns UNSUPPORTED for them.
+// and the RAGGED / KV_OFFSETS gather formats are extensions; the reference
+// returns UNSUPPORTED for them (kernels/kvx_paged_kv.cu:481-490, :788-790).
 #include <hip/hip_runtime.h>
 
 #include "kvx_ext.h"
@@ -92,6 +93,17 @@ kvx_status_t fill_geom(const kvx_cache_desc_t *cache,
     default:
       return KVX_STATUS_UNSUPPORTED;
   }
+}
+
+// True when all in-block offsets of `g` (block index 0) are non-negative and
+// the last element ends within `pitch` bytes.
+bool block_fits(const Geom &g, int64_t bs, int64_t heads, int64_t head_dim, int esize,
+                int64_t pitch) {
+  if (g.s_off < 0 || g.s_head < 0 || g.s_piece < 0 || g.s_inner < 0) return false;
+  const int64_t pieces = head_dim / g.pack;
+  const int64_t last = (bs - 1) * g.s_off + (heads - 1) * g.s_head +
+                       (pieces - 1) * g.s_piece + (int64_t)(g.pack - 1) * g.s_inner;
+  return (last + 1) * esize <= pitch;
 }
 
 // Resolve a per-tensor F32 scale for the quantizing write
@@ -232,7 +244,9 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
   } else if (io_dt != expected || gather->io.value.dtype != expected) {
     return KVX_STATUS_UNSUPPORTED;
   }
-  if (gather->block_table.format != KVX_BLOCK_TABLE_PACKED)
+  const kvx_block_table_format_t fmt = gather->block_table.format;
+  if (fmt != KVX_BLOCK_TABLE_PACKED && fmt != KVX_BLOCK_TABLE_RAGGED &&
+      fmt != KVX_BLOCK_TABLE_KV_OFFSETS)
     return KVX_STATUS_UNSUPPORTED;
   const int32_t heads = (int32_t)gather->io.num_kv_heads;
   const int32_t head_dim = (int32_t)gather->io.head_dim;
@@ -266,19 +280,51 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
 
   const int64_t total = (int64_t)seq_count * max_seq_len * heads * head_dim;
   if (total == 0) return KVX_STATUS_OK;
-  const kvx_dtype_t idx_dt = gather->block_table.index_dtype;
+  const kvx_block_table_t &tb = gather->block_table;
+  const kvx_dtype_t idx_dt = tb.index_dtype;
   const kvx_dtype_t len_dt = gather->seq_lens.dtype;
   const bool s32 = idx_dt == KVX_DTYPE_S32 && len_dt == KVX_DTYPE_S32;
   const bool s64 = idx_dt == KVX_DTYPE_S64 && len_dt == KVX_DTYPE_S64;
-  if (!s32 && !s64) return KVX_STATUS_INVALID_ARGUMENT;
+  if (fmt == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    // KVX_SPEC.md:116-122: S32 KVCacheIndex values, flag set, power-of-two
+    // block size, a primary pool; beam_width > 1 has no output layout here.
+    if (idx_dt != KVX_DTYPE_S32) return KVX_STATUS_INVALID_ARGUMENT;
+    if (len_dt != KVX_DTYPE_S32 && len_dt != KVX_DTYPE_S64) return KVX_STATUS_INVALID_ARGUMENT;
+    if ((tb.flags & KVX_BLOCK_TABLE_FLAG_KVCACHEINDEX) == 0) return KVX_STATUS_INVALID_ARGUMENT;
+    if (tb.beam_width == 0) return KVX_STATUS_INVALID_ARGUMENT;
+    if (tb.beam_width != 1) return KVX_STATUS_UNSUPPORTED;
+    if (cache->block_size == 0 || (cache->block_size & (cache->block_size - 1)) != 0)
+      return KVX_STATUS_INVALID_ARGUMENT;
+    if (cache->pool.bytes_per_block == 0 || cache->pool.primary == nullptr)
+      return KVX_STATUS_INVALID_ARGUMENT;
+    if ((uint64_t)tb.indices_count != (uint64_t)tb.seq_count * 2u * tb.max_blocks_per_seq)
+      return KVX_STATUS_INVALID_ARGUMENT;
+    // Every element of a block must lie inside its bytes_per_block pitch.
+    const int esize = dtype_size(cache->k.dtype);
+    if (!block_fits(p.gk, cache->block_size, heads, head_dim, esize,
+                    cache->pool.bytes_per_block) ||
+        !block_fits(p.gv, cache->block_size, heads, head_dim, esize,
+                    cache->pool.bytes_per_block))
+      return KVX_STATUS_INVALID_ARGUMENT;
+  } else if (!s32 && !s64) {
+    return KVX_STATUS_INVALID_ARGUMENT;
+  }
+  if (fmt == KVX_BLOCK_TABLE_RAGGED) {
+    // KVX_SPEC.md:107-114: indptr holds seq_count + 1 prefix sums.
+    if (tb.indptr_dtype != KVX_DTYPE_S32 && tb.indptr_dtype != KVX_DTYPE_S64)
+      return KVX_STATUS_INVALID_ARGUMENT;
+    if (tb.indptr == nullptr || tb.indptr_count != tb.seq_count + 1)
+      return KVX_STATUS_INVALID_ARGUMENT;
+  }
 
   // Checks added by this build (see file comment).
   if (cache->block_size == 0) return KVX_STATUS_INVALID_ARGUMENT;
   if (gather->io.key.data == nullptr || gather->io.value.data == nullptr ||
-      cache->k.data == nullptr || cache->v.data == nullptr ||
       gather->seq_lens.lengths == nullptr ||
-      (gather->block_table.max_blocks_per_seq > 0 &&
-       gather->block_table.indices == nullptr))
+      (fmt != KVX_BLOCK_TABLE_KV_OFFSETS &&
+       (cache->k.data == nullptr || cache->v.data == nullptr)) ||
+      (fmt == KVX_BLOCK_TABLE_PACKED && tb.max_blocks_per_seq > 0 && tb.indices == nullptr) ||
+      (fmt != KVX_BLOCK_TABLE_PACKED && tb.indices_count > 0 && tb.indices == nullptr))
     return KVX_STATUS_INVALID_ARGUMENT;
 
   p.src_k = cache->k.data;
@@ -287,7 +333,15 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
   p.dst_v = gather->io.value.data;
   p.block_table = gather->block_table.indices;
   p.seq_lens = gather->seq_lens.lengths;
-  p.index_is64 = s64;
+  p.format = fmt;
+  p.index_is64 = idx_dt == KVX_DTYPE_S64;
+  p.lens_is64 = len_dt == KVX_DTYPE_S64;
+  p.indptr = tb.indptr;
+  p.table_count = tb.indices_count;
+  p.indptr_is64 = tb.indptr_dtype == KVX_DTYPE_S64;
+  p.pool[0] = static_cast<const char *>(cache->pool.primary);
+  p.pool[1] = static_cast<const char *>(cache->pool.secondary);
+  p.bytes_per_block = cache->pool.bytes_per_block;
   p.seq_count = seq_count;
   p.max_blocks_per_seq = (int32_t)gather->block_table.max_blocks_per_seq;
   p.max_seq_len = max_seq_len;

@@ -138,10 +138,79 @@ def build_write(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
     return w
 
 
+@dataclass
+class RaggedTable:
+    """RAGGED block table (KVX_SPEC.md:107-114): token t of sequence s is
+    cached in block ``indices[indptr[s] + t]`` at offset ``t % block_size``,
+    for t < indptr[s+1] - indptr[s]."""
+
+    indices: torch.Tensor  # [total tokens] int32 / int64 block ids
+    indptr: torch.Tensor   # [seq_count + 1] int32 / int64 prefix sums
+
+
+@dataclass
+class OffsetsTable:
+    """KV_OFFSETS block table (KVX_SPEC.md:116-122, TensorRT-LLM's
+    KVBlockArray): int32 ``offsets[s, 0, 0 (K) / 1 (V), j]`` are KVCacheIndex
+    values; block j of sequence s lives at ``pool + (value & 0x7FFFFFFF) *
+    bytes_per_block`` with bit 31 choosing the secondary pool.  The cache's K
+    / V tensors give only the in-block layout."""
+
+    offsets: torch.Tensor              # int32 [seq_count, 1, 2, max_blocks_per_seq]
+    primary: torch.Tensor              # pool storage (its bytes)
+    secondary: torch.Tensor | None
+    bytes_per_block: int
+
+
+def kv_cache_index(block: int, secondary: bool = False) -> int:
+    """The int32 KVCacheIndex value for `block` in the primary or secondary
+    pool (KV_CACHE_LAYOUTS.md:91-92)."""
+    v = (int(block) & 0x7FFFFFFF) | (0x80000000 if secondary else 0)
+    return v - (1 << 32) if v >= 0x80000000 else v
+
+
+def _table_desc(table) -> abi.BlockTable:
+    if isinstance(table, RaggedTable):
+        t = abi.BlockTable()
+        t.size = C.sizeof(abi.BlockTable)
+        t.format = int(abi.TableFormat.RAGGED)
+        t.index_dtype = int(dtype_code(table.indices))
+        t.indptr_dtype = int(dtype_code(table.indptr))
+        t.seq_count = table.indptr.numel() - 1
+        t.beam_width = 1
+        t.max_blocks_per_seq = 1  # not used by RAGGED; the ABI path requires > 0
+        t.indices = table.indices.data_ptr()
+        t.indptr = table.indptr.data_ptr()
+        t.indices_count = table.indices.numel()
+        t.indptr_count = table.indptr.numel()
+        return t
+    if isinstance(table, OffsetsTable):
+        S, beam, two, mbps = table.offsets.shape
+        if two != 2 or table.offsets.dtype != torch.int32:
+            raise ValueError("KV_OFFSETS table is int32 [seq_count, beam, 2, max_blocks]")
+        t = abi.BlockTable()
+        t.size = C.sizeof(abi.BlockTable)
+        t.format = int(abi.TableFormat.KV_OFFSETS)
+        t.index_dtype = int(DType.S32)
+        t.seq_count = S
+        t.beam_width = beam
+        t.max_blocks_per_seq = mbps
+        t.indices = table.offsets.data_ptr()
+        t.indices_count = table.offsets.numel()
+        t.flags = abi.TABLE_FLAG_KVCACHEINDEX
+        return t
+    S, mbps = table.shape
+    return abi.make_block_table_packed(S, mbps, dtype_code(table), table.data_ptr())
+
+
 def build_gather(key_out: torch.Tensor, value_out: torch.Tensor,
-                 block_table: torch.Tensor, seq_lens: torch.Tensor,
+                 block_table, seq_lens: torch.Tensor,
                  max_seq_len: int) -> abi.GatherDesc:
-    S, mbps = block_table.shape
+    """kvx_gather_desc_t for [S, max_seq_len, H, D] outputs.  `block_table` is
+    a [S, max_blocks_per_seq] tensor (PACKED), a RaggedTable or an
+    OffsetsTable."""
+    tb = _table_desc(block_table)
+    S = tb.seq_count
     g = abi.GatherDesc()
     g.size = C.sizeof(abi.GatherDesc)
     g.io.size = C.sizeof(abi.KvIoDesc)
@@ -150,8 +219,7 @@ def build_gather(key_out: torch.Tensor, value_out: torch.Tensor,
     g.io.num_tokens = S * max_seq_len
     g.io.num_kv_heads = key_out.shape[2]
     g.io.head_dim = key_out.shape[3]
-    g.block_table = abi.make_block_table_packed(S, mbps, dtype_code(block_table),
-                                                block_table.data_ptr())
+    g.block_table = tb
     g.seq_lens = abi.make_seq_lens(seq_lens.numel(), dtype_code(seq_lens),
                                    seq_lens.data_ptr())
     g.max_seq_len = max_seq_len
@@ -177,14 +245,23 @@ def write_kv(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
 
 
 def gather_kv(cache: PagedCache, key_out: torch.Tensor, value_out: torch.Tensor,
-              block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int, *,
+              block_table, seq_lens: torch.Tensor, max_seq_len: int, *,
               k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
               stream=None, entry: str = "launch") -> Status:
     """Gather sequences into contiguous [S, max_seq_len, H, D] buffers.
+    `block_table` is a PACKED [S, max_blocks_per_seq] tensor, a RaggedTable
+    or an OffsetsTable (whose pool replaces the cache tensors' data).
     With k_scale/v_scale the FP8 cache is dequantized
     (kvx_launch_gather_kv_dequant)."""
     lib = abi.load()
     cd = cache.desc()
+    if isinstance(block_table, OffsetsTable):
+        cd.pool.size = C.sizeof(abi.PoolDesc)
+        cd.pool.memory = int(memory_of(block_table.primary))
+        cd.pool.bytes_per_block = block_table.bytes_per_block
+        cd.pool.primary = block_table.primary.data_ptr()
+        cd.pool.secondary = (None if block_table.secondary is None
+                             else block_table.secondary.data_ptr())
     gd = build_gather(key_out, value_out, block_table, seq_lens, max_seq_len)
     s = _stream_handle(stream)
     if entry == "abi":

@@ -41,6 +41,12 @@ def lib() -> C.CDLL:
         L.oracle_gather_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32,
                                                           i32, i32, i32, i32, i32, i32, i]
         L.oracle_gather_kv_fast.restype = i
+        L.oracle_gather_kv_ragged.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, vp, i,
+                                                            vp, i, i32, i32, i32, i32, i32,
+                                                            i32, i, i, f32, f32]
+        L.oracle_gather_kv_offsets.argtypes = geom + geom + [vp, vp, i64, vp, vp, vp, vp, i,
+                                                             i32, i32, i32, i32, i32, i32,
+                                                             i32, i, i, f32, f32]
         L.oracle_f32_to_e4m3.argtypes = [f32]
         L.oracle_f32_to_e4m3.restype = C.c_uint8
         L.oracle_e4m3_to_f32.argtypes = [C.c_uint8]
@@ -111,6 +117,41 @@ def gather_kv(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value
                            seq_count, max_blocks_per_seq, max_seq_len, heads, head_dim,
                            block_size, num_blocks, int(cache_dtype), int(io_dtype),
                            float(k_scale), float(v_scale))
+
+
+def gather_kv_ragged(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value_out,
+                     indices, indptr, seq_lens, *, max_seq_len, heads, head_dim, block_size,
+                     num_blocks, cache_dtype, io_dtype, k_scale=1.0, v_scale=1.0) -> None:
+    """RAGGED-table gather (KVX_SPEC.md:107-114), in place."""
+    indices = np.ascontiguousarray(indices)
+    indptr = np.ascontiguousarray(indptr)
+    seq_lens = np.ascontiguousarray(seq_lens)
+    lib().oracle_gather_kv_ragged(*gk.args(), *gv.args(), _ptr(key_cache), _ptr(value_cache),
+                                  _ptr(key_out), _ptr(value_out), _ptr(indices),
+                                  int(indices.dtype == np.int64), int(indices.size),
+                                  _ptr(indptr),
+                                  int(indptr.dtype == np.int64), _ptr(seq_lens),
+                                  int(seq_lens.dtype == np.int64), int(seq_lens.size),
+                                  max_seq_len, heads, head_dim, block_size, num_blocks,
+                                  int(cache_dtype), int(io_dtype), float(k_scale),
+                                  float(v_scale))
+
+
+def gather_kv_offsets(gk: Geometry, gv: Geometry, pool_primary, pool_secondary,
+                      bytes_per_block, key_out, value_out, table, seq_lens, *,
+                      max_blocks_per_seq, max_seq_len, heads, head_dim, block_size,
+                      num_blocks, cache_dtype, io_dtype, k_scale=1.0, v_scale=1.0) -> None:
+    """KV_OFFSETS-table gather (KVX_SPEC.md:116-122), in place.  `table` is
+    int32 [seq_count, 1, 2, max_blocks_per_seq]; pool_secondary may be None."""
+    table = np.ascontiguousarray(table, dtype=np.int32)
+    seq_lens = np.ascontiguousarray(seq_lens)
+    sec = None if pool_secondary is None else _ptr(pool_secondary)
+    lib().oracle_gather_kv_offsets(*gk.args(), *gv.args(), _ptr(pool_primary), sec,
+                                   int(bytes_per_block), _ptr(key_out), _ptr(value_out),
+                                   _ptr(table), _ptr(seq_lens), int(seq_lens.dtype == np.int64),
+                                   int(seq_lens.size), max_blocks_per_seq, max_seq_len, heads,
+                                   head_dim, block_size, num_blocks, int(cache_dtype),
+                                   int(io_dtype), float(k_scale), float(v_scale))
 
 
 def write_kv_fast(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache, slots,

@@ -317,6 +317,97 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
   }
 }
 
+/* One element of a row: copy or dequantize from `src` to `dst`. */
+static void move_elem(const uint8_t *src, uint8_t *dst, int dequant, int cs, int is,
+                      int io_dtype, float scale) {
+  if (dequant) {
+    dequant_one(*src, scale, io_dtype, dst);
+  } else {
+    memcpy(dst, src, (size_t)(cs < is ? cs : is));
+  }
+}
+
+/* KVX_SPEC.md:107-114 */
+void oracle_gather_kv_ragged(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                             int v_layout, const int64_t *v_stride, int64_t v_pack,
+                             const void *key_cache, const void *value_cache,
+                             void *key_out, void *value_out, const void *indices,
+                             int index_is64, int64_t indices_count, const void *indptr,
+                             int indptr_is64, const void *seq_lens, int lens_is64,
+                             int32_t seq_count, int32_t max_seq_len, int32_t heads,
+                             int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                             int cache_dtype, int io_dtype, float k_scale, float v_scale) {
+  const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
+  const int dequant = io_dtype != cache_dtype;
+  const uint8_t *kc = key_cache, *vc = value_cache;
+  uint8_t *ko_ = key_out, *vo_ = value_out;
+  for (int64_t s = 0; s < seq_count; ++s) {
+    const int64_t seq_len = load_index(seq_lens, s, lens_is64);
+    const int64_t start = load_index(indptr, s, indptr_is64);
+    const int64_t cnt = load_index(indptr, s + 1, indptr_is64) - start;
+    for (int64_t t = 0; t < max_seq_len; ++t) {
+      if (t >= seq_len || t >= cnt || start < 0 || start + t >= indices_count) continue;
+      const int64_t bid = load_index(indices, start + t, index_is64);
+      if (bid < 0 || bid >= num_blocks) continue;
+      const int64_t o = t % block_size;
+      for (int64_t h = 0; h < heads; ++h) {
+        for (int64_t d = 0; d < head_dim; ++d) {
+          const int64_t idx = ((s * max_seq_len + t) * heads + h) * head_dim + d;
+          const int64_t ko = oracle_cache_offset(k_layout, k_stride, k_pack, bid, o, h, d);
+          const int64_t vo = oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d);
+          move_elem(kc + ko * cs, ko_ + idx * is, dequant, cs, is, io_dtype, k_scale);
+          move_elem(vc + vo * cs, vo_ + idx * is, dequant, cs, is, io_dtype, v_scale);
+        }
+      }
+    }
+  }
+}
+
+/* KVX_SPEC.md:116-122; KV_CACHE_LAYOUTS.md:89-94 */
+void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                              int v_layout, const int64_t *v_stride, int64_t v_pack,
+                              const void *pool_primary, const void *pool_secondary,
+                              int64_t bytes_per_block, void *key_out, void *value_out,
+                              const int32_t *table, const void *seq_lens, int lens_is64,
+                              int32_t seq_count, int32_t max_blocks_per_seq,
+                              int32_t max_seq_len, int32_t heads, int32_t head_dim,
+                              int32_t block_size, int32_t num_blocks, int cache_dtype,
+                              int io_dtype, float k_scale, float v_scale) {
+  const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
+  const int dequant = io_dtype != cache_dtype;
+  const uint8_t *pools[2] = {pool_primary, pool_secondary};
+  uint8_t *outs[2] = {key_out, value_out};
+  const int layouts[2] = {k_layout, v_layout};
+  const int64_t *strides[2] = {k_stride, v_stride};
+  const int64_t packs[2] = {k_pack, v_pack};
+  const float scales[2] = {k_scale, v_scale};
+  for (int64_t s = 0; s < seq_count; ++s) {
+    const int64_t seq_len = load_index(seq_lens, s, lens_is64);
+    for (int64_t t = 0; t < max_seq_len; ++t) {
+      if (t >= seq_len) continue;
+      const int64_t lb = t / block_size;
+      if (lb >= max_blocks_per_seq) continue;
+      const int64_t o = t - lb * block_size;
+      for (int kv = 0; kv < 2; ++kv) {
+        const uint32_t raw = (uint32_t)table[(s * 2 + kv) * max_blocks_per_seq + lb];
+        const uint8_t *pool = pools[raw >> 31];
+        const int64_t blk = (int64_t)(raw & 0x7FFFFFFFu);
+        if (pool == NULL || blk >= num_blocks) continue;
+        const uint8_t *base = pool + blk * bytes_per_block;
+        for (int64_t h = 0; h < heads; ++h) {
+          for (int64_t d = 0; d < head_dim; ++d) {
+            const int64_t idx = ((s * max_seq_len + t) * heads + h) * head_dim + d;
+            const int64_t off = oracle_cache_offset(layouts[kv], strides[kv], packs[kv], 0, o,
+                                                    h, d);
+            move_elem(base + off * cs, outs[kv] + idx * is, dequant, cs, is, io_dtype,
+                      scales[kv]);
+          }
+        }
+      }
+    }
+  }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Fast bit-copy variants (the timed CPU baseline).                           */
 

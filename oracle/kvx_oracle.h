@@ -51,6 +51,38 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                       int32_t num_blocks, int cache_dtype, int io_dtype,
                       float k_scale, float v_scale);
 
+/* RAGGED table gather (KVX_SPEC.md:107-114): row t of sequence s is token
+ * i = indptr[s] + t for t < min(seq_len, indptr[s+1] - indptr[s],
+ * max_seq_len); its block id is indices[i] (skipped when < 0 or
+ * >= num_blocks) and its block offset t % block_size.  Tokens with
+ * i outside [0, indices_count) are skipped (malformed indptr). */
+void oracle_gather_kv_ragged(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                             int v_layout, const int64_t *v_stride, int64_t v_pack,
+                             const void *key_cache, const void *value_cache,
+                             void *key_out, void *value_out, const void *indices,
+                             int index_is64, int64_t indices_count, const void *indptr,
+                             int indptr_is64, const void *seq_lens, int lens_is64,
+                             int32_t seq_count, int32_t max_seq_len, int32_t heads,
+                             int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                             int cache_dtype, int io_dtype, float k_scale, float v_scale);
+
+/* KV_OFFSETS table gather (KVX_SPEC.md:116-122, KV_CACHE_LAYOUTS.md:89-94):
+ * table [seq_count, 1, 2, max_blocks_per_seq] of int32 KVCacheIndex values,
+ * bit 31 selecting the secondary pool; block address = pool + (value &
+ * 0x7FFFFFFF) * bytes_per_block, skipped when the index is >= num_blocks or
+ * the pool is NULL.  In-block addressing follows the K / V strides (the
+ * block stride is unused).  Rows t >= min(seq_len, max_seq_len) or with
+ * t / block_size >= max_blocks_per_seq are untouched. */
+void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                              int v_layout, const int64_t *v_stride, int64_t v_pack,
+                              const void *pool_primary, const void *pool_secondary,
+                              int64_t bytes_per_block, void *key_out, void *value_out,
+                              const int32_t *table, const void *seq_lens, int lens_is64,
+                              int32_t seq_count, int32_t max_blocks_per_seq,
+                              int32_t max_seq_len, int32_t heads, int32_t head_dim,
+                              int32_t block_size, int32_t num_blocks, int cache_dtype,
+                              int io_dtype, float k_scale, float v_scale);
+
 /* Same results as the element-wise functions for bit-copy calls, with one
  * memcpy per contiguous run and OpenMP over tokens / (sequence, block); the
  * timed CPU baseline.  Returns the number of OpenMP threads used. */

@@ -8,7 +8,7 @@ import torch
 
 import oracle
 from kvx_amd import paged
-from kvx_amd.abi import DType, Layout, Status
+from kvx_amd.abi import DType, Layout, Status, contiguous_strides
 
 TORCH_DT = {DType.F32: torch.float32, DType.F16: torch.float16,
             DType.BF16: torch.bfloat16, DType.F8_E4M3: torch.float8_e4m3fn}
@@ -112,3 +112,93 @@ def check_gather(pc, kbuf, vbuf, key_out, value_out, table, lens, max_seq_len, *
 def _first_diff(a: np.ndarray, b: np.ndarray) -> str:
     idx = np.flatnonzero(a != b)
     return f"{idx.size} bytes differ, first at {idx[:8].tolist()}"
+
+
+def _scales(k_scale, v_scale, device):
+    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
+                                                   device=device)
+    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
+                                                   device=device)
+    return ks, vs
+
+
+def check_gather_ragged(pc, kbuf, vbuf, key_out, value_out, table: paged.RaggedTable, lens,
+                        max_seq_len, *, cache_dtype, io_dtype, k_scale=None, v_scale=None,
+                        entry="launch"):
+    """RAGGED-table gather on the GPU and in the oracle; bit-identical outputs."""
+    ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
+    ks, vs = _scales(k_scale, v_scale, key_out.device)
+    st = paged.gather_kv(pc, key_out, value_out, table, lens, max_seq_len, k_scale=ks,
+                         v_scale=vs, entry=entry)
+    assert st == Status.OK, st
+    torch.cuda.synchronize()
+    oracle.gather_kv_ragged(kbuf.geometry(), vbuf.geometry(), np_bytes(kbuf.base),
+                            np_bytes(vbuf.base), ko0, vo0, table.indices.cpu().numpy(),
+                            table.indptr.cpu().numpy(), lens.cpu().numpy(),
+                            max_seq_len=max_seq_len, heads=pc.heads, head_dim=pc.head_dim,
+                            block_size=pc.block_size, num_blocks=pc.num_blocks,
+                            cache_dtype=cache_dtype, io_dtype=io_dtype,
+                            k_scale=1.0 if k_scale is None else k_scale,
+                            v_scale=1.0 if v_scale is None else v_scale)
+    got_k, got_v = np_bytes(key_out), np_bytes(value_out)
+    assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
+    assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)
+
+
+class OffsetsPool:
+    """KV_OFFSETS storage: a primary (and optional secondary) pool of
+    `num_blocks` single-tensor blocks every `bytes_per_block` bytes, and K / V
+    cache views over the primary pool that carry the in-block layouts."""
+
+    def __init__(self, k_layout, v_layout, dtype, nb, bs, H, D, pack=8, pitch_pad=0,
+                 secondary=True, device="cuda", gen=None):
+        gen = gen or torch.Generator().manual_seed(0)
+        es = TORCH_DT[dtype].itemsize
+        self.bytes_per_block = bs * H * D * es + pitch_pad
+        assert self.bytes_per_block % es == 0
+        self.primary = random_fill(torch.empty(nb * self.bytes_per_block, dtype=torch.uint8,
+                                               device=device), gen)
+        self.secondary = None
+        if secondary:
+            self.secondary = random_fill(torch.empty_like(self.primary), gen)
+        typed = self.primary.view(TORCH_DT[dtype])
+        self.geoms = []
+        views = []
+        for layout in (k_layout, v_layout):
+            shape = paged.cache_shape(layout, nb, bs, H, D, pack)
+            st = list(contiguous_strides(shape))
+            st[0] = self.bytes_per_block // es
+            views.append(torch.as_strided(typed, shape, st))
+            self.geoms.append(oracle.Geometry(layout, st,
+                                              pack if layout == Layout.BLOCK_HND_PACKED else 1))
+        self.pc = paged.PagedCache(views[0], views[1], Layout(k_layout), Layout(v_layout),
+                                   nb, bs, H, D)
+
+    def table(self, offsets: torch.Tensor) -> paged.OffsetsTable:
+        return paged.OffsetsTable(offsets, self.primary, self.secondary, self.bytes_per_block)
+
+
+def check_gather_offsets(pool: OffsetsPool, key_out, value_out, offsets, lens, max_seq_len,
+                         *, cache_dtype, io_dtype, k_scale=None, v_scale=None,
+                         entry="launch"):
+    """KV_OFFSETS-table gather on the GPU and in the oracle; bit-identical
+    outputs."""
+    pc = pool.pc
+    ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
+    ks, vs = _scales(k_scale, v_scale, key_out.device)
+    st = paged.gather_kv(pc, key_out, value_out, pool.table(offsets), lens, max_seq_len,
+                         k_scale=ks, v_scale=vs, entry=entry)
+    assert st == Status.OK, st
+    torch.cuda.synchronize()
+    sec = None if pool.secondary is None else np_bytes(pool.secondary)
+    oracle.gather_kv_offsets(pool.geoms[0], pool.geoms[1], np_bytes(pool.primary), sec,
+                             pool.bytes_per_block, ko0, vo0, offsets.cpu().numpy(),
+                             lens.cpu().numpy(), max_blocks_per_seq=offsets.shape[3],
+                             max_seq_len=max_seq_len, heads=pc.heads, head_dim=pc.head_dim,
+                             block_size=pc.block_size, num_blocks=pc.num_blocks,
+                             cache_dtype=cache_dtype, io_dtype=io_dtype,
+                             k_scale=1.0 if k_scale is None else k_scale,
+                             v_scale=1.0 if v_scale is None else v_scale)
+    got_k, got_v = np_bytes(key_out), np_bytes(value_out)
+    assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
+    assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)

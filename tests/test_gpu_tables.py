@@ -1,0 +1,249 @@
+"""GPU parity of the RAGGED and KV_OFFSETS block-table gathers
+(KVX_SPEC.md:107-122): libkvx_amd.so through the C ABI, bit-identical to the
+CPU oracle on the same seeded inputs, outputs pre-filled with random bytes so
+that untouched rows are checked too.
+
+RAGGED: random per-token block ids with -1 and out-of-range ids, indptr
+ranges shorter and longer than seq_len / max_seq_len, S32 / S64 indices,
+indptr and lengths.  KV_OFFSETS: K and V blocks drawn from one pool,
+secondary-pool flags with and without a secondary pool, out-of-range
+indices, padded block pitches (including pitches that force narrower
+vector chunks), in-block layouts NHD / HND / HND_PACKED, mixed K / V.  Both:
+FP8 dequantizing gathers, rows wide enough for the kernel's tail loop,
+misaligned outputs, and the kvx_abi.h entry point.
+"""
+import numpy as np
+import pytest
+import torch
+
+from kvx_amd import paged
+from kvx_amd.abi import DType, Layout
+
+from gpu_helpers import (TORCH_DT, OffsetsPool, check_gather_offsets, check_gather_ragged,
+                         make_cache, random_fill)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NHD, HND, PK = Layout.BLOCK_NHD, Layout.BLOCK_HND, Layout.BLOCK_HND_PACKED
+LAYOUTS = [NHD, HND, PK]
+DTYPES = [DType.F32, DType.F16, DType.BF16, DType.F8_E4M3]
+
+
+def out_pair(S, L, H, D, dtype, gen, misalign=False):
+    outs = []
+    for _ in range(2):
+        if misalign:
+            flat = torch.empty(S * L * H * D + 1, dtype=TORCH_DT[dtype], device=DEV)
+            t = flat[1:].view(S, L, H, D)
+        else:
+            t = torch.empty((S, L, H, D), dtype=TORCH_DT[dtype], device=DEV)
+        outs.append(random_fill(t, gen))
+    return outs
+
+
+def ragged_table(rng, S, L, nb, idt, pdt, long_tail=True):
+    counts = rng.integers(0, L + (4 if long_tail else 1), size=S)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(pdt)
+    indices = rng.integers(-1, nb + 2, size=max(int(indptr[-1]), 1)).astype(idt)
+    return paged.RaggedTable(torch.from_numpy(indices).to(DEV),
+                             torch.from_numpy(indptr).to(DEV))
+
+
+def lens_tensor(rng, S, L, dt):
+    return torch.from_numpy(rng.integers(-1, L + 4, size=S).astype(dt)).to(DEV)
+
+
+# ---------------------------------------------------------------------------
+# RAGGED
+
+@pytest.mark.parametrize("seed", range(24))
+def test_ragged_random(seed):
+    rng = np.random.default_rng(3000 + seed)
+    gen = torch.Generator().manual_seed(seed)
+    dt = DTYPES[seed % 4]
+    kl, vl = LAYOUTS[seed % 3], LAYOUTS[(seed // 3) % 3]
+    H = int(rng.choice([1, 2, 8]))
+    D = int(rng.choice([8, 64, 128]))
+    bs = int(rng.choice([1, 4, 16, 32]))
+    nb = int(rng.integers(2, 40))
+    pad = [None, 1, 2][seed % 3]
+    pc, kb, vb = make_cache(kl, vl, dt, nb, bs, H, D, gen=gen, k_pad=pad,
+                            v_pad=[None, 0, 3][seed % 3])
+    S, L = int(rng.integers(1, 7)), int(rng.integers(1, 300))
+    idt = [np.int32, np.int64][seed % 2]
+    pdt = [np.int32, np.int64][(seed // 2) % 2]
+    table = ragged_table(rng, S, L, nb, idt, pdt)
+    lens = lens_tensor(rng, S, L, idt)
+    ko, vo = out_pair(S, L, H, D, dt, gen, misalign=seed % 5 == 4)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("io", [DType.BF16, DType.F16, DType.F32])
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_ragged_fp8_dequant(io, layout):
+    rng = np.random.default_rng(41)
+    gen = torch.Generator().manual_seed(41)
+    H, D, bs, nb, S, L = 4, 128, 16, 24, 5, 90
+    pc, kb, vb = make_cache(layout, layout, DType.F8_E4M3, nb, bs, H, D, gen=gen)
+    table = ragged_table(rng, S, L, nb, np.int32, np.int64)
+    lens = lens_tensor(rng, S, L, np.int32)
+    ko, vo = out_pair(S, L, H, D, io, gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=DType.F8_E4M3,
+                        io_dtype=io, k_scale=0.0172, v_scale=3.5)
+
+
+@pytest.mark.parametrize("dt,H", [(DType.F32, 16), (DType.BF16, 32), (DType.F8_E4M3, 8)])
+def test_ragged_wide_rows(dt, H):
+    """Rows of more than 4 chunks per lane exercise the kernel's tail loop."""
+    rng = np.random.default_rng(5)
+    gen = torch.Generator().manual_seed(5)
+    D, bs, nb, S, L = 128, 16, 20, 3, 70
+    pc, kb, vb = make_cache(NHD, HND, dt, nb, bs, H, D, gen=gen)
+    table = ragged_table(rng, S, L, nb, np.int64, np.int32)
+    lens = lens_tensor(rng, S, L, np.int64)
+    ko, vo = out_pair(S, L, H, D, dt, gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F16, DType.F32])
+def test_ragged_abi_entry(dt):
+    """kvx_gather_kv (kvx_abi.h) executes RAGGED tables on device memory."""
+    rng = np.random.default_rng(8)
+    gen = torch.Generator().manual_seed(8)
+    H, D, bs, nb, S, L = 8, 128, 16, 32, 4, 64
+    for layout in LAYOUTS:
+        pc, kb, vb = make_cache(layout, layout, dt, nb, bs, H, D, gen=gen)
+        table = ragged_table(rng, S, L, nb, np.int32, np.int32)
+        lens = lens_tensor(rng, S, L, np.int32)
+        ko, vo = out_pair(S, L, H, D, dt, gen)
+        check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt,
+                            io_dtype=dt, entry="abi")
+
+
+def test_ragged_decode_shape():
+    """A decode batch in RAGGED form: 64 sequences of 100-900 tokens,
+    Llama-3-8B KV shape, token ids listing each sequence's blocks in order."""
+    rng = np.random.default_rng(9)
+    gen = torch.Generator().manual_seed(9)
+    H, D, bs, S = 8, 128, 16, 64
+    lens_np = rng.integers(100, 900, size=S).astype(np.int32)
+    L = int(lens_np.max())
+    nblk = (lens_np + bs - 1) // bs
+    nb = int(nblk.sum())
+    perm = rng.permutation(nb)
+    indices, base = [], 0
+    for s in range(S):
+        blocks = perm[base: base + nblk[s]]
+        base += nblk[s]
+        indices.append(np.repeat(blocks, bs)[: lens_np[s]])
+    indptr = np.concatenate([[0], np.cumsum(lens_np)]).astype(np.int32)
+    table = paged.RaggedTable(torch.from_numpy(np.concatenate(indices).astype(np.int32)).to(DEV),
+                              torch.from_numpy(indptr).to(DEV))
+    pc, kb, vb = make_cache(NHD, NHD, DType.BF16, nb, bs, H, D, gen=gen)
+    ko, vo = out_pair(S, L, H, D, DType.BF16, gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, torch.from_numpy(lens_np).to(DEV), L,
+                        cache_dtype=DType.BF16, io_dtype=DType.BF16)
+
+
+# ---------------------------------------------------------------------------
+# KV_OFFSETS
+
+def offsets_table(rng, S, mbps, nb, secondary_frac=0.4):
+    raw = rng.integers(0, nb + 2, size=(S, 1, 2, mbps)).astype(np.uint32)
+    raw |= (rng.random(raw.shape) < secondary_frac).astype(np.uint32) << 31
+    return torch.from_numpy(raw.view(np.int32)).to(DEV)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_kv_offsets_random(seed):
+    rng = np.random.default_rng(4000 + seed)
+    gen = torch.Generator().manual_seed(seed)
+    dt = DTYPES[seed % 4]
+    es = TORCH_DT[dt].itemsize
+    kl, vl = LAYOUTS[seed % 3], LAYOUTS[(seed // 3) % 3]
+    H = int(rng.choice([1, 2, 8]))
+    D = int(rng.choice([8, 64, 128]))
+    bs = int(rng.choice([1, 4, 16, 32]))
+    nb = int(rng.integers(2, 40))
+    pitch_pad = [0, 16, es, 256][seed % 4]
+    pool = OffsetsPool(kl, vl, dt, nb, bs, H, D, pitch_pad=pitch_pad,
+                       secondary=seed % 3 != 0, gen=gen)
+    S, L = int(rng.integers(1, 7)), int(rng.integers(1, 300))
+    mbps = int(rng.integers(1, (L + bs - 1) // bs + 2))
+    offsets = offsets_table(rng, S, mbps, nb)
+    lens = lens_tensor(rng, S, L, [np.int32, np.int64][seed % 2])
+    ko, vo = out_pair(S, L, H, D, dt, gen, misalign=seed % 5 == 4)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("io", [DType.BF16, DType.F16, DType.F32])
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_kv_offsets_fp8_dequant(io, layout):
+    rng = np.random.default_rng(43)
+    gen = torch.Generator().manual_seed(43)
+    H, D, bs, nb, S, L = 4, 128, 16, 24, 5, 90
+    pool = OffsetsPool(layout, layout, DType.F8_E4M3, nb, bs, H, D, pitch_pad=64, gen=gen)
+    offsets = offsets_table(rng, S, (L + bs - 1) // bs, nb)
+    lens = lens_tensor(rng, S, L, np.int32)
+    ko, vo = out_pair(S, L, H, D, io, gen)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=DType.F8_E4M3,
+                         io_dtype=io, k_scale=0.0172, v_scale=3.5)
+
+
+@pytest.mark.parametrize("dt,H", [(DType.F32, 16), (DType.BF16, 32)])
+def test_kv_offsets_wide_rows(dt, H):
+    rng = np.random.default_rng(6)
+    gen = torch.Generator().manual_seed(6)
+    D, bs, nb, S, L = 128, 16, 12, 3, 70
+    pool = OffsetsPool(HND, HND, dt, nb, bs, H, D, gen=gen)
+    offsets = offsets_table(rng, S, (L + bs - 1) // bs, nb)
+    lens = lens_tensor(rng, S, L, np.int32)
+    ko, vo = out_pair(S, L, H, D, dt, gen)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F16, DType.F32])
+def test_kv_offsets_abi_entry(dt):
+    """kvx_gather_kv (kvx_abi.h) executes KV_OFFSETS tables: the pool is
+    device memory, the cache tensors carry the canonical block layout."""
+    rng = np.random.default_rng(10)
+    gen = torch.Generator().manual_seed(10)
+    H, D, bs, nb, S, L = 8, 128, 16, 32, 4, 64
+    for layout in LAYOUTS:
+        pool = OffsetsPool(layout, layout, dt, nb, bs, H, D, gen=gen)
+        offsets = offsets_table(rng, S, (L + bs - 1) // bs, nb)
+        lens = lens_tensor(rng, S, L, np.int32)
+        ko, vo = out_pair(S, L, H, D, dt, gen)
+        check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=dt,
+                             entry="abi")
+
+
+def test_kv_offsets_trtllm_pairs():
+    """TensorRT-LLM's pairing: the V block of a K block is the next pool
+    block; all tokens of every sequence valid, no secondary pool."""
+    gen = torch.Generator().manual_seed(12)
+    H, D, bs, S, L = 8, 128, 32, 16, 512
+    mbps = L // bs
+    nb = 2 * S * mbps
+    pool = OffsetsPool(HND, HND, DType.BF16, nb, bs, H, D, secondary=False, gen=gen)
+    k = torch.arange(0, nb, 2, dtype=torch.int32).reshape(S, 1, mbps)
+    offsets = torch.stack([k, k + 1], dim=2).to(DEV)          # [S, 1, 2, M]
+    lens = torch.full((S,), L, dtype=torch.int32, device=DEV)
+    ko, vo = out_pair(S, L, H, D, DType.BF16, gen)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=DType.BF16,
+                         io_dtype=DType.BF16)
+
+
+def test_ragged_malformed_indptr_stays_in_bounds():
+    """indptr that decreases or points past the indices array: rows whose
+    token index falls outside [0, indices_count) are skipped, the rest
+    gathered, nothing read out of bounds."""
+    gen = torch.Generator().manual_seed(13)
+    H, D, bs, nb, L = 2, 64, 4, 8, 12
+    pc, kb, vb = make_cache(NHD, NHD, DType.BF16, nb, bs, H, D, gen=gen)
+    indices = torch.arange(20, dtype=torch.int32, device=DEV) % nb
+    indptr = torch.tensor([0, 10, 6, 18, 40, -3], dtype=torch.int64, device=DEV)
+    lens = torch.full((5,), L, dtype=torch.int32, device=DEV)
+    ko, vo = out_pair(5, L, H, D, DType.BF16, gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, paged.RaggedTable(indices, indptr), lens, L,
+                        cache_dtype=DType.BF16, io_dtype=DType.BF16)

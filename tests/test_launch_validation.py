@@ -222,8 +222,10 @@ def test_gather_single_faults(kvx_lib):
     case(INV, lambda c, g: setattr(g.block_table, "size", 4))                 # :777
     case(INV, lambda c, g: setattr(g.seq_lens, "size", 4))                    # :778
     case(UNS, lambda c, g: setattr(g.io.key, "dtype", DType.F32))             # :784
-    case(UNS, lambda c, g: setattr(g.block_table, "format", TableFormat.RAGGED))  # :788
-    case(UNS, lambda c, g: setattr(g.block_table, "format", TableFormat.KV_OFFSETS))
+    # :788 rejects every non-PACKED format; this build also gathers RAGGED and
+    # KV_OFFSETS (tested below), so unknown formats keep the reference code
+    case(UNS, lambda c, g: setattr(g.block_table, "format", TableFormat.INVALID))
+    case(UNS, lambda c, g: setattr(g.block_table, "format", 7))
     case(INV, lambda c, g: setattr(g.io, "num_kv_heads", 1))                  # :791
     case(INV, lambda c, g: setattr(g.seq_lens, "seq_count", 1))               # :795
     case(INV, lambda c, g: g.io.key.shape.__setitem__(1, 7))                  # :302
@@ -247,7 +249,7 @@ def test_gather_single_faults(kvx_lib):
 def test_gather_check_order_and_empty(kvx_lib):
     # format (UNSUPPORTED) before heads (INVALID): :788 before :791
     c, g = base_gather()
-    g.block_table.format = TableFormat.RAGGED
+    g.block_table.format = TableFormat.INVALID
     g.io.num_kv_heads = 5
     assert G(kvx_lib, c, g) == UNS
     # total == 0 (max_seq_len 0) is OK before the index dtype check
@@ -281,7 +283,7 @@ def test_dequant_gather_validation(kvx_lib):
     bad = abi.scale_desc(None)
     assert call(c, g, k=bad) == INV
     c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.BF16)
-    g.block_table.format = TableFormat.RAGGED
+    g.block_table.format = 9
     assert call(c, g) == UNS
 
 
@@ -295,3 +297,72 @@ def test_gather_safety_checks_added_by_this_build(kvx_lib):
     c, g = base_gather()
     g.io.value.data = None
     assert G(kvx_lib, c, g) == INV
+
+
+# ---------------------------------------------------------------------------
+# RAGGED / KV_OFFSETS gather (this build's extension; KVX_SPEC.md:99-122).
+# Their checks follow the reference's index-dtype check, so every earlier
+# fault keeps the reference code.
+
+def ragged_gather(**kw):
+    c, g = base_gather(**kw)
+    g.block_table.format = TableFormat.RAGGED
+    g.block_table.indptr = FAKE
+    g.block_table.indptr_dtype = DType.S32
+    g.block_table.indptr_count = g.block_table.seq_count + 1
+    return c, g
+
+
+def offsets_gather(**kw):
+    c, g = base_gather(**kw)
+    t = g.block_table
+    t.format = TableFormat.KV_OFFSETS
+    t.flags = abi.TABLE_FLAG_KVCACHEINDEX
+    t.indices_count = t.seq_count * 2 * t.max_blocks_per_seq
+    c.pool.primary = FAKE
+    c.pool.bytes_per_block = 4096
+    return c, g
+
+
+def test_ragged_validation(kvx_lib):
+    c, g = ragged_gather(L=0)
+    assert G(kvx_lib, c, g) == OK                       # empty output: no launch
+    for mutate in (lambda g: setattr(g.block_table, "indptr_dtype", DType.U32),
+                   lambda g: setattr(g.block_table, "indptr", None),
+                   lambda g: setattr(g.block_table, "indptr_count", 2),
+                   lambda g: setattr(g.block_table, "index_dtype", DType.S64),
+                   lambda g: setattr(g.block_table, "indices", None)):
+        c, g = ragged_gather()
+        mutate(g)
+        assert G(kvx_lib, c, g) == INV
+    c, g = ragged_gather()
+    g.io.key.dtype = DType.F32                          # earlier reference check wins
+    g.block_table.indptr = None
+    assert G(kvx_lib, c, g) == UNS
+
+
+def test_kv_offsets_validation(kvx_lib):
+    c, g = offsets_gather(L=0)
+    assert G(kvx_lib, c, g) == OK
+    cases = [
+        (INV, lambda c, g: setattr(g.block_table, "index_dtype", DType.S64)),
+        (INV, lambda c, g: setattr(g.block_table, "flags", 0)),
+        (INV, lambda c, g: setattr(g.block_table, "beam_width", 0)),
+        (UNS, lambda c, g: (setattr(g.block_table, "beam_width", 2),
+                            setattr(g.block_table, "indices_count", g.block_table.indices_count * 2))),
+        (INV, lambda c, g: setattr(c, "block_size", 6)),
+        (INV, lambda c, g: setattr(c.pool, "primary", None)),
+        (INV, lambda c, g: setattr(c.pool, "bytes_per_block", 0)),
+        (INV, lambda c, g: setattr(c.pool, "bytes_per_block", 127)),   # block is 128 B
+        (INV, lambda c, g: c.k.stride.__setitem__(1, -c.k.stride[1])),
+        (INV, lambda c, g: setattr(g.block_table, "indices_count", 3)),
+        (INV, lambda c, g: setattr(g.block_table, "indices", None)),
+    ]
+    for expect, mutate in cases:
+        c, g = offsets_gather()
+        mutate(c, g)
+        assert G(kvx_lib, c, g) == expect
+    # S64 seq_lens are accepted with S32 offsets; the pool replaces cache data
+    c, g = offsets_gather(L=0, lens=DType.S64)
+    c.k.data = c.v.data = None
+    assert G(kvx_lib, c, g) == OK
