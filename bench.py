@@ -51,6 +51,9 @@ def parse_args():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--table", default="packed", choices=["packed", "ragged", "kv_offsets"],
+                   help="block-table format of the gather (c1, c2, c4, c5); kv_offsets "
+                        "puts K and V blocks in one TensorRT-LLM-style pool")
     p.add_argument("--layers", type=int, default=None,
                    help="override the layer count of c1/c2/c4")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -92,7 +95,7 @@ class Launch:
             raise RuntimeError(f"{self.kind} launch returned status {st}")
 
 
-def build_config(name: str, layers_override, dev):
+def build_config(name: str, layers_override, dev, table_fmt="packed"):
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -104,15 +107,28 @@ def build_config(name: str, layers_override, dev):
     w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
 
+    if table_fmt != "packed" and name == "c3":
+        raise SystemExit("c3 has no gather: --table applies to c1, c2, c4, c5")
+
+    def fill(t):
+        if t.dtype == torch.float8_e4m3fn:
+            t.view(torch.uint8).random_(0, 256)
+        else:
+            t.normal_()
+
     def cache_for(wl):
+        """(cache the write uses, cache the gather uses)"""
+        if table_fmt == "kv_offsets":
+            pool, pc = paged.alloc_block_pool(wl.num_blocks, wl.block_size, wl.heads,
+                                              wl.head_dim, tdt[wl.cache_dtype], dev,
+                                              wl.k_layout, wl.pack)
+            fill(pool.key_cache)
+            return pc, pool
         pc = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
                                tdt[wl.cache_dtype], dev, wl.k_layout, wl.v_layout, wl.pack)
         for t in (pc.key_cache, pc.value_cache):
-            if t.dtype == torch.float8_e4m3fn:
-                t.view(torch.uint8).random_(0, 256)
-            else:
-                t.normal_()
-        return pc
+            fill(t)
+        return pc, pc
 
     def rows(wl, sigma=1.0):
         x = torch.empty((wl.num_tokens, wl.heads, wl.head_dim), dtype=tdt[wl.io_dtype],
@@ -120,10 +136,21 @@ def build_config(name: str, layers_override, dev):
         return x.normal_(0.0, sigma)
 
     slots = torch.tensor(w.slots, device=dev)
-    table = torch.tensor(w.block_table, device=dev)
     lens = torch.tensor(w.seq_lens, device=dev)
-    keep += [slots, table, lens]
-    wbytes, gbytes = W.write_bytes(w), W.gather_bytes(w)
+    if table_fmt == "ragged":
+        indices, indptr = W.ragged_table(w)
+        table = paged.RaggedTable(torch.tensor(indices, device=dev),
+                                  torch.tensor(indptr, device=dev))
+        keep += [table.indices, table.indptr]
+    elif table_fmt == "kv_offsets":
+        offsets = torch.tensor(W.kv_offsets_table(w), device=dev)
+        table = None  # one OffsetsTable per pool, built in gather_launch
+        keep.append(offsets)
+    else:
+        table = torch.tensor(w.block_table, device=dev)
+        keep.append(table)
+    keep += [slots, lens]
+    wbytes, gbytes = W.write_bytes(w), W.gather_bytes(w, table_fmt)
     wtok, gtok = w.valid_write_tokens(), w.gathered_tokens()
     steps = []  # list of per-step launch lists (rotated by step index)
 
@@ -138,9 +165,10 @@ def build_config(name: str, layers_override, dev):
                       wbytes, wtok)
 
     def gather_launch(pc, ko, vo, ks=None, vs=None):
-        cd = pc.desc()
-        gd = paged.build_gather(ko, vo, table, lens, w.max_seq_len)
-        keep.extend([cd, gd])
+        tb = paged.pool_table(pc, offsets) if table_fmt == "kv_offsets" else table
+        cd = paged.gather_cache_desc(pc, tb)
+        gd = paged.build_gather(ko, vo, tb, lens, w.max_seq_len)
+        keep.extend([cd, gd, tb])
         if ks is not None:
             ksd, vsd = abi.scale_desc(ks.data_ptr()), abi.scale_desc(vs.data_ptr())
             keep.extend([ksd, vsd])
@@ -169,28 +197,30 @@ def build_config(name: str, layers_override, dev):
             keep += [ks, vs]
         step = []
         for _ in range(layers):
-            pc = cache_for(w)
+            pc, gc = cache_for(w)
             sigma = w.notes.get("io_sigma", 1.0)
             step.append(write_launch(pc, rows(w, sigma), rows(w, sigma), ks, vs))
-            step.append(gather_launch(pc, ko, vo, ks, vs))
+            step.append(gather_launch(gc, ko, vo, ks, vs))
         steps.append(step)
         cfg = {"layers": layers}
     elif name == "c3":
         # four rotating buffer sets (> the 256 MB Infinity Cache)
         for _ in range(4):
-            pc = cache_for(w)
+            pc, _ = cache_for(w)
             steps.append([write_launch(pc, rows(w), rows(w))])
         cfg = {"buffer_sets": 4}
     else:  # c5
-        pc = cache_for(w)
+        pc, gc = cache_for(w)
         ko = torch.empty((w.seq_count, w.max_seq_len, w.heads, w.head_dim),
                          dtype=torch.bfloat16, device=dev)
         vo = torch.empty_like(ko)
         keep += [ko, vo]
-        steps.append([write_launch(pc, rows(w), rows(w)), gather_launch(pc, ko, vo)])
+        steps.append([write_launch(pc, rows(w), rows(w)), gather_launch(gc, ko, vo)])
         cfg = {"layers": 1}
     torch.cuda.synchronize()
-    cfg.update({"workload": w.name, "seed": w.seed, "heads": w.heads,
+    if table_fmt != "packed":
+        w.name = f"{w.name}_{table_fmt}"
+    cfg.update({"workload": w.name, "table": table_fmt, "seed": w.seed, "heads": w.heads,
                 "head_dim": w.head_dim, "block_size": w.block_size,
                 "num_tokens": w.num_tokens, "seq_count": w.seq_count,
                 "max_seq_len": w.max_seq_len, "pool_blocks": w.num_blocks,
@@ -310,7 +340,7 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
-    w, steps, cfg, keep = build_config(args.config, args.layers, dev)
+    w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table)
     stream = torch.cuda.Stream(device=dev)
     sh = stream.cuda_stream
 
@@ -376,6 +406,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline and not args.profile_only:
         cpu = cpu_baseline(w, args.cpu_seconds)
+        if cpu is not None and args.table != "packed":
+            cpu["sample"] += ("; the oracle's fast path reads the PACKED form of this "
+                              "workload's table (same rows and bytes)")
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,

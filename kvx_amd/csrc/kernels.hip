@@ -48,7 +48,22 @@ constexpr int kMaxChunksPerLane = 4;
 #ifndef KVX_GATHER_TILE_BYTES
 #define KVX_GATHER_TILE_BYTES 4096
 #endif
+// Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
+// together (the table load and the data load of each are dependent).
+#ifndef KVX_INDEXED_UNROLL
+#define KVX_INDEXED_UNROLL 4
+#endif
+// KV_OFFSETS row-dense gather: table entries of the dequantizing gather are
+// loaded once per workgroup tile (1) or by every chunk (0).  The copy gather
+// always loads them per chunk: on MI355X that measures 5% faster for bf16,
+// while per-chunk loads cost the dequantizing gather (8-byte source chunks,
+// twice the table loads per byte) 15%.
+#ifndef KVX_OFFSETS_TILE
+#define KVX_OFFSETS_TILE 1
+#endif
+constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
+constexpr int kIndexedUnroll = KVX_INDEXED_UNROLL;
 constexpr bool kGatherNtLoad = KVX_GATHER_NT_LOAD != 0;
 constexpr bool kGatherNtStore = KVX_GATHER_NT_STORE != 0;
 
@@ -298,6 +313,17 @@ __device__ __forceinline__ int64_t load_index(const void *base, int64_t i,
                                               int32_t is64) {
   return is64 ? reinterpret_cast<const int64_t *>(base)[i]
               : (int64_t)reinterpret_cast<const int32_t *>(base)[i];
+}
+
+// Value i of an int32 (I64 = false) or int64 index array.  Gather kernels
+// take the dtype as a template parameter: with a runtime dtype every load
+// sits behind its own branch and the loads complete one after another; with
+// a fixed one, independent loads (seq_len, block id, indptr) are issued
+// together.
+template <bool I64>
+__device__ __forceinline__ int64_t load_idx(const void *base, int64_t i) {
+  if constexpr (I64) return reinterpret_cast<const int64_t *>(base)[i];
+  return (int64_t)reinterpret_cast<const int32_t *>(base)[i];
 }
 
 // Byte offset, relative to the (block, offset) base, of the chunk that
@@ -642,6 +668,8 @@ struct GatherArgs {
   int32_t flat;  // cache rows of a block are contiguous for K and V
   int32_t split_log2;  // flat only: workgroups per block = 1 << split_log2
   int32_t format;      // kvx_block_table_format_t
+  int32_t nchunks_log2;  // indexed flat: nchunks is a power of two
+  int32_t bs_log2;       // log2(block_size), or -1 when not a power of two
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -658,18 +686,18 @@ struct BlockJob {
   float vs;
 };
 
-template <class Op>
+template <class Op, bool I64>
 __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
-  const int64_t wg = blockIdx.x;
-  const int64_t s = wg / a.blocks_per_seq;
-  const int32_t lb = (int32_t)(wg - s * a.blocks_per_seq);
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int32_t lb = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
   if (lb >= a.max_blocks_per_seq) return false;
-  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int64_t t0 = (int64_t)lb * a.block_size;
   if (t0 >= n) return false;
-  const int64_t bid =
-      load_index(a.table, s * a.max_blocks_per_seq + lb, a.index_is64);
   if (bid < 0 || bid >= a.num_blocks) return false;
   const int64_t rem = n - t0;
   j.rows = rem < a.block_size ? (int32_t)rem : a.block_size;
@@ -722,17 +750,18 @@ __device__ __forceinline__ void flat_copy(const char *ck, const char *cv, char *
   }
 }
 
-template <class Op>
+template <class Op, bool I64>
 __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a) {
-  const int64_t wg = blockIdx.x;
-  const int64_t s = wg / a.blocks_per_seq;
-  const int32_t w = (int32_t)(wg - s * a.blocks_per_seq);
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
   const int32_t lb = w >> a.split_log2;
   const int32_t part = w & ((1 << a.split_log2) - 1);
   if (lb >= a.max_blocks_per_seq) return;
   // seq_len and the block id do not depend on each other: load both at once.
-  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
-  const int64_t bid = load_index(a.table, s * a.max_blocks_per_seq + lb, a.index_is64);
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int32_t rows_per_part = a.block_size >> a.split_log2;
   const int64_t t0 = (int64_t)lb * a.block_size + (int64_t)part * rows_per_part;
@@ -754,10 +783,10 @@ __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a
 
 // Any other layout: rows go to (wave, lane group), each lane keeps the
 // cache offsets of its chunks in registers.
-template <class Op>
+template <class Op, bool I64>
 __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a) {
   BlockJob j;
-  if (!gather_job<Op>(a, j)) return;
+  if (!gather_job<Op, I64>(a, j)) return;
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
   const int lpt = 1 << a.lpt_log2;
@@ -827,26 +856,15 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
 //               index * bytes_per_block, offset t % block_size.  K and V rows
 //               are resolved independently.
 // Rows t >= min(seq_len, max_seq_len) are untouched, as in the PACKED gather.
-template <class Op, int FMT>
+template <class Op, int FMT, bool I64, bool P64>
 __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArgs a) {
-  const int64_t wg = blockIdx.x;
-  const int64_t s = wg / a.blocks_per_seq;
-  const int64_t t0 = (wg - s * a.blocks_per_seq) * (int64_t)a.rows_per_wg;
-  const int64_t seq_len = load_index(a.seq_lens, s, a.lens_is64);
-  int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
-  int64_t start = 0;
-  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
-    start = load_index(a.indptr, s, a.indptr_is64);
-    if (start < 0) return;
-    int64_t cnt = load_index(a.indptr, s + 1, a.indptr_is64) - start;
-    const int64_t left = a.table_count - start;  // entries the table holds
-    cnt = left < cnt ? left : cnt;
-    n = cnt < n ? cnt : n;
-  } else {
-    const int64_t cap = (int64_t)a.max_blocks_per_seq * a.block_size;
-    n = cap < n ? cap : n;
-  }
-  if (t0 >= n) return;
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
+  int64_t n;
+  int64_t start;
+  if (!indexed_extent<FMT, I64, P64>(a, s, t0, n, start)) return;
 
   float ks = 1.0f;
   float vs = 1.0f;
@@ -881,7 +899,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
     const char *rk = nullptr;
     const char *rv = nullptr;
     if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
-      const int64_t bid = load_index(a.table, start + t, a.index_is64);
+      const int64_t bid = load_idx<I64>(a.table, start + t);
       if (bid >= 0 && bid < a.num_blocks) {
         const int64_t o = t % a.block_size;
         rk = a.src_k + bid * a.gk.s_block + o * a.gk.s_off;
@@ -921,6 +939,170 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
       if (rv != nullptr)
         st<Op::kDst>(wv + (int64_t)c * Op::kDst,
                      Op::apply(ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim)), vs));
+    }
+  }
+}
+
+// Rows of sequence s that exist (t < n) for an indexed-format workgroup,
+// plus RAGGED's first token index; false when the workgroup's rows
+// [t0, ...) are all past the end.  seq_len, the indptr pair and (TILE) the
+// KV_OFFSETS entries ek / ev of K and V at logical block lb are independent
+// loads, issued together.
+template <int FMT, bool I64, bool P64, bool TILE = false>
+__device__ __forceinline__ bool indexed_extent(const GatherArgs &a, int64_t s, int64_t t0,
+                                               int64_t &n, int64_t &start, uint32_t lb = 0,
+                                               uint32_t *ek = nullptr, uint32_t *ev = nullptr) {
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  int64_t end = 0;
+  start = 0;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    start = load_idx<P64>(a.indptr, s);
+    end = load_idx<P64>(a.indptr, s + 1);
+  }
+  if constexpr (TILE) {
+    const int32_t *row =
+        reinterpret_cast<const int32_t *>(a.table) + s * 2 * (int64_t)a.max_blocks_per_seq;
+    *ek = (uint32_t)row[lb];
+    *ev = (uint32_t)row[a.max_blocks_per_seq + lb];
+    // consumed here, so the loads are not sunk below the length test
+    asm volatile("" ::"s"(*ek), "s"(*ev));
+  }
+  // Keep the loads above ahead of their uses, so that they are in flight
+  // together.
+  __builtin_amdgcn_sched_barrier(0);
+  n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    int64_t cnt = end - start;
+    const int64_t left = a.table_count - start;  // entries the table holds
+    cnt = left < cnt ? left : cnt;
+    n = cnt < n ? cnt : n;
+    if (start < 0) n = 0;
+  } else {
+    const int64_t cap = (int64_t)a.max_blocks_per_seq * a.block_size;
+    n = cap < n ? cap : n;
+  }
+  return t0 < n;
+}
+
+// Cache address of row t (sequence s) of K (v = false) or V, or nullptr
+// when the table skips it.  The in-block offset of the row is o * s_off.
+template <int FMT, bool I64>
+__device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, int64_t s,
+                                                   int64_t start, int64_t t) {
+  const uint32_t tu = (uint32_t)t;  // t < max_seq_len < 2^31
+  uint32_t lb;
+  uint32_t o;
+  if (a.bs_log2 >= 0) {
+    lb = tu >> a.bs_log2;
+    o = tu & ((1u << a.bs_log2) - 1u);
+  } else {
+    lb = tu / (uint32_t)a.block_size;
+    o = tu - lb * (uint32_t)a.block_size;
+  }
+  const GeomBytes &g = v ? a.gv : a.gk;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    const int64_t bid = load_idx<I64>(a.table, start + t);
+    if (bid < 0 || bid >= a.num_blocks) return nullptr;
+    return (v ? a.src_v : a.src_k) + bid * g.s_block + (int64_t)o * g.s_off;
+  } else {
+    const uint32_t e = (uint32_t)reinterpret_cast<const int32_t *>(
+        a.table)[(s * 2 + (v ? 1 : 0)) * (int64_t)a.max_blocks_per_seq + lb];
+    const char *pool = a.pool[e >> 31];
+    const int64_t idx = e & 0x7FFFFFFFu;
+    if (pool == nullptr || idx >= a.num_blocks) return nullptr;
+    return pool + idx * a.bytes_per_block + (int64_t)o * g.s_off;
+  }
+}
+
+// RAGGED / KV_OFFSETS gather when every cache row is H * D contiguous
+// elements (NHD with dense heads, any block / offset strides): the
+// workgroup's rows x chunks of K, then of V, are spread over all threads as
+// in gather_flat_kernel, and each thread resolves the source row of its own
+// chunk (threads of one row load the same table entry).
+template <class Op, int FMT, bool I64, bool P64>
+__global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(GatherArgs a) {
+  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled;
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
+  // KV_OFFSETS tiles lie inside one block (rows_per_wg divides block_size).
+  // kTile: the tile's K and V table entries are two scalar loads, issued with
+  // the seq_len load; otherwise every chunk loads its own entry.
+  uint32_t ek = 0;
+  uint32_t ev = 0;
+  uint32_t lb = 0;
+  if constexpr (kTile) {
+    lb = (uint32_t)t0 >> a.bs_log2;
+    if (lb >= (uint32_t)a.max_blocks_per_seq) return;
+  }
+  int64_t n;
+  int64_t start;
+  if (!indexed_extent<FMT, I64, P64, kTile>(a, s, t0, n, start, lb, &ek, &ev)) return;
+  const char *tk = nullptr;
+  const char *tv = nullptr;
+  if constexpr (kTile) {
+    const int64_t o0 = t0 & ((1 << a.bs_log2) - 1);
+    const char *pk = (ek >> 31) ? a.pool[1] : a.pool[0];
+    const char *pv = (ev >> 31) ? a.pool[1] : a.pool[0];
+    const int64_t kb = ek & 0x7FFFFFFFu;
+    const int64_t vb = ev & 0x7FFFFFFFu;
+    if (pk != nullptr && kb < a.num_blocks) tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
+    if (pv != nullptr && vb < a.num_blocks) tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
+    if (tk == nullptr && tv == nullptr) return;
+  }
+  const int64_t rem = n - t0;
+  const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;
+  float ks = 1.0f;
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = *a.k_scale;
+    vs = *a.v_scale;
+  }
+  const uint32_t total = (uint32_t)rows << a.nchunks_log2;
+  const uint32_t both = 2 * total;
+  const uint32_t cmask = (1u << a.nchunks_log2) - 1u;
+  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
+  // Chunk f: K for f < total, V above; row r = index >> nchunks_log2.  Each
+  // pass resolves kIndexedUnroll chunks' rows, then loads them all, then
+  // stores them, so the table and data latencies overlap across chunks.
+  for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * kBlockThreads) {
+    const char *src[kIndexedUnroll];
+    char *dst[kIndexedUnroll];
+    bool isv[kIndexedUnroll];
+#pragma unroll
+    for (int u = 0; u < kIndexedUnroll; ++u) {
+      const uint32_t f = base + u * kBlockThreads;
+      src[u] = nullptr;
+      dst[u] = nullptr;
+      isv[u] = f >= total;
+      if (f < both) {
+        const uint32_t gi = f - (isv[u] ? total : 0u);
+        const uint32_t r = gi >> a.nchunks_log2;
+        const uint32_t c = gi & cmask;
+        if constexpr (kTile) {
+          const char *base = isv[u] ? tv : tk;
+          src[u] = base == nullptr ? nullptr
+                                   : base + (int64_t)r * (isv[u] ? a.gv.s_off : a.gk.s_off);
+        } else {
+          src[u] = indexed_row<FMT, I64>(a, isv[u], s, start, t0 + r);
+        }
+        if (src[u] != nullptr) {
+          src[u] += (int64_t)c * Op::kSrc;
+          dst[u] = (isv[u] ? a.dst_v : a.dst_k) + out0 + (int64_t)r * a.out_row_bytes +
+                   (int64_t)c * Op::kDst;
+        }
+      }
+    }
+    Raw<Op::kSrc> x[kIndexedUnroll];
+#pragma unroll
+    for (int u = 0; u < kIndexedUnroll; ++u) {
+      if (src[u] != nullptr) x[u] = ld<Op::kSrc, kGatherNtLoad>(src[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kIndexedUnroll; ++u) {
+      if (src[u] != nullptr)
+        st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], isv[u] ? vs : ks));
     }
   }
 }
@@ -1002,20 +1184,48 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   }
 }
 
+// I64: dtype of seq_lens (and of PACKED / RAGGED block ids, which share it);
+// P64: dtype of RAGGED's indptr.
+template <class Op, bool I64, bool P64>
+void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
+  const dim3 g((uint32_t)grid);
+  const dim3 b(kBlockThreads);
+  if (a.format == KVX_BLOCK_TABLE_RAGGED) {
+    if (a.flat) {
+      hipLaunchKernelGGL((gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g,
+                         b, 0, s, a);
+    } else {
+      hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g, b, 0,
+                         s, a);
+    }
+  } else if constexpr (!P64) {
+    if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+      if (a.flat) {
+        hipLaunchKernelGGL(
+            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>), g, b, 0,
+            s, a);
+      } else {
+        hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>),
+                           g, b, 0, s, a);
+      }
+    } else if (a.flat) {
+      hipLaunchKernelGGL((gather_flat_kernel<Op, I64>), g, b, 0, s, a);
+    } else {
+      hipLaunchKernelGGL((gather_rows_kernel<Op, I64>), g, b, 0, s, a);
+    }
+  }
+}
+
 template <class Op>
 void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
-  if (a.format == KVX_BLOCK_TABLE_RAGGED) {
-    hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_RAGGED>), dim3((uint32_t)grid),
-                       dim3(kBlockThreads), 0, s, a);
-  } else if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
-    hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS>),
-                       dim3((uint32_t)grid), dim3(kBlockThreads), 0, s, a);
-  } else if (a.flat) {
-    hipLaunchKernelGGL(gather_flat_kernel<Op>, dim3((uint32_t)grid),
-                       dim3(kBlockThreads), 0, s, a);
+  const bool i64 = a.lens_is64 != 0;  // equals index_is64 for PACKED / RAGGED
+  const bool p64 = a.format == KVX_BLOCK_TABLE_RAGGED && a.indptr_is64 != 0;
+  if (i64) {
+    if (p64) launch_gather_typed<Op, true, true>(a, grid, s);
+    else launch_gather_typed<Op, true, false>(a, grid, s);
   } else {
-    hipLaunchKernelGGL(gather_rows_kernel<Op>, dim3((uint32_t)grid),
-                       dim3(kBlockThreads), 0, s, a);
+    if (p64) launch_gather_typed<Op, false, true>(a, grid, s);
+    else launch_gather_typed<Op, false, false>(a, grid, s);
   }
 }
 
@@ -1213,14 +1423,28 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
+  a.nchunks_log2 = log2_exact(a.nchunks);
+  a.bs_log2 = log2_exact(p.block_size);
   if (p.format != KVX_BLOCK_TABLE_PACKED) {
-    // indexed formats: tiles of rows, about 4 KiB of each tensor's cache rows,
-    // at least one full pass of the workgroup's row groups
-    const int64_t per_pass = (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
+    // indexed formats: tiles of rows, about TILE_BYTES of each tensor's cache
+    // rows.  Rows that are H*D contiguous elements (any row stride) and a
+    // power-of-two chunk count take the flat kernel; otherwise the row
+    // kernel, with at least one full pass of its row groups.
+    auto row_dense = [&](const Geom &g) {
+      return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
+    };
+    a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
     int64_t rows = KVX_GATHER_TILE_BYTES / (row_elems * cs);
+    const int64_t per_pass = a.flat ? 1 : (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
     rows = rows < per_pass ? per_pass : rows;
+    if (a.flat && p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+      // a power of two no larger than the (power-of-two) block: tiles never
+      // straddle blocks
+      int64_t r2 = 1;
+      while (r2 * 2 <= rows && r2 * 2 <= p.block_size) r2 *= 2;
+      rows = r2;
+    }
     a.rows_per_wg = (int32_t)rows;
-    a.flat = 0;
     a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
   } else if (a.flat) {
     // split a block into power-of-two row ranges of about TILE_BYTES per tensor

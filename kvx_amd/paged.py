@@ -103,6 +103,31 @@ def alloc_cache(num_blocks: int, block_size: int, heads: int, head_dim: int,
                       heads, head_dim)
 
 
+def alloc_block_pool(num_blocks: int, block_size: int, heads: int, head_dim: int,
+                     dtype: torch.dtype, device, layout=Layout.BLOCK_NHD,
+                     pack: int = 8) -> tuple[PagedCache, PagedCache]:
+    """One pool of 2 * num_blocks single-tensor blocks in TensorRT-LLM's
+    KVBlockArray pairing: the K block of logical block b is pool block 2b, its
+    V block is 2b + 1.  Returns (pool, kv): `pool` describes all pool blocks
+    (the cache for KV_OFFSETS gathers, whose OffsetsTable is
+    ``pool_table``); `kv` views the same memory as K and V caches of
+    num_blocks blocks for PACKED-table writes and gathers."""
+    shape = cache_shape(layout, 2 * num_blocks, block_size, heads, head_dim, pack)
+    mem = torch.empty(shape, dtype=dtype, device=device)
+    layout = Layout(layout)
+    pool = PagedCache(mem, mem, layout, layout, 2 * num_blocks, block_size, heads, head_dim)
+    kv = PagedCache(mem[0::2], mem[1::2], layout, layout, num_blocks, block_size, heads,
+                    head_dim)
+    return pool, kv
+
+
+def pool_table(pool: PagedCache, offsets: torch.Tensor,
+               secondary: torch.Tensor | None = None) -> "OffsetsTable":
+    """OffsetsTable over the memory of `pool` (see alloc_block_pool)."""
+    mem = pool.key_cache
+    return OffsetsTable(offsets, mem, secondary, mem.stride(0) * mem.element_size())
+
+
 def _stream_handle(stream) -> int | None:
     if stream is None:
         return torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
@@ -203,6 +228,20 @@ def _table_desc(table) -> abi.BlockTable:
     return abi.make_block_table_packed(S, mbps, dtype_code(table), table.data_ptr())
 
 
+def gather_cache_desc(cache: PagedCache, block_table) -> abi.CacheDesc:
+    """The cache descriptor of a gather; an OffsetsTable also fills its pool
+    fields (kvx_pool_desc_t)."""
+    cd = cache.desc()
+    if isinstance(block_table, OffsetsTable):
+        cd.pool.size = C.sizeof(abi.PoolDesc)
+        cd.pool.memory = int(memory_of(block_table.primary))
+        cd.pool.bytes_per_block = block_table.bytes_per_block
+        cd.pool.primary = block_table.primary.data_ptr()
+        cd.pool.secondary = (None if block_table.secondary is None
+                             else block_table.secondary.data_ptr())
+    return cd
+
+
 def build_gather(key_out: torch.Tensor, value_out: torch.Tensor,
                  block_table, seq_lens: torch.Tensor,
                  max_seq_len: int) -> abi.GatherDesc:
@@ -254,14 +293,7 @@ def gather_kv(cache: PagedCache, key_out: torch.Tensor, value_out: torch.Tensor,
     With k_scale/v_scale the FP8 cache is dequantized
     (kvx_launch_gather_kv_dequant)."""
     lib = abi.load()
-    cd = cache.desc()
-    if isinstance(block_table, OffsetsTable):
-        cd.pool.size = C.sizeof(abi.PoolDesc)
-        cd.pool.memory = int(memory_of(block_table.primary))
-        cd.pool.bytes_per_block = block_table.bytes_per_block
-        cd.pool.primary = block_table.primary.data_ptr()
-        cd.pool.secondary = (None if block_table.secondary is None
-                             else block_table.secondary.data_ptr())
+    cd = gather_cache_desc(cache, block_table)
     gd = build_gather(key_out, value_out, block_table, seq_lens, max_seq_len)
     s = _stream_handle(stream)
     if entry == "abi":

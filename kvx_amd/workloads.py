@@ -92,18 +92,58 @@ def write_bytes(w: Workload) -> int:
     return int(b)
 
 
-def gather_bytes(w: Workload) -> int:
-    """Algorithmic bytes of one gather: gathered rows of K and V read from the
-    cache and written out, plus the block-table entries used and seq_lens."""
-    e = w.row_elems
+TABLE_FORMATS = ("packed", "ragged", "kv_offsets")
+
+
+def _gathered_per_seq(w: Workload) -> np.ndarray:
     n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
-    n = np.minimum(n, w.max_blocks_per_seq * w.block_size)
+    return np.minimum(n, w.max_blocks_per_seq * w.block_size)
+
+
+def gather_bytes(w: Workload, table: str = "packed") -> int:
+    """Algorithmic bytes of one gather: gathered rows of K and V read from the
+    cache and written out, plus the index entries used and seq_lens.  Index
+    entries per format: PACKED one per used block; RAGGED one per gathered
+    token plus indptr (S + 1 entries); KV_OFFSETS two int32 (K and V) per
+    used block."""
+    e = w.row_elems
+    n = _gathered_per_seq(w)
     blocks = (n + w.block_size - 1) // w.block_size
     b = int(n.sum()) * 2 * e * (dtype_bytes(w.cache_dtype) + dtype_bytes(w.io_dtype))
-    b += int(blocks.sum()) * w.block_table.itemsize + w.seq_count * w.seq_lens.itemsize
+    if table == "packed":
+        b += int(blocks.sum()) * w.block_table.itemsize
+    elif table == "ragged":
+        b += int(n.sum()) * w.block_table.itemsize + (w.seq_count + 1) * 4
+    elif table == "kv_offsets":
+        b += int(blocks.sum()) * 2 * 4
+    else:
+        raise ValueError(table)
+    b += w.seq_count * w.seq_lens.itemsize
     if w.cache_dtype != w.io_dtype:
         b += 8
     return int(b)
+
+
+def ragged_table(w: Workload) -> tuple[np.ndarray, np.ndarray]:
+    """The workload's block table as a RAGGED table (KVX_SPEC.md:107-114):
+    one block id per gathered token, int32, and int32 indptr prefix sums."""
+    n = _gathered_per_seq(w)
+    parts = [w.block_table[s, np.arange(n[s]) // w.block_size] for s in range(w.seq_count)]
+    indices = np.concatenate(parts).astype(np.int32) if parts else np.zeros(0, np.int32)
+    indptr = np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+    return indices, indptr
+
+
+def kv_offsets_table(w: Workload) -> np.ndarray:
+    """The workload's block table as an int32 KV_OFFSETS table
+    [S, 1, 2, max_blocks_per_seq] over a pool of 2 * num_blocks blocks in
+    TensorRT-LLM's pairing (K of logical block b at pool block 2b, V at
+    2b + 1).  Unused entries (-1) become 0x7FFFFFFF, an index past the pool
+    that the gather skips."""
+    t = w.block_table.astype(np.int64)
+    k = np.where(t < 0, 0x7FFFFFFF, 2 * t)
+    v = np.where(t < 0, 0x7FFFFFFF, 2 * t + 1)
+    return np.stack([k, v], axis=1)[:, None].astype(np.int32)
 
 
 def _slots_for(positions: np.ndarray, table_row: np.ndarray, bs: int) -> np.ndarray:

@@ -247,3 +247,37 @@ def test_ragged_malformed_indptr_stays_in_bounds():
     ko, vo = out_pair(5, L, H, D, DType.BF16, gen)
     check_gather_ragged(pc, kb, vb, ko, vo, paged.RaggedTable(indices, indptr), lens, L,
                         cache_dtype=DType.BF16, io_dtype=DType.BF16)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_block_pool_write_then_offsets_gather(layout):
+    """alloc_block_pool: PACKED writes into the paired K / V views, then a
+    KV_OFFSETS gather over the pool returns what a PACKED gather returns."""
+    from kvx_amd import workloads as W
+
+    w = W.c1_tinyllama()
+    gen = torch.Generator().manual_seed(21)
+    pool, kv = paged.alloc_block_pool(w.num_blocks, w.block_size, w.heads, w.head_dim,
+                                      torch.float16, DEV, layout)
+    random_fill(pool.key_cache, gen)
+    T = w.num_tokens
+    key = random_fill(torch.empty((T, w.heads, w.head_dim), dtype=torch.float16,
+                                  device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(kv, key, val, slots, tokens_per_seq=w.tokens_per_seq) == 0
+    lens = torch.tensor(w.seq_lens, device=DEV)
+    shape = (w.seq_count, w.max_seq_len, w.heads, w.head_dim)
+    pk, pv = torch.zeros(shape, dtype=torch.float16, device=DEV), torch.zeros(
+        shape, dtype=torch.float16, device=DEV)
+    assert paged.gather_kv(kv, pk, pv, torch.tensor(w.block_table, device=DEV), lens,
+                           w.max_seq_len) == 0
+    ok, ov = torch.zeros_like(pk), torch.zeros_like(pv)
+    offs = torch.tensor(W.kv_offsets_table(w), device=DEV)
+    assert paged.gather_kv(pool, ok, ov, paged.pool_table(pool, offs), lens,
+                           w.max_seq_len) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(ok.view(torch.int16), pk.view(torch.int16))
+    assert torch.equal(ov.view(torch.int16), pv.view(torch.int16))
+    # the written rows are the inputs (c1 writes every gathered token)
+    assert torch.equal(pk.view(torch.int16).reshape(T, -1), key.view(torch.int16).reshape(T, -1))

@@ -218,3 +218,39 @@ def test_table_dequant_is_copy_then_dequant():
             assert np.array_equal(dk[mask], oracle.dequantize_e4m3(bk[mask], ks, io))
             assert np.array_equal(dv[mask], oracle.dequantize_e4m3(bv[mask], vs, io))
             assert not dk[~mask].any() and not dv[~mask].any()
+
+
+def test_workload_tables_match_packed():
+    """kvx_amd.workloads' RAGGED and KV_OFFSETS forms of c1's table gather
+    the same rows as the PACKED table (the bench's --table variants)."""
+    from kvx_amd import workloads as W
+
+    w = W.c1_tinyllama()
+    H, D, bs, nb, L = w.heads, w.head_dim, w.block_size, w.num_blocks, w.max_seq_len
+    S = w.seq_count
+    rng = np.random.default_rng(1)
+    shape = cache_shape(Layout.BLOCK_NHD, nb, bs, H, D)
+    kc = _rand_bytes(rng, int(np.prod(shape)) * 2).view(np.uint16)   # f16 bits
+    vc = _rand_bytes(rng, kc.nbytes).view(np.uint16)
+    g = _geom(Layout.BLOCK_NHD, shape, 1)
+    kw = dict(max_seq_len=L, heads=H, head_dim=D, block_size=bs, cache_dtype=DType.F16,
+              io_dtype=DType.F16)
+    pk, pv = np.zeros(S * L * H * D, np.uint16), np.zeros(S * L * H * D, np.uint16)
+    oracle.gather_kv(g, g, kc, vc, pk, pv, w.block_table, w.seq_lens, seq_count=S,
+                     max_blocks_per_seq=w.max_blocks_per_seq, num_blocks=nb, **kw)
+    indices, indptr = W.ragged_table(w)
+    rk, rv = np.zeros_like(pk), np.zeros_like(pv)
+    oracle.gather_kv_ragged(g, g, kc, vc, rk, rv, indices, indptr, w.seq_lens, num_blocks=nb,
+                            **kw)
+    assert np.array_equal(rk, pk) and np.array_equal(rv, pv)
+    # one pool holding K of block b at 2b and V at 2b + 1
+    pool = np.empty((2 * nb,) + shape[1:], np.uint16)
+    pool[0::2], pool[1::2] = kc.reshape(shape), vc.reshape(shape)
+    ok, ov = np.zeros_like(pk), np.zeros_like(pv)
+    oracle.gather_kv_offsets(g, g, pool.view(np.uint8).reshape(-1), None,
+                             int(np.prod(shape[1:])) * 2, ok, ov, W.kv_offsets_table(w),
+                             w.seq_lens, max_blocks_per_seq=w.max_blocks_per_seq,
+                             num_blocks=2 * nb, **kw)
+    assert np.array_equal(ok, pk) and np.array_equal(ov, pv)
+    assert W.gather_bytes(w, "ragged") - W.gather_bytes(w) == \
+        (indices.size - w.block_table.size) * 4 + (S + 1) * 4
