@@ -54,6 +54,10 @@ def parse_args():
     p.add_argument("--table", default="packed", choices=["packed", "ragged", "kv_offsets"],
                    help="block-table format of the gather (c1, c2, c4, c5); kv_offsets "
                         "puts K and V blocks in one TensorRT-LLM-style pool")
+    p.add_argument("--write-entry", default="launch", choices=["launch", "torch_op"],
+                   help="issue the writes through kvx_launch_write_kv* (ctypes) or the "
+                        "PyTorch-ROCm op _C_cache_ops.reshape_and_cache_flash_kvx "
+                        "(c1, c2, c4, c5: NHD caches)")
     p.add_argument("--layers", type=int, default=None,
                    help="override the layer count of c1/c2/c4")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -95,7 +99,7 @@ class Launch:
             raise RuntimeError(f"{self.kind} launch returned status {st}")
 
 
-def build_config(name: str, layers_override, dev, table_fmt="packed"):
+def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch"):
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -109,6 +113,14 @@ def build_config(name: str, layers_override, dev, table_fmt="packed"):
 
     if table_fmt != "packed" and name == "c3":
         raise SystemExit("c3 has no gather: --table applies to c1, c2, c4, c5")
+    if write_entry == "torch_op" and name == "c3":
+        raise SystemExit("the torch op writes vLLM's NHD caches; c3's K is x-packed")
+    op = None
+    if write_entry == "torch_op":
+        from kvx_amd import torch_ops
+
+        torch_ops.load()
+        op = torch.ops._C_cache_ops.reshape_and_cache_flash_kvx
 
     def fill(t):
         if t.dtype == torch.float8_e4m3fn:
@@ -155,6 +167,19 @@ def build_config(name: str, layers_override, dev, table_fmt="packed"):
     steps = []  # list of per-step launch lists (rotated by step index)
 
     def write_launch(pc, key, val, ks=None, vs=None):
+        if op is not None:
+            # the op writes on torch's current stream (the bench stream)
+            one = torch.ones(1, dtype=torch.float32, device=dev)
+            kvd = "fp8" if ks is not None else "auto"
+            args = (key, val, pc.key_cache, pc.value_cache, slots, kvd,
+                    one if ks is None else ks, one if vs is None else vs)
+            keep.extend([pc, key, val, one])
+
+            def call(_stream):
+                op(*args)
+                return 0
+
+            return Launch("write", call, (), wbytes, wtok)
         cd = pc.desc()
         wd = paged.build_write(pc, key, val, slots, ks, vs)
         keep.extend([pc, key, val, cd, wd])
@@ -220,7 +245,8 @@ def build_config(name: str, layers_override, dev, table_fmt="packed"):
     torch.cuda.synchronize()
     if table_fmt != "packed":
         w.name = f"{w.name}_{table_fmt}"
-    cfg.update({"workload": w.name, "table": table_fmt, "seed": w.seed, "heads": w.heads,
+    cfg.update({"workload": w.name, "table": table_fmt, "write_entry": write_entry,
+                "seed": w.seed, "heads": w.heads,
                 "head_dim": w.head_dim, "block_size": w.block_size,
                 "num_tokens": w.num_tokens, "seq_count": w.seq_count,
                 "max_seq_len": w.max_seq_len, "pool_blocks": w.num_blocks,
@@ -330,7 +356,7 @@ def main():
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the paged write/gather shards by KV head or by sequence with no "
-              "exchange; see DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+              "exchange).  Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     if args.copy_probe:
@@ -340,9 +366,11 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
-    w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table)
+    w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table,
+                                       args.write_entry)
     stream = torch.cuda.Stream(device=dev)
     sh = stream.cuda_stream
+    torch.cuda.set_stream(stream)  # launches that use torch's current stream
 
     for i in range(args.warmup):
         for launch in steps[i % len(steps)]:

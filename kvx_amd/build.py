@@ -86,5 +86,35 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
+TORCH_OPS_LIB = PKG_DIR / "libkvx_amd_torch.so"
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """Compile the PyTorch-ROCm op library (csrc/torch_ops.cpp) against the
+    installed torch and link it to libkvx_amd.so (found next to it at run
+    time).  Host code only: g++ with torch's and ROCm's headers."""
+    import torch
+
+    if torch.version.hip is None:
+        raise RuntimeError("the torch op library needs a ROCm build of PyTorch")
+    tdir = Path(torch.__file__).resolve().parent
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cxx = shutil.which("g++") or "g++"
+    tmp = TORCH_OPS_LIB.with_suffix(".so.tmp")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+          "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          f"-I{INCLUDE}", f"-I{tdir / 'include'}",
+          f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+          f"-I{rocm / 'include'}", str(TORCH_OPS_SRC), "-o", str(tmp),
+          f"-L{PKG_DIR}", "-lkvx_amd", f"-L{tdir / 'lib'}", "-lc10", "-lc10_hip",
+          "-ltorch_cpu", "-ltorch_hip", f"-L{rocm / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, TORCH_OPS_LIB)
+    return TORCH_OPS_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_torch_ops(verbose="-v" in sys.argv))
