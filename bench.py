@@ -58,6 +58,12 @@ def parse_args():
                    help="issue the writes through kvx_launch_write_kv* (ctypes) or the "
                         "PyTorch-ROCm op _C_cache_ops.reshape_and_cache_flash_kvx "
                         "(c1, c2, c4, c5: NHD caches)")
+    p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
+                   help="c4: FP8 format of the cache")
+    p.add_argument("--scales", default="tensor",
+                   choices=["tensor", "head", "block", "block_head"],
+                   help="c4: FP8 scale granularity (per tensor, per KV head, per physical "
+                        "block, per block and head)")
     p.add_argument("--layers", type=int, default=None,
                    help="override the layer count of c1/c2/c4")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -99,7 +105,8 @@ class Launch:
             raise RuntimeError(f"{self.kind} launch returned status {st}")
 
 
-def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch"):
+def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch",
+                 fp8="e4m3", scales="tensor"):
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -107,9 +114,18 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
 
     lib = abi.load()
     tdt = {DType.BF16: torch.bfloat16, DType.F16: torch.float16,
-           DType.F8_E4M3: torch.float8_e4m3fn}
+           DType.F8_E4M3: torch.float8_e4m3fn, DType.F8_E5M2: torch.float8_e5m2}
     w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
+    if (fp8 != "e4m3" or scales != "tensor") and name != "c4":
+        raise SystemExit("--fp8 / --scales apply to c4")
+    if scales != "tensor" and write_entry == "torch_op":
+        raise SystemExit("the torch op takes per-tensor scales")
+    if fp8 == "e5m2":
+        w.cache_dtype = DType.F8_E5M2
+        w.name = w.name.replace("fp8_e4m3", "fp8_e5m2")
+    if scales != "tensor":
+        w.name = f"{w.name}_scale_{scales}"
 
     if table_fmt != "packed" and name == "c3":
         raise SystemExit("c3 has no gather: --table applies to c1, c2, c4, c5")
@@ -123,7 +139,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         op = torch.ops._C_cache_ops.reshape_and_cache_flash_kvx
 
     def fill(t):
-        if t.dtype == torch.float8_e4m3fn:
+        if t.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
             t.view(torch.uint8).random_(0, 256)
         else:
             t.normal_()
@@ -163,6 +179,12 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         keep.append(table)
     keep += [slots, lens]
     wbytes, gbytes = W.write_bytes(w), W.gather_bytes(w, table_fmt)
+    if scales != "tensor":
+        # scale reads replace the two per-tensor f32 values already counted
+        per_blk = {"head": 0, "block": 1, "block_head": w.heads}[scales]
+        per_tensor = w.heads if scales == "head" else 0
+        wbytes += 8 * (per_tensor + per_blk * w.valid_write_tokens()) - 8
+        gbytes += 8 * (per_tensor + per_blk * int(W.gathered_blocks(w))) - 8
     wtok, gtok = w.valid_write_tokens(), w.gathered_tokens()
     steps = []  # list of per-step launch lists (rotated by step index)
 
@@ -170,7 +192,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         if op is not None:
             # the op writes on torch's current stream (the bench stream)
             one = torch.ones(1, dtype=torch.float32, device=dev)
-            kvd = "fp8" if ks is not None else "auto"
+            kvd = ("fp8_e5m2" if fp8 == "e5m2" else "fp8") if ks is not None else "auto"
             args = (key, val, pc.key_cache, pc.value_cache, slots, kvd,
                     one if ks is None else ks, one if vs is None else vs)
             keep.extend([pc, key, val, one])
@@ -195,7 +217,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         gd = paged.build_gather(ko, vo, tb, lens, w.max_seq_len)
         keep.extend([cd, gd, tb])
         if ks is not None:
-            ksd, vsd = abi.scale_desc(ks.data_ptr()), abi.scale_desc(vs.data_ptr())
+            ksd, vsd = paged.scale_desc_of(ks), paged.scale_desc_of(vs)
             keep.extend([ksd, vsd])
             return Launch("gather", lib.kvx_launch_gather_kv_dequant,
                           (C.byref(cd), C.byref(gd), C.byref(ksd), C.byref(vsd)),
@@ -217,8 +239,25 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
                                 device=dev) * 2.0
             cal_v = torch.randn((w.num_tokens, w.heads, w.head_dim), generator=g,
                                 device=dev) * 2.0
-            ks = (cal_k.abs().max() / 448.0).reshape(1).float()
-            vs = (cal_v.abs().max() / 448.0).reshape(1).float()
+            top = 57344.0 if fp8 == "e5m2" else 448.0
+            ks = (cal_k.abs().max() / top).reshape(1).float()
+            vs = (cal_v.abs().max() / top).reshape(1).float()
+            if scales != "tensor":
+                # per-head amax / top, and (block kinds) a seeded per-block factor
+                gs = torch.Generator(device=dev).manual_seed(w.notes["calibration_seed"] + 1)
+                hk = cal_k.abs().amax(dim=(0, 2)) / top
+                hv = cal_v.abs().amax(dim=(0, 2)) / top
+                nb = w.num_blocks * (2 if table_fmt == "kv_offsets" else 1)
+                fk = torch.rand((nb, 1), generator=gs, device=dev) + 0.5
+                fv = torch.rand((nb, 1), generator=gs, device=dev) + 0.5
+                vals = {"head": (hk, hv),
+                        "block": ((fk * ks).reshape(nb), (fv * vs).reshape(nb)),
+                        "block_head": (fk * hk, fv * hv)}[scales]
+                gran = {"head": abi.ScaleGranularity.PER_HEAD,
+                        "block": abi.ScaleGranularity.PER_BLOCK,
+                        "block_head": abi.ScaleGranularity.PER_BLOCK_HEAD}[scales]
+                ks = paged.Scales(vals[0].float().contiguous(), gran)
+                vs = paged.Scales(vals[1].float().contiguous(), gran)
             keep += [ks, vs]
         step = []
         for _ in range(layers):
@@ -245,6 +284,8 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
     torch.cuda.synchronize()
     if table_fmt != "packed":
         w.name = f"{w.name}_{table_fmt}"
+    if name == "c4":
+        cfg.update({"fp8": fp8, "scales": scales})
     cfg.update({"workload": w.name, "table": table_fmt, "write_entry": write_entry,
                 "seed": w.seed, "heads": w.heads,
                 "head_dim": w.head_dim, "block_size": w.block_size,
@@ -367,7 +408,7 @@ def main():
 
     dev = torch.device("cuda:0")
     w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table,
-                                       args.write_entry)
+                                       args.write_entry, args.fp8, args.scales)
     stream = torch.cuda.Stream(device=dev)
     sh = stream.cuda_stream
     torch.cuda.set_stream(stream)  # launches that use torch's current stream
@@ -442,7 +483,8 @@ def main():
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8_e4m3" if w.cache_dtype.name == "F8_E4M3" else w.io_dtype.name.lower(),
+        "dtype": {"F8_E4M3": "fp8_e4m3", "F8_E5M2": "fp8_e5m2"}.get(
+            w.cache_dtype.name, w.io_dtype.name.lower()),
         "data": "synthetic",
         "config": cfg,
         "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),

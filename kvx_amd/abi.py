@@ -307,15 +307,21 @@ def make_write(num_tokens, heads, head_dim, dtype, memory, key_data, value_data,
     return w
 
 
-def scale_desc(data, dtype=DType.F32,
-               granularity=ScaleGranularity.PER_TENSOR) -> ScaleDesc:
+def scale_desc(data, dtype=DType.F32, granularity=ScaleGranularity.PER_TENSOR,
+               shape=(1,), stride=None) -> ScaleDesc:
+    """kvx_scale_desc_t.  Shapes this build accepts (strides in elements,
+    contiguous by default): PER_TENSOR any; PER_HEAD [num_kv_heads];
+    PER_BLOCK [num_blocks]; PER_BLOCK_HEAD [num_blocks, num_kv_heads]."""
     s = ScaleDesc()
     s.size = C.sizeof(ScaleDesc)
     s.dtype = int(dtype)
     s.granularity = int(granularity)
-    s.ndim = 1
-    s.shape[0] = 1
-    s.stride[0] = 1
+    shape = tuple(int(x) for x in shape)
+    stride = contiguous_strides(shape) if stride is None else tuple(int(x) for x in stride)
+    s.ndim = len(shape)
+    for i, (n, st) in enumerate(zip(shape, stride)):
+        s.shape[i] = n
+        s.stride[i] = st
     s.data = data
     return s
 

@@ -232,8 +232,9 @@ __device__ __forceinline__ void f32_to_io(float v, Raw<B> &y, int i) {
   }
 }
 
-// io (F16/BF16/F32) -> E4M3: q = e4m3(sat(x / scale)).
-template <int G, int IO>
+// io (F16/BF16/F32) -> FP8 (F8 = KVX_DTYPE_F8_E4M3 or KVX_DTYPE_F8_E5M2):
+// q = fp8(sat(x / scale)).
+template <int G, int IO, int F8>
 struct QuantOp {
   static constexpr int kSrc = G * IoType<IO>::kBytes;
   static constexpr int kDst = G;
@@ -245,18 +246,20 @@ struct QuantOp {
     for (int k = 0; k < Raw<kDst>::kWords; ++k) y.w[k] = 0;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      put8(y, i, f32_to_e4m3(io_to_f32<IO>(x, i) / scale));
+      const float q = io_to_f32<IO>(x, i) / scale;
+      put8(y, i, F8 == KVX_DTYPE_F8_E5M2 ? f32_to_e5m2(q) : f32_to_e4m3(q));
     }
     return y;
   }
 };
 
-// E4M3 -> io (F16/BF16/F32): y = io(f32(q) * scale); any NaN result is the
+// FP8 -> io (F16/BF16/F32): y = io(f32(q) * scale); any NaN result is the
 // canonical quiet NaN of the io type.  gfx950 decodes two OCP E4M3 codes
-// exactly with v_cvt_pk_f32_fp8, multiplies in f32, and narrows two values
-// with round-to-nearest-even (v_cvt_pk_bf16_f32 / v_cvt_f16_f32); the result
-// equals fp_convert.h's e4m3_to_f32 / f32_to_bf16 / f32_to_f16, which the
-// GPU tests check for every code.
+// exactly with v_cvt_pk_f32_fp8 (E5M2: v_cvt_pk_f32_bf8), multiplies in f32,
+// and narrows two values with round-to-nearest-even (v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32); the result equals fp_convert.h's e4m3_to_f32 /
+// e5m2_to_f32 / f32_to_bf16 / f32_to_f16, which the GPU tests check for
+// every code.
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -278,7 +281,18 @@ __device__ __forceinline__ uint32_t pack_pair(f32x2 f) {
   }
 }
 
-template <int G, int IO>
+template <bool kE5M2>
+__device__ __forceinline__ f32x2 decode_pair(int word, bool hi) {
+  if constexpr (kE5M2) {
+    return hi ? __builtin_amdgcn_cvt_pk_f32_bf8(word, true)
+              : __builtin_amdgcn_cvt_pk_f32_bf8(word, false);
+  } else {
+    return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(word, true)
+              : __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+  }
+}
+
+template <int G, int IO, int F8>
 struct DequantOp {
   static constexpr int kSrc = G;
   static constexpr int kDst = G * IoType<IO>::kBytes;
@@ -291,8 +305,7 @@ struct DequantOp {
     for (int p = 0; p < (G + 1) / 2; ++p) {
       // codes 2p, 2p+1 sit in halfword (p & 1) of word p / 2
       const int word = (int)x.w[p >> 1];
-      const f32x2 f = ((p & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8(word, true)
-                               : __builtin_amdgcn_cvt_pk_f32_fp8(word, false)) * scale;
+      const f32x2 f = decode_pair<F8 == KVX_DTYPE_F8_E5M2>(word, (p & 1) != 0) * scale;
       if constexpr (IO == KVX_DTYPE_F32) {
         y.w[2 * p] = f32_bits(canon_nan_f32(f[0]));
         if (2 * p + 1 < G) y.w[2 * p + 1] = f32_bits(canon_nan_f32(f[1]));
@@ -324,6 +337,13 @@ template <bool I64>
 __device__ __forceinline__ int64_t load_idx(const void *base, int64_t i) {
   if constexpr (I64) return reinterpret_cast<const int64_t *>(base)[i];
   return (int64_t)reinterpret_cast<const int32_t *>(base)[i];
+}
+
+// Scale of (block b, head h): the workgroup's per-tensor value, or the
+// indexed entry.
+__device__ __forceinline__ float scale_of(const ScaleRef &r, float uniform, int64_t b,
+                                          uint32_t h) {
+  return r.indexed ? r.p[b * r.s_block + (int64_t)h * r.s_head] : uniform;
 }
 
 // Byte offset, relative to the (block, offset) base, of the chunk that
@@ -366,8 +386,8 @@ struct WriteArgs {
   char *dst_k;
   char *dst_v;
   const void *slots;
-  const float *k_scale;
-  const float *v_scale;
+  ScaleRef ksc;  // quantizing ops only
+  ScaleRef vsc;
   GeomBytes gk;
   GeomBytes gv;
   int64_t num_tokens;
@@ -396,22 +416,25 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 
   int64_t koff[kMaxChunksPerLane];
   int64_t voff[kMaxChunksPerLane];
+  uint32_t hk[kMaxChunksPerLane];  // head of each chunk (indexed scales)
 #pragma unroll
   for (int k = 0; k < kMaxChunksPerLane; ++k) {
     const int c = l + k * lpt;
     koff[k] = 0;
     voff[k] = 0;
+    hk[k] = 0;
     if (c < a.nchunks) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
       koff[k] = chunk_off(a.gk, e, (uint32_t)a.head_dim);
       voff[k] = chunk_off(a.gv, e, (uint32_t)a.head_dim);
+      if constexpr (Op::kScaled) hk[k] = e / (uint32_t)a.head_dim;
     }
   }
   float ks = 1.0f;
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
   }
 
   for (int64_t g = wave; g < a.num_groups; g += nwaves) {
@@ -456,18 +479,19 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
     for (int k = 0; k < kMaxChunksPerLane; ++k) {
       const int c = l + k * lpt;
       if (c < a.nchunks) {
-        st<Op::kDst>(dk + koff[k], Op::apply(xk[k], ks));
-        st<Op::kDst>(dv + voff[k], Op::apply(xv[k], vs));
+        st<Op::kDst>(dk + koff[k], Op::apply(xk[k], scale_of(a.ksc, ks, b, hk[k])));
+        st<Op::kDst>(dv + voff[k], Op::apply(xv[k], scale_of(a.vsc, vs, b, hk[k])));
       }
     }
     for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      const uint32_t h = e / (uint32_t)a.head_dim;
       const Raw<Op::kSrc> yk = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
       const Raw<Op::kSrc> yv = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
       st<Op::kDst>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim),
-                   Op::apply(yk, ks));
+                   Op::apply(yk, scale_of(a.ksc, ks, b, h)));
       st<Op::kDst>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim),
-                   Op::apply(yv, vs));
+                   Op::apply(yv, scale_of(a.vsc, vs, b, h)));
     }
   }
 }
@@ -569,11 +593,12 @@ __global__ __launch_bounds__(kBlockThreads) void write_blocks_kernel(WriteArgs a
   const int tid = (int)threadIdx.x;
   const int lane = tid & (kWave - 1);
 
+  // Per-tensor scales only: the host keeps indexed scales on write_kernel.
   float ks = 1.0f;
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
   }
 
   if (tid < kWave) {  // wave 0 checks that the group fills one block in order
@@ -643,8 +668,8 @@ struct GatherArgs {
   char *dst_v;
   const void *table;
   const void *seq_lens;
-  const float *k_scale;
-  const float *v_scale;
+  ScaleRef ksc;              // dequantizing ops only
+  ScaleRef vsc;
   const void *indptr;        // RAGGED
   int64_t table_count;       // RAGGED: entries of `table`
   const char *pool[2];       // KV_OFFSETS primary / secondary
@@ -681,6 +706,7 @@ struct BlockJob {
   const char *cv;
   char *ok;
   char *ov;
+  int64_t bid;
   int32_t rows;
   float ks;
   float vs;
@@ -701,11 +727,12 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
   if (bid < 0 || bid >= a.num_blocks) return false;
   const int64_t rem = n - t0;
   j.rows = rem < a.block_size ? (int32_t)rem : a.block_size;
+  j.bid = bid;
   j.ks = 1.0f;
   j.vs = 1.0f;
   if constexpr (Op::kScaled) {
-    j.ks = *a.k_scale;
-    j.vs = *a.v_scale;
+    j.ks = a.ksc.p[0];
+    j.vs = a.vsc.p[0];
   }
   j.ck = a.src_k + bid * a.gk.s_block;
   j.cv = a.src_v + bid * a.gv.s_block;
@@ -720,9 +747,21 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
 // one power-of-two row range of a block (KVX_GATHER_TILE_BYTES).
 // Copy `total` chunks of K and of V: flat index f < 2 * total, K for
 // f < total, V above, so a one-row tile still gives every thread a chunk.
+// Scale of chunk i (counted from a row start) of a flat run: the
+// per-tensor value, or the indexed entry of block `bid` and the chunk's head.
+__device__ __forceinline__ float run_scale(const GatherArgs &a, bool v, float ks, float vs,
+                                           int64_t bid, int64_t i) {
+  const ScaleRef &r = v ? a.vsc : a.ksc;
+  if (!r.indexed) return v ? vs : ks;
+  const uint32_t c = (uint32_t)i % (uint32_t)a.nchunks;  // i < 2^31 within a tile
+  const uint32_t h = c * (uint32_t)a.chunk_elems / (uint32_t)a.head_dim;
+  return r.p[bid * r.s_block + (int64_t)h * r.s_head];
+}
+
 template <class Op>
-__device__ __forceinline__ void flat_copy(const char *ck, const char *cv, char *ok,
-                                          char *ov, int64_t total, float ks, float vs) {
+__device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, const char *cv,
+                                          char *ok, char *ov, int64_t total, float ks, float vs,
+                                          int64_t bid) {
   const int64_t both = 2 * total;
   int64_t f = threadIdx.x;
   for (; f + (kFlatUnroll - 1) * kBlockThreads < both; f += kFlatUnroll * kBlockThreads) {
@@ -737,16 +776,20 @@ __device__ __forceinline__ void flat_copy(const char *ck, const char *cv, char *
     for (int u = 0; u < kFlatUnroll; ++u) {
       const int64_t g = f + u * kBlockThreads;
       const bool v = g >= total;
-      st<Op::kDst, kGatherNtStore>((v ? ov : ok) + (g - (v ? total : 0)) * Op::kDst,
-                                   Op::apply(x[u], v ? vs : ks));
+      const int64_t i = g - (v ? total : 0);
+      float sc = v ? vs : ks;
+      if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, i);
+      st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst, Op::apply(x[u], sc));
     }
   }
   for (; f < both; f += kBlockThreads) {
     const bool v = f >= total;
     const int64_t i = f - (v ? total : 0);
+    float sc = v ? vs : ks;
+    if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, i);
     st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst,
                                  Op::apply(ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + i * Op::kSrc),
-                                           v ? vs : ks));
+                                           sc));
   }
 }
 
@@ -768,17 +811,17 @@ __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a
   if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
   const int64_t rem = n - t0;
   const int32_t rows = rem < rows_per_part ? (int32_t)rem : rows_per_part;
-  float ks = 1.0f;
+  float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
   }
   const int64_t row0 = (int64_t)part * rows_per_part;
   const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
-  flat_copy<Op>(a.src_k + bid * a.gk.s_block + row0 * a.gk.s_off,
+  flat_copy<Op>(a, a.src_k + bid * a.gk.s_block + row0 * a.gk.s_off,
                 a.src_v + bid * a.gv.s_block + row0 * a.gv.s_off, a.dst_k + out0,
-                a.dst_v + out0, (int64_t)rows * a.nchunks, ks, vs);
+                a.dst_v + out0, (int64_t)rows * a.nchunks, ks, vs, bid);
 }
 
 // Any other layout: rows go to (wave, lane group), each lane keeps the
@@ -794,17 +837,28 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
   const int sub = lane >> a.lpt_log2;
   const int l = lane & (lpt - 1);
 
+  // Per chunk: cache offsets and (dequantizing ops) the scales of its head in
+  // this block, the same for every row of the block.
   int64_t koff[kMaxChunksPerLane];
   int64_t voff[kMaxChunksPerLane];
+  float ksk[kMaxChunksPerLane];
+  float vsk[kMaxChunksPerLane];
 #pragma unroll
   for (int k = 0; k < kMaxChunksPerLane; ++k) {
     const int c = l + k * lpt;
     koff[k] = 0;
     voff[k] = 0;
+    ksk[k] = j.ks;
+    vsk[k] = j.vs;
     if (c < a.nchunks) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
       koff[k] = chunk_off(a.gk, e, (uint32_t)a.head_dim);
       voff[k] = chunk_off(a.gv, e, (uint32_t)a.head_dim);
+      if constexpr (Op::kScaled) {
+        const uint32_t h = e / (uint32_t)a.head_dim;
+        ksk[k] = scale_of(a.ksc, j.ks, j.bid, h);
+        vsk[k] = scale_of(a.vsc, j.vs, j.bid, h);
+      }
     }
   }
 
@@ -827,18 +881,19 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
     for (int k = 0; k < kMaxChunksPerLane; ++k) {
       const int c = l + k * lpt;
       if (c < a.nchunks) {
-        st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(xk[k], j.ks));
-        st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(xv[k], j.vs));
+        st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(xk[k], ksk[k]));
+        st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(xv[k], vsk[k]));
       }
     }
     for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      const uint32_t h = e / (uint32_t)a.head_dim;
       const Raw<Op::kSrc> yk =
           ld<Op::kSrc>(rk + chunk_off(a.gk, e, (uint32_t)a.head_dim));
       const Raw<Op::kSrc> yv =
           ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim));
-      st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(yk, j.ks));
-      st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(yv, j.vs));
+      st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(yk, scale_of(a.ksc, j.ks, j.bid, h)));
+      st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(yv, scale_of(a.vsc, j.vs, j.bid, h)));
     }
   }
 }
@@ -866,11 +921,11 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
   int64_t start;
   if (!indexed_extent<FMT, I64, P64>(a, s, t0, n, start)) return;
 
-  float ks = 1.0f;
+  float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
   }
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
@@ -881,15 +936,18 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
 
   int64_t koff[kMaxChunksPerLane];
   int64_t voff[kMaxChunksPerLane];
+  uint32_t hk[kMaxChunksPerLane];  // head of each chunk (indexed scales)
 #pragma unroll
   for (int k = 0; k < kMaxChunksPerLane; ++k) {
     const int c = l + k * lpt;
     koff[k] = 0;
     voff[k] = 0;
+    hk[k] = 0;
     if (c < a.nchunks) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
       koff[k] = chunk_off(a.gk, e, (uint32_t)a.head_dim);
       voff[k] = chunk_off(a.gv, e, (uint32_t)a.head_dim);
+      if constexpr (Op::kScaled) hk[k] = e / (uint32_t)a.head_dim;
     }
   }
 
@@ -898,8 +956,10 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
     if (t >= n) break;
     const char *rk = nullptr;
     const char *rv = nullptr;
+    int64_t sb = 0;  // block of block-indexed scales (RAGGED; KV_OFFSETS has none)
     if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
       const int64_t bid = load_idx<I64>(a.table, start + t);
+      sb = bid;
       if (bid >= 0 && bid < a.num_blocks) {
         const int64_t o = t % a.block_size;
         rk = a.src_k + bid * a.gk.s_block + o * a.gk.s_off;
@@ -926,19 +986,24 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
       const int c = l + k * lpt;
       if (c < a.nchunks) {
         if (rk != nullptr)
-          st<Op::kDst>(wk + (int64_t)c * Op::kDst, Op::apply(ld<Op::kSrc>(rk + koff[k]), ks));
+          st<Op::kDst>(wk + (int64_t)c * Op::kDst,
+                       Op::apply(ld<Op::kSrc>(rk + koff[k]), scale_of(a.ksc, ks, sb, hk[k])));
         if (rv != nullptr)
-          st<Op::kDst>(wv + (int64_t)c * Op::kDst, Op::apply(ld<Op::kSrc>(rv + voff[k]), vs));
+          st<Op::kDst>(wv + (int64_t)c * Op::kDst,
+                       Op::apply(ld<Op::kSrc>(rv + voff[k]), scale_of(a.vsc, vs, sb, hk[k])));
       }
     }
     for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+      const uint32_t h = e / (uint32_t)a.head_dim;
       if (rk != nullptr)
         st<Op::kDst>(wk + (int64_t)c * Op::kDst,
-                     Op::apply(ld<Op::kSrc>(rk + chunk_off(a.gk, e, (uint32_t)a.head_dim)), ks));
+                     Op::apply(ld<Op::kSrc>(rk + chunk_off(a.gk, e, (uint32_t)a.head_dim)),
+                               scale_of(a.ksc, ks, sb, h)));
       if (rv != nullptr)
         st<Op::kDst>(wv + (int64_t)c * Op::kDst,
-                     Op::apply(ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim)), vs));
+                     Op::apply(ld<Op::kSrc>(rv + chunk_off(a.gv, e, (uint32_t)a.head_dim)),
+                               scale_of(a.vsc, vs, sb, h)));
     }
   }
 }
@@ -988,7 +1053,7 @@ __device__ __forceinline__ bool indexed_extent(const GatherArgs &a, int64_t s, i
 // when the table skips it.  The in-block offset of the row is o * s_off.
 template <int FMT, bool I64>
 __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, int64_t s,
-                                                   int64_t start, int64_t t) {
+                                                   int64_t start, int64_t t, int64_t *blk) {
   const uint32_t tu = (uint32_t)t;  // t < max_seq_len < 2^31
   uint32_t lb;
   uint32_t o;
@@ -1002,6 +1067,7 @@ __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, 
   const GeomBytes &g = v ? a.gv : a.gk;
   if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
     const int64_t bid = load_idx<I64>(a.table, start + t);
+    *blk = bid;
     if (bid < 0 || bid >= a.num_blocks) return nullptr;
     return (v ? a.src_v : a.src_k) + bid * g.s_block + (int64_t)o * g.s_off;
   } else {
@@ -1053,11 +1119,11 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(Gath
   }
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;
-  float ks = 1.0f;
+  float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
-    ks = *a.k_scale;
-    vs = *a.v_scale;
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
   }
   const uint32_t total = (uint32_t)rows << a.nchunks_log2;
   const uint32_t both = 2 * total;
@@ -1070,12 +1136,14 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(Gath
     const char *src[kIndexedUnroll];
     char *dst[kIndexedUnroll];
     bool isv[kIndexedUnroll];
+    float sc[kIndexedUnroll];
 #pragma unroll
     for (int u = 0; u < kIndexedUnroll; ++u) {
       const uint32_t f = base + u * kBlockThreads;
       src[u] = nullptr;
       dst[u] = nullptr;
       isv[u] = f >= total;
+      sc[u] = isv[u] ? vs : ks;
       if (f < both) {
         const uint32_t gi = f - (isv[u] ? total : 0u);
         const uint32_t r = gi >> a.nchunks_log2;
@@ -1084,13 +1152,20 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(Gath
           const char *base = isv[u] ? tv : tk;
           src[u] = base == nullptr ? nullptr
                                    : base + (int64_t)r * (isv[u] ? a.gv.s_off : a.gk.s_off);
-        } else {
-          src[u] = indexed_row<FMT, I64>(a, isv[u], s, start, t0 + r);
         }
+        int64_t blk = 0;  // RAGGED block for block-indexed scales (KV_OFFSETS: none)
+        if constexpr (!kTile) src[u] = indexed_row<FMT, I64>(a, isv[u], s, start, t0 + r, &blk);
         if (src[u] != nullptr) {
           src[u] += (int64_t)c * Op::kSrc;
           dst[u] = (isv[u] ? a.dst_v : a.dst_k) + out0 + (int64_t)r * a.out_row_bytes +
                    (int64_t)c * Op::kDst;
+          if constexpr (Op::kScaled) {
+            const ScaleRef &sr = isv[u] ? a.vsc : a.ksc;
+            if (sr.indexed)
+              sc[u] = sr.p[blk * sr.s_block +
+                           (int64_t)(c * (uint32_t)a.chunk_elems / (uint32_t)a.head_dim) *
+                               sr.s_head];
+          }
         }
       }
     }
@@ -1102,7 +1177,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(Gath
 #pragma unroll
     for (int u = 0; u < kIndexedUnroll; ++u) {
       if (src[u] != nullptr)
-        st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], isv[u] ? vs : ks));
+        st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
   }
 }
@@ -1229,24 +1304,43 @@ void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
   }
 }
 
-template <int IO>
+template <int IO, int F8>
 void dispatch_quant(int ge, const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   switch (ge) {
-    case 8: launch_write_op<QuantOp<8, IO>>(a, w, s); break;
-    case 4: launch_write_op<QuantOp<4, IO>>(a, w, s); break;
-    case 2: launch_write_op<QuantOp<2, IO>>(a, w, s); break;
-    default: launch_write_op<QuantOp<1, IO>>(a, w, s); break;
+    case 8: launch_write_op<QuantOp<8, IO, F8>>(a, w, s); break;
+    case 4: launch_write_op<QuantOp<4, IO, F8>>(a, w, s); break;
+    case 2: launch_write_op<QuantOp<2, IO, F8>>(a, w, s); break;
+    default: launch_write_op<QuantOp<1, IO, F8>>(a, w, s); break;
   }
 }
 
-template <int IO>
+template <int F8>
+void dispatch_quant_io(int io, int ge, const WriteArgs &a, const WriteLaunch &w,
+                       hipStream_t s) {
+  switch (io) {
+    case KVX_DTYPE_F32: dispatch_quant<KVX_DTYPE_F32, F8>(ge, a, w, s); break;
+    case KVX_DTYPE_F16: dispatch_quant<KVX_DTYPE_F16, F8>(ge, a, w, s); break;
+    default: dispatch_quant<KVX_DTYPE_BF16, F8>(ge, a, w, s); break;
+  }
+}
+
+template <int IO, int F8>
 void dispatch_dequant(int ge, const GatherArgs &a, int64_t grid,
                       hipStream_t s) {
   switch (ge) {
-    case 8: launch_gather_op<DequantOp<8, IO>>(a, grid, s); break;
-    case 4: launch_gather_op<DequantOp<4, IO>>(a, grid, s); break;
-    case 2: launch_gather_op<DequantOp<2, IO>>(a, grid, s); break;
-    default: launch_gather_op<DequantOp<1, IO>>(a, grid, s); break;
+    case 8: launch_gather_op<DequantOp<8, IO, F8>>(a, grid, s); break;
+    case 4: launch_gather_op<DequantOp<4, IO, F8>>(a, grid, s); break;
+    case 2: launch_gather_op<DequantOp<2, IO, F8>>(a, grid, s); break;
+    default: launch_gather_op<DequantOp<1, IO, F8>>(a, grid, s); break;
+  }
+}
+
+template <int F8>
+void dispatch_dequant_io(int io, int ge, const GatherArgs &a, int64_t grid, hipStream_t s) {
+  switch (io) {
+    case KVX_DTYPE_F32: dispatch_dequant<KVX_DTYPE_F32, F8>(ge, a, grid, s); break;
+    case KVX_DTYPE_F16: dispatch_dequant<KVX_DTYPE_F16, F8>(ge, a, grid, s); break;
+    default: dispatch_dequant<KVX_DTYPE_BF16, F8>(ge, a, grid, s); break;
   }
 }
 
@@ -1323,8 +1417,8 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   a.dst_k = static_cast<char *>(p.dst_k);
   a.dst_v = static_cast<char *>(p.dst_v);
   a.slots = p.slots;
-  a.k_scale = p.k_scale;
-  a.v_scale = p.v_scale;
+  a.ksc = p.k_scale;
+  a.vsc = p.v_scale;
   a.gk = to_bytes(p.gk, cs);
   a.gv = to_bytes(p.gv, cs);
   a.num_tokens = p.num_tokens;
@@ -1341,7 +1435,10 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
   WriteLaunch wl;
   wl.grid = (int)(want < 2048 ? want : 2048);
-  wl.blocks = plan_block_write(p, ge, a.nchunks, (p.conv == kConvQuant) ? ge * is : ge * cs,
+  // The block kernel applies per-tensor scales only.
+  const bool indexed = p.k_scale.indexed || p.v_scale.indexed;
+  wl.blocks = !indexed &&
+              plan_block_write(p, ge, a.nchunks, (p.conv == kConvQuant) ? ge * is : ge * cs,
                                &wl.bw, &wl.block_grid, &wl.lds_bytes);
   hipStream_t s = as_stream(stream);
 
@@ -1354,10 +1451,10 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
       default: launch_write_op<CopyOp<1>>(a, wl, s); break;
     }
   } else {
-    switch (p.io_dtype) {
-      case KVX_DTYPE_F32: dispatch_quant<KVX_DTYPE_F32>(ge, a, wl, s); break;
-      case KVX_DTYPE_F16: dispatch_quant<KVX_DTYPE_F16>(ge, a, wl, s); break;
-      default: dispatch_quant<KVX_DTYPE_BF16>(ge, a, wl, s); break;
+    if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
+      dispatch_quant_io<KVX_DTYPE_F8_E5M2>(p.io_dtype, ge, a, wl, s);
+    } else {
+      dispatch_quant_io<KVX_DTYPE_F8_E4M3>(p.io_dtype, ge, a, wl, s);
     }
   }
   return hipGetLastError() == hipSuccess ? KVX_STATUS_OK
@@ -1388,8 +1485,8 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.dst_v = static_cast<char *>(p.dst_v);
   a.table = p.block_table;
   a.seq_lens = p.seq_lens;
-  a.k_scale = p.k_scale;
-  a.v_scale = p.v_scale;
+  a.ksc = p.k_scale;
+  a.vsc = p.v_scale;
   a.gk = to_bytes(p.gk, cs);
   a.gv = to_bytes(p.gv, cs);
   a.out_row_bytes = row_elems * is;
@@ -1468,10 +1565,10 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       default: launch_gather_op<CopyOp<1>>(a, grid, s); break;
     }
   } else {
-    switch (p.io_dtype) {
-      case KVX_DTYPE_F32: dispatch_dequant<KVX_DTYPE_F32>(ge, a, grid, s); break;
-      case KVX_DTYPE_F16: dispatch_dequant<KVX_DTYPE_F16>(ge, a, grid, s); break;
-      default: dispatch_dequant<KVX_DTYPE_BF16>(ge, a, grid, s); break;
+    if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
+      dispatch_dequant_io<KVX_DTYPE_F8_E5M2>(p.io_dtype, ge, a, grid, s);
+    } else {
+      dispatch_dequant_io<KVX_DTYPE_F8_E4M3>(p.io_dtype, ge, a, grid, s);
     }
   }
   return hipGetLastError() == hipSuccess ? KVX_STATUS_OK

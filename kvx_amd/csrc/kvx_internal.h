@@ -31,8 +31,19 @@ struct Geom {
 // Element conversion applied while moving one element.
 enum ConvKind : int32_t {
   kConvCopy = 0,     // bit copy, any element size
-  kConvQuant = 1,    // F16/BF16/F32 io -> E4M3 cache, divide by scale
-  kConvDequant = 2,  // E4M3 cache -> F16/BF16/F32 io, multiply by scale
+  kConvQuant = 1,    // F16/BF16/F32 io -> E4M3/E5M2 cache, divide by scale
+  kConvDequant = 2,  // E4M3/E5M2 cache -> F16/BF16/F32 io, multiply by scale
+};
+
+// FP8 scales of one tensor (device memory, F32): element (block b, head h)
+// uses p[b * s_block + h * s_head].  indexed == 0 is the per-tensor case,
+// p[0] for every element.
+struct ScaleRef {
+  const float *p;
+  int64_t s_block;  // elements
+  int64_t s_head;   // elements
+  int32_t indexed;
+  int32_t pad_;
 };
 
 // Everything the write kernels need, already validated on the host.
@@ -42,8 +53,8 @@ struct WritePlan {
   void *dst_k;
   void *dst_v;
   const void *slots;
-  const float *k_scale;  // device pointers; only for kConvQuant
-  const float *v_scale;
+  ScaleRef k_scale;  // only for kConvQuant
+  ScaleRef v_scale;
   Geom gk;
   Geom gv;
   int64_t num_tokens;
@@ -65,8 +76,8 @@ struct GatherPlan {
   void *dst_v;
   const void *block_table;
   const void *seq_lens;
-  const float *k_scale;  // device pointers; only for kConvDequant
-  const float *v_scale;
+  ScaleRef k_scale;  // only for kConvDequant
+  ScaleRef v_scale;
   const void *indptr;       // RAGGED: [seq_count + 1] token prefix sums
   int64_t table_count;      // entries of block_table
   const char *pool[2];      // KV_OFFSETS: primary / secondary pool bases

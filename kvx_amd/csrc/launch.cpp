@@ -9,7 +9,8 @@
 // or dereference NULL:
 //   - block_size == 0 with a non-empty batch   -> INVALID_ARGUMENT
 //   - NULL io / cache / index data pointers     -> INVALID_ARGUMENT
-// F8_E4M3 caches (quantizing write, byte-copy gather, dequantizing gather)
+// F8_E4M3 / F8_E5M2 caches (quantizing write, byte-copy gather, dequantizing
+// gather; per-tensor, per-head, per-block and per-block-head F32 scales)
 // and the RAGGED / KV_OFFSETS gather formats are extensions; the reference
 // returns UNSUPPORTED for them (kernels/kvx_paged_kv.cu:481-490, :788-790).
 #include <hip/hip_runtime.h>
@@ -24,6 +25,8 @@ namespace {
 bool is_io_float(kvx_dtype_t dt) {
   return dt == KVX_DTYPE_F16 || dt == KVX_DTYPE_BF16 || dt == KVX_DTYPE_F32;
 }
+
+bool is_fp8(kvx_dtype_t dt) { return dt == KVX_DTYPE_F8_E4M3 || dt == KVX_DTYPE_F8_E5M2; }
 
 // reference kvx_paged_kv.cu:269-289 (no size/dtype/data checks on this path)
 kvx_status_t check_io_3d(const kvx_tensor_desc_t *t, int32_t num_tokens,
@@ -106,40 +109,65 @@ bool block_fits(const Geom &g, int64_t bs, int64_t heads, int64_t head_dim, int 
   return (last + 1) * esize <= pitch;
 }
 
-// Resolve a per-tensor F32 scale for the quantizing write
-// (KVX_SPEC.md:258-259: scale descriptor first, raw pointer as fallback).
-kvx_status_t resolve_write_scale(const kvx_scale_desc_t *desc,
-                                 const void *raw, const float **out) {
-  if (desc->data != nullptr) {
-    if (desc->size < sizeof(kvx_scale_desc_t))
-      return KVX_STATUS_INVALID_ARGUMENT;
-    if (desc->dtype != KVX_DTYPE_F32) return KVX_STATUS_UNSUPPORTED;
-    if (desc->granularity != KVX_SCALE_PER_TENSOR)
-      return KVX_STATUS_UNSUPPORTED;
-    *out = static_cast<const float *>(desc->data);
-    return KVX_STATUS_OK;
+// A scale descriptor -> ScaleRef.  F32 scales only.  Granularities
+// (KVX_SPEC.md:190-197 names the fields; the shapes are this build's):
+//   PER_TENSOR      one value, data[0]
+//   PER_HEAD        ndim 1, shape [num_kv_heads], stride[0] in elements
+//   PER_BLOCK       ndim 1, shape [num_blocks], indexed by physical block id
+//   PER_BLOCK_HEAD  ndim 2, shape [num_blocks, num_kv_heads]
+// Block-indexed scales need physical block ids: KV_OFFSETS gathers
+// (block_ok = false) return UNSUPPORTED for them.
+kvx_status_t resolve_scale_desc(const kvx_scale_desc_t *d, const kvx_cache_desc_t *cache,
+                                bool block_ok, ScaleRef *out) {
+  if (d->size < sizeof(kvx_scale_desc_t)) return KVX_STATUS_INVALID_ARGUMENT;
+  if (d->dtype != KVX_DTYPE_F32) return KVX_STATUS_UNSUPPORTED;
+  const kvx_scale_granularity_t g = d->granularity;
+  if (g != KVX_SCALE_PER_TENSOR && g != KVX_SCALE_PER_HEAD && g != KVX_SCALE_PER_BLOCK &&
+      g != KVX_SCALE_PER_BLOCK_HEAD)
+    return KVX_STATUS_UNSUPPORTED;
+  if (!block_ok && (g == KVX_SCALE_PER_BLOCK || g == KVX_SCALE_PER_BLOCK_HEAD))
+    return KVX_STATUS_UNSUPPORTED;
+  if (d->data == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  const int64_t nb = cache->num_blocks;
+  const int64_t H = cache->num_kv_heads;
+  *out = ScaleRef{static_cast<const float *>(d->data), 0, 0, 0, 0};
+  switch (g) {
+    case KVX_SCALE_PER_HEAD:
+      if (d->ndim != 1 || d->shape[0] != H) return KVX_STATUS_INVALID_ARGUMENT;
+      out->s_head = d->stride[0];
+      break;
+    case KVX_SCALE_PER_BLOCK:
+      if (d->ndim != 1 || d->shape[0] != nb) return KVX_STATUS_INVALID_ARGUMENT;
+      out->s_block = d->stride[0];
+      break;
+    case KVX_SCALE_PER_BLOCK_HEAD:
+      if (d->ndim != 2 || d->shape[0] != nb || d->shape[1] != H)
+        return KVX_STATUS_INVALID_ARGUMENT;
+      out->s_block = d->stride[0];
+      out->s_head = d->stride[1];
+      break;
+    default:
+      return KVX_STATUS_OK;  // PER_TENSOR
   }
-  if (raw == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
-  *out = static_cast<const float *>(raw);
+  out->indexed = 1;
   return KVX_STATUS_OK;
 }
 
-kvx_status_t resolve_gather_scale(const kvx_scale_desc_t *desc,
-                                  const float **out) {
-  if (desc->size < sizeof(kvx_scale_desc_t))
-    return KVX_STATUS_INVALID_ARGUMENT;
-  if (desc->dtype != KVX_DTYPE_F32) return KVX_STATUS_UNSUPPORTED;
-  if (desc->granularity != KVX_SCALE_PER_TENSOR) return KVX_STATUS_UNSUPPORTED;
-  if (desc->data == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
-  *out = static_cast<const float *>(desc->data);
+// The quantizing write's scale (KVX_SPEC.md:258-259): the descriptor when
+// its data is set, else the raw pointer as a per-tensor F32 scale.
+kvx_status_t resolve_write_scale(const kvx_scale_desc_t *desc, const void *raw,
+                                 const kvx_cache_desc_t *cache, ScaleRef *out) {
+  if (desc->data != nullptr) return resolve_scale_desc(desc, cache, true, out);
+  if (raw == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  *out = ScaleRef{static_cast<const float *>(raw), 0, 0, 0, 0};
   return KVX_STATUS_OK;
 }
 
 }  // namespace
 
 // `expected` is the payload dtype of the per-dtype helper; KVX_DTYPE_F8_E4M3
-// is this build's FP8 path, where io may be F16/BF16/F32 (quantize) or
-// F8_E4M3 (byte copy).
+// and KVX_DTYPE_F8_E5M2 are this build's FP8 paths, where io may be
+// F16/BF16/F32 (quantize) or the cache's own FP8 dtype (byte copy).
 kvx_status_t launch_write(const kvx_cache_desc_t *cache,
                           const kvx_write_desc_t *write, int32_t tokens_per_seq,
                           bool prefill, kvx_dtype_t expected, void *stream) {
@@ -155,9 +183,8 @@ kvx_status_t launch_write(const kvx_cache_desc_t *cache,
   if (cache->k.dtype != expected || cache->v.dtype != expected)
     return KVX_STATUS_UNSUPPORTED;
   const kvx_dtype_t io_dt = write->io.key.dtype;
-  if (expected == KVX_DTYPE_F8_E4M3) {
-    if (write->io.value.dtype != io_dt ||
-        !(is_io_float(io_dt) || io_dt == KVX_DTYPE_F8_E4M3))
+  if (is_fp8(expected)) {
+    if (write->io.value.dtype != io_dt || !(is_io_float(io_dt) || io_dt == expected))
       return KVX_STATUS_UNSUPPORTED;
   } else if (io_dt != expected || write->io.value.dtype != expected) {
     return KVX_STATUS_UNSUPPORTED;
@@ -181,13 +208,13 @@ kvx_status_t launch_write(const kvx_cache_desc_t *cache,
   st = fill_geom(cache, &cache->v, &p.gv);
   if (st != KVX_STATUS_OK) return st;
 
-  const bool quant = expected == KVX_DTYPE_F8_E4M3 && io_dt != KVX_DTYPE_F8_E4M3;
-  p.k_scale = nullptr;
-  p.v_scale = nullptr;
+  const bool quant = is_fp8(expected) && io_dt != expected;
+  p.k_scale = ScaleRef{};
+  p.v_scale = ScaleRef{};
   if (quant) {
-    st = resolve_write_scale(&write->k_scale_desc, write->k_scale, &p.k_scale);
+    st = resolve_write_scale(&write->k_scale_desc, write->k_scale, cache, &p.k_scale);
     if (st != KVX_STATUS_OK) return st;
-    st = resolve_write_scale(&write->v_scale_desc, write->v_scale, &p.v_scale);
+    st = resolve_write_scale(&write->v_scale_desc, write->v_scale, cache, &p.v_scale);
     if (st != KVX_STATUS_OK) return st;
   }
 
@@ -269,12 +296,13 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
   st = fill_geom(cache, &cache->v, &p.gv);
   if (st != KVX_STATUS_OK) return st;
 
-  p.k_scale = nullptr;
-  p.v_scale = nullptr;
+  p.k_scale = ScaleRef{};
+  p.v_scale = ScaleRef{};
   if (dequant) {
-    st = resolve_gather_scale(k_scale, &p.k_scale);
+    const bool block_ok = fmt != KVX_BLOCK_TABLE_KV_OFFSETS;
+    st = resolve_scale_desc(k_scale, cache, block_ok, &p.k_scale);
     if (st != KVX_STATUS_OK) return st;
-    st = resolve_gather_scale(v_scale, &p.v_scale);
+    st = resolve_scale_desc(v_scale, cache, block_ok, &p.v_scale);
     if (st != KVX_STATUS_OK) return st;
   }
 
@@ -393,6 +421,7 @@ KVX_API kvx_status_t kvx_launch_write_kv(const kvx_cache_desc_t *cache,
     case KVX_DTYPE_BF16:
     case KVX_DTYPE_F32:
     case KVX_DTYPE_F8_E4M3:
+    case KVX_DTYPE_F8_E5M2:
       return launch_write(cache, write, 0, false, cache->k.dtype, stream);
     default:
       return KVX_STATUS_UNSUPPORTED;
@@ -430,6 +459,7 @@ KVX_API kvx_status_t kvx_launch_write_kv_prefill(
     case KVX_DTYPE_BF16:
     case KVX_DTYPE_F32:
     case KVX_DTYPE_F8_E4M3:
+    case KVX_DTYPE_F8_E5M2:
       return launch_write(cache, write, tokens_per_seq, true, cache->k.dtype,
                           stream);
     default:
@@ -468,6 +498,7 @@ KVX_API kvx_status_t kvx_launch_gather_kv(const kvx_cache_desc_t *cache,
     case KVX_DTYPE_BF16:
     case KVX_DTYPE_F32:
     case KVX_DTYPE_F8_E4M3:
+    case KVX_DTYPE_F8_E5M2:
       return launch_gather(cache, gather, nullptr, nullptr, false,
                            cache->k.dtype, stream);
     default:
@@ -481,9 +512,8 @@ KVX_API kvx_status_t kvx_launch_gather_kv_dequant(
     void *stream) {
   if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
   if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
-  if (cache->k.dtype != KVX_DTYPE_F8_E4M3) return KVX_STATUS_UNSUPPORTED;
-  return launch_gather(cache, gather, k_scale, v_scale, true,
-                       KVX_DTYPE_F8_E4M3, stream);
+  if (!kvx::is_fp8(cache->k.dtype)) return KVX_STATUS_UNSUPPORTED;
+  return launch_gather(cache, gather, k_scale, v_scale, true, cache->k.dtype, stream);
 }
 
 }  // extern "C"

@@ -23,7 +23,8 @@
 //   - Rows past slot_mapping.size(0) in key / value are ignored, as in vLLM
 //     (num_actual_tokens); the reference op fails on them.
 //   - kv_cache_dtype "fp8" / "fp8_e4m3" writes an E4M3 cache (uint8 or
-//     float8_e4m3fn tensor) with q = e4m3(sat(x / scale)); the reference op
+//     float8_e4m3fn tensor) and "fp8_e5m2" an E5M2 cache (uint8 or
+//     float8_e5m2 tensor), with q = fp8(sat(x / scale)); the reference op
 //     accepts only "auto".
 #include <ATen/ATen.h>
 // PyTorch-ROCm reports GPU tensors as device type "cuda": its device guard
@@ -55,8 +56,10 @@ kvx_dtype_t slot_dtype(at::ScalarType t) {
   }
 }
 
-bool is_fp8_cache(at::ScalarType t) {
-  return t == at::ScalarType::Byte || t == at::ScalarType::Float8_e4m3fn;
+bool is_fp8_cache(at::ScalarType t, kvx_dtype_t fmt) {
+  if (t == at::ScalarType::Byte) return true;
+  return fmt == KVX_DTYPE_F8_E5M2 ? t == at::ScalarType::Float8_e5m2
+                                  : t == at::ScalarType::Float8_e4m3fn;
 }
 
 void describe(kvx_tensor_desc_t *d, const at::Tensor &t, kvx_dtype_t dtype,
@@ -80,9 +83,10 @@ void reshape_and_cache_flash_kvx(const at::Tensor &key, const at::Tensor &value,
                                  const at::Tensor &slot_mapping,
                                  const std::string &kv_cache_dtype, const at::Tensor &k_scale,
                                  const at::Tensor &v_scale) {
-  const bool fp8 = kv_cache_dtype == "fp8" || kv_cache_dtype == "fp8_e4m3";
+  const bool e5m2 = kv_cache_dtype == "fp8_e5m2";
+  const bool fp8 = kv_cache_dtype == "fp8" || kv_cache_dtype == "fp8_e4m3" || e5m2;
   TORCH_CHECK(kv_cache_dtype == "auto" || fp8,
-              "KVX cache write supports kv_cache_dtype auto, fp8 and fp8_e4m3, not ",
+              "KVX cache write supports kv_cache_dtype auto, fp8, fp8_e4m3 and fp8_e5m2, not ",
               kv_cache_dtype);
   TORCH_CHECK(key.is_cuda() && value.is_cuda(), "key/value must be CUDA tensors");
   TORCH_CHECK(key_cache.is_cuda() && value_cache.is_cuda(),
@@ -96,9 +100,9 @@ void reshape_and_cache_flash_kvx(const at::Tensor &key, const at::Tensor &value,
   TORCH_CHECK(dt != KVX_DTYPE_INVALID, "KVX cache write unsupported dtype");
   kvx_dtype_t cache_dt = dt;
   if (fp8) {
-    TORCH_CHECK(is_fp8_cache(key_cache.scalar_type()),
-                "fp8 kv_cache_dtype needs a uint8 or float8_e4m3fn cache");
-    cache_dt = KVX_DTYPE_F8_E4M3;
+    cache_dt = e5m2 ? KVX_DTYPE_F8_E5M2 : KVX_DTYPE_F8_E4M3;
+    TORCH_CHECK(is_fp8_cache(key_cache.scalar_type(), cache_dt),
+                "fp8 kv_cache_dtype needs a uint8 or matching float8 cache");
   } else {
     TORCH_CHECK(key_cache.scalar_type() == key.scalar_type(),
                 "key/value dtype must match cache dtype");

@@ -26,6 +26,7 @@ _TORCH_DTYPE = {
     torch.bfloat16: DType.BF16,
     torch.float32: DType.F32,
     torch.float8_e4m3fn: DType.F8_E4M3,
+    torch.float8_e5m2: DType.F8_E5M2,
     torch.int32: DType.S32,
     torch.int64: DType.S64,
 }
@@ -136,9 +137,31 @@ def _stream_handle(stream) -> int | None:
     return int(stream)
 
 
+@dataclass
+class Scales:
+    """FP8 scales of one tensor with a granularity: `values` is a float32
+    device tensor of shape [1] (PER_TENSOR), [num_kv_heads] (PER_HEAD),
+    [num_blocks] (PER_BLOCK, by physical block id) or [num_blocks,
+    num_kv_heads] (PER_BLOCK_HEAD); its own strides are passed."""
+
+    values: torch.Tensor
+    granularity: abi.ScaleGranularity = abi.ScaleGranularity.PER_TENSOR
+
+
+def scale_desc_of(scale) -> abi.ScaleDesc:
+    """kvx_scale_desc_t for a one-element float32 tensor (per tensor) or a
+    Scales."""
+    if isinstance(scale, Scales):
+        v = scale.values
+        shape = tuple(v.shape) or (1,)
+        stride = tuple(v.stride()) or (1,)
+        return abi.scale_desc(v.data_ptr(), granularity=scale.granularity, shape=shape,
+                              stride=stride)
+    return abi.scale_desc(scale.data_ptr())
+
+
 def build_write(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
-                slot_mapping: torch.Tensor, k_scale: torch.Tensor | None = None,
-                v_scale: torch.Tensor | None = None) -> abi.WriteDesc:
+                slot_mapping: torch.Tensor, k_scale=None, v_scale=None) -> abi.WriteDesc:
     """kvx_write_desc_t for [T, H, D] key/value rows and [T] slots.  FP8
     scales are one-element F32 device tensors, passed as PER_TENSOR scale
     descriptors."""
@@ -157,9 +180,9 @@ def build_write(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
     w.slots.invalid_slot = -1
     w.slots.slots = slot_mapping.data_ptr()
     if k_scale is not None:
-        w.k_scale_desc = abi.scale_desc(k_scale.data_ptr())
+        w.k_scale_desc = scale_desc_of(k_scale)
     if v_scale is not None:
-        w.v_scale_desc = abi.scale_desc(v_scale.data_ptr())
+        w.v_scale_desc = scale_desc_of(v_scale)
     return w
 
 
@@ -299,8 +322,8 @@ def gather_kv(cache: PagedCache, key_out: torch.Tensor, value_out: torch.Tensor,
     if entry == "abi":
         return Status(lib.kvx_gather_kv(C.byref(cd), C.byref(gd), s))
     if k_scale is not None or v_scale is not None:
-        ks = abi.scale_desc(k_scale.data_ptr())
-        vs = abi.scale_desc(v_scale.data_ptr())
+        ks = scale_desc_of(k_scale)
+        vs = scale_desc_of(v_scale)
         return Status(lib.kvx_launch_gather_kv_dequant(C.byref(cd), C.byref(gd),
                                                        C.byref(ks), C.byref(vs), s))
     return Status(lib.kvx_launch_gather_kv(C.byref(cd), C.byref(gd), s))

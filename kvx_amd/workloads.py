@@ -77,7 +77,8 @@ class Workload:
 
 
 def dtype_bytes(dt: DType) -> int:
-    return {DType.F16: 2, DType.BF16: 2, DType.F32: 4, DType.F8_E4M3: 1}[DType(dt)]
+    return {DType.F16: 2, DType.BF16: 2, DType.F32: 4, DType.F8_E4M3: 1,
+            DType.F8_E5M2: 1}[DType(dt)]
 
 
 def write_bytes(w: Workload) -> int:
@@ -122,6 +123,12 @@ def gather_bytes(w: Workload, table: str = "packed") -> int:
     if w.cache_dtype != w.io_dtype:
         b += 8
     return int(b)
+
+
+def gathered_blocks(w: Workload) -> int:
+    """Block-table entries a gather uses (logical blocks with rows)."""
+    n = _gathered_per_seq(w)
+    return int(((n + w.block_size - 1) // w.block_size).sum())
 
 
 def ragged_table(w: Workload) -> tuple[np.ndarray, np.ndarray]:

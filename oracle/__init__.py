@@ -20,6 +20,43 @@ _LIB = None
 _I64P = C.POINTER(C.c_int64)
 
 
+class _ScaleT(C.Structure):
+    _fields_ = [("p", C.c_void_p), ("s_block", C.c_int64), ("s_head", C.c_int64)]
+
+
+class Scale:
+    """FP8 scales of one tensor: the scale of (block b, head h) is
+    values.flat[b * s_block + h * s_head].  A float is a per-tensor scale."""
+
+    def __init__(self, values, s_block: int = 0, s_head: int = 0):
+        self.values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+        self.s_block = int(s_block)
+        self.s_head = int(s_head)
+
+    @classmethod
+    def per_head(cls, values):
+        return cls(values, 0, 1)
+
+    @classmethod
+    def per_block(cls, values):
+        return cls(values, 1, 0)
+
+    @classmethod
+    def per_block_head(cls, values):
+        v = np.asarray(values, dtype=np.float32)
+        return cls(v, v.shape[1], 1)
+
+
+def _scale_arg(x):
+    """(keep-alive, pointer) for a float / Scale / None scale."""
+    if x is None:
+        return None, None
+    if not isinstance(x, Scale):
+        x = Scale([float(x)])
+    st = _ScaleT(x.values.ctypes.data, x.s_block, x.s_head)
+    return (x, st), C.pointer(st)
+
+
 def lib() -> C.CDLL:
     global _LIB
     if _LIB is None:
@@ -30,11 +67,11 @@ def lib() -> C.CDLL:
         geom = [i, _I64P, i64]
         L.oracle_cache_offset.argtypes = [i, _I64P, i64, i64, i64, i64, i64]
         L.oracle_cache_offset.restype = i64
+        sp = C.POINTER(_ScaleT)
         L.oracle_write_kv.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, i32, i32,
-                                                    i32, i32, i, i, f32, f32]
+                                                    i32, i32, i, i, sp, sp]
         L.oracle_gather_kv.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32, i32,
-                                                     i32, i32, i32, i32, i32, i, i, f32,
-                                                     f32]
+                                                     i32, i32, i32, i32, i32, i, i, sp, sp]
         L.oracle_write_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, i32,
                                                          i32, i32, i32, i]
         L.oracle_write_kv_fast.restype = i
@@ -43,22 +80,26 @@ def lib() -> C.CDLL:
         L.oracle_gather_kv_fast.restype = i
         L.oracle_gather_kv_ragged.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, vp, i,
                                                             vp, i, i32, i32, i32, i32, i32,
-                                                            i32, i, i, f32, f32]
+                                                            i32, i, i, sp, sp]
         L.oracle_gather_kv_offsets.argtypes = geom + geom + [vp, vp, i64, vp, vp, vp, vp, i,
                                                              i32, i32, i32, i32, i32, i32,
-                                                             i32, i, i, f32, f32]
+                                                             i32, i, i, sp, sp]
         L.oracle_f32_to_e4m3.argtypes = [f32]
         L.oracle_f32_to_e4m3.restype = C.c_uint8
         L.oracle_e4m3_to_f32.argtypes = [C.c_uint8]
         L.oracle_e4m3_to_f32.restype = f32
+        L.oracle_f32_to_e5m2.argtypes = [f32]
+        L.oracle_f32_to_e5m2.restype = C.c_uint8
+        L.oracle_e5m2_to_f32.argtypes = [C.c_uint8]
+        L.oracle_e5m2_to_f32.restype = f32
         L.oracle_f32_to_bf16.argtypes = [f32]
         L.oracle_f32_to_bf16.restype = C.c_uint16
         L.oracle_f32_to_f16.argtypes = [f32]
         L.oracle_f32_to_f16.restype = C.c_uint16
         L.oracle_f16_to_f32.argtypes = [C.c_uint16]
         L.oracle_f16_to_f32.restype = f32
-        L.oracle_quantize_e4m3.argtypes = [vp, i, i64, f32, vp]
-        L.oracle_dequantize_e4m3.argtypes = [vp, i64, f32, i, vp]
+        L.oracle_quantize_fp8.argtypes = [vp, i, i64, f32, i, vp]
+        L.oracle_dequantize_fp8.argtypes = [vp, i64, f32, i, i, vp]
         _LIB = L
     return _LIB
 
@@ -95,11 +136,13 @@ def write_kv(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache, slo
              k_scale=1.0, v_scale=1.0) -> None:
     """Element-wise write (kernels/kvx_paged_kv.cu:93-124), in place."""
     slots = np.ascontiguousarray(slots)
+    kk, ks = _scale_arg(k_scale)
+    vk, vs = _scale_arg(v_scale)
     lib().oracle_write_kv(*gk.args(), *gv.args(), _ptr(key), _ptr(value),
                           _ptr(key_cache), _ptr(value_cache), _ptr(slots),
                           int(slots.dtype == np.int64), int(slots.size), heads,
                           head_dim, block_size, num_blocks, int(io_dtype),
-                          int(cache_dtype), float(k_scale), float(v_scale))
+                          int(cache_dtype), ks, vs)
 
 
 def gather_kv(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value_out,
@@ -111,12 +154,13 @@ def gather_kv(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value
     seq_lens = np.ascontiguousarray(seq_lens)
     if block_table.dtype != seq_lens.dtype:
         raise ValueError("block table and seq_lens share one index dtype")
+    kk, ks = _scale_arg(k_scale)
+    vk, vs = _scale_arg(v_scale)
     lib().oracle_gather_kv(*gk.args(), *gv.args(), _ptr(key_cache), _ptr(value_cache),
                            _ptr(key_out), _ptr(value_out), _ptr(block_table),
                            _ptr(seq_lens), int(block_table.dtype == np.int64),
                            seq_count, max_blocks_per_seq, max_seq_len, heads, head_dim,
-                           block_size, num_blocks, int(cache_dtype), int(io_dtype),
-                           float(k_scale), float(v_scale))
+                           block_size, num_blocks, int(cache_dtype), int(io_dtype), ks, vs)
 
 
 def gather_kv_ragged(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out, value_out,
@@ -126,6 +170,8 @@ def gather_kv_ragged(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out
     indices = np.ascontiguousarray(indices)
     indptr = np.ascontiguousarray(indptr)
     seq_lens = np.ascontiguousarray(seq_lens)
+    kk, ks = _scale_arg(k_scale)
+    vk, vs = _scale_arg(v_scale)
     lib().oracle_gather_kv_ragged(*gk.args(), *gv.args(), _ptr(key_cache), _ptr(value_cache),
                                   _ptr(key_out), _ptr(value_out), _ptr(indices),
                                   int(indices.dtype == np.int64), int(indices.size),
@@ -133,8 +179,7 @@ def gather_kv_ragged(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out
                                   int(indptr.dtype == np.int64), _ptr(seq_lens),
                                   int(seq_lens.dtype == np.int64), int(seq_lens.size),
                                   max_seq_len, heads, head_dim, block_size, num_blocks,
-                                  int(cache_dtype), int(io_dtype), float(k_scale),
-                                  float(v_scale))
+                                  int(cache_dtype), int(io_dtype), ks, vs)
 
 
 def gather_kv_offsets(gk: Geometry, gv: Geometry, pool_primary, pool_secondary,
@@ -146,12 +191,14 @@ def gather_kv_offsets(gk: Geometry, gv: Geometry, pool_primary, pool_secondary,
     table = np.ascontiguousarray(table, dtype=np.int32)
     seq_lens = np.ascontiguousarray(seq_lens)
     sec = None if pool_secondary is None else _ptr(pool_secondary)
+    kk, ks = _scale_arg(k_scale)
+    vk, vs = _scale_arg(v_scale)
     lib().oracle_gather_kv_offsets(*gk.args(), *gv.args(), _ptr(pool_primary), sec,
                                    int(bytes_per_block), _ptr(key_out), _ptr(value_out),
                                    _ptr(table), _ptr(seq_lens), int(seq_lens.dtype == np.int64),
                                    int(seq_lens.size), max_blocks_per_seq, max_seq_len, heads,
                                    head_dim, block_size, num_blocks, int(cache_dtype),
-                                   int(io_dtype), float(k_scale), float(v_scale))
+                                   int(io_dtype), ks, vs)
 
 
 def write_kv_fast(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache, slots,
@@ -175,18 +222,30 @@ def gather_kv_fast(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out,
                                        block_size, num_blocks, elem_size)
 
 
-def quantize_e4m3(x: np.ndarray, io_dtype: int, scale: float) -> np.ndarray:
-    """e4m3(sat(x / scale)) of a raw io buffer (f32 / f16 / bf16 bits)."""
+E4M3, E5M2 = 4, 5  # kvx_abi.h dtype codes of the FP8 formats
+
+
+def quantize_fp8(x: np.ndarray, io_dtype: int, scale: float, fp8: int = E4M3) -> np.ndarray:
+    """fp8(sat(x / scale)) of a raw io buffer (f32 / f16 / bf16 bits)."""
     x = np.ascontiguousarray(x)
     n = x.size
     out = np.empty(n, np.uint8)
-    lib().oracle_quantize_e4m3(_ptr(x), int(io_dtype), n, float(scale), _ptr(out))
+    lib().oracle_quantize_fp8(_ptr(x), int(io_dtype), n, float(scale), int(fp8), _ptr(out))
     return out
 
 
-def dequantize_e4m3(q: np.ndarray, scale: float, io_dtype: int) -> np.ndarray:
+def dequantize_fp8(q: np.ndarray, scale: float, io_dtype: int, fp8: int = E4M3) -> np.ndarray:
     """io(f32(q) * scale) as raw bits (uint32 for F32, uint16 otherwise)."""
     q = np.ascontiguousarray(q, dtype=np.uint8)
     out = np.empty(q.size, np.uint32 if int(io_dtype) == 3 else np.uint16)
-    lib().oracle_dequantize_e4m3(_ptr(q), q.size, float(scale), int(io_dtype), _ptr(out))
+    lib().oracle_dequantize_fp8(_ptr(q), q.size, float(scale), int(fp8), int(io_dtype),
+                                _ptr(out))
     return out
+
+
+def quantize_e4m3(x: np.ndarray, io_dtype: int, scale: float) -> np.ndarray:
+    return quantize_fp8(x, io_dtype, scale, E4M3)
+
+
+def dequantize_e4m3(q: np.ndarray, scale: float, io_dtype: int) -> np.ndarray:
+    return dequantize_fp8(q, scale, io_dtype, E4M3)

@@ -26,14 +26,15 @@
 #endif
 
 enum { L_NHD = 1, L_HND = 2, L_PACKED = 3 };
-enum { D_F16 = 1, D_BF16 = 2, D_F32 = 3, D_E4M3 = 4 };
+enum { D_F16 = 1, D_BF16 = 2, D_F32 = 3, D_E4M3 = 4, D_E5M2 = 5 };
 
 static int dtype_size(int dt) {
   switch (dt) {
     case D_F32: return 4;
     case D_F16:
     case D_BF16: return 2;
-    case D_E4M3: return 1;
+    case D_E4M3:
+    case D_E5M2: return 1;
     default: return 0;
   }
 }
@@ -106,6 +107,36 @@ uint8_t oracle_f32_to_e4m3(float v) {
 float oracle_e4m3_to_f32(uint8_t q) {
   if ((q & 0x7F) == 0x7F) return float_of(0x7FC00000u);
   const double m = e4m3_mag(q & 0x7F);
+  return (float)((q & 0x80) ? -m : m);
+}
+
+/* Magnitude of E5M2 code c (0..123): exponent field e, mantissa m. */
+static double e5m2_mag(int c) {
+  const int e = (c >> 2) & 31, m = c & 3;
+  if (e == 0) return ldexp((double)m, -16);
+  return ldexp(4.0 + m, e - 17);
+}
+
+uint8_t oracle_f32_to_e5m2(float v) {
+  if (isnan(v)) return 0x7E;
+  const uint8_t sign = signbit(v) ? 0x80 : 0x00;
+  const double a = fabs((double)v);
+  if (a >= 57344.0) return sign | 0x7B; /* saturate, infinities included */
+  int lo = 0, hi = 123;                 /* largest code with mag <= a */
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (e5m2_mag(mid) <= a) lo = mid; else hi = mid - 1;
+  }
+  if (e5m2_mag(lo) == a) return sign | (uint8_t)lo;
+  return sign | (uint8_t)nearest(a, (uint32_t)lo, e5m2_mag(lo),
+                                 (uint32_t)lo + 1, e5m2_mag(lo + 1));
+}
+
+float oracle_e5m2_to_f32(uint8_t q) {
+  const int c = q & 0x7F;
+  if (c > 0x7C) return float_of(0x7FC00000u);
+  if (c == 0x7C) return (q & 0x80) ? -INFINITY : INFINITY;
+  const double m = e5m2_mag(c);
   return (float)((q & 0x80) ? -m : m);
 }
 
@@ -202,31 +233,37 @@ static void store_io_f32(uint8_t *p, int dt, float v) {
   }
 }
 
-/* q = e4m3(sat(f32(x) / scale)); the division is one IEEE f32 division. */
-static uint8_t quant_one(const uint8_t *src, int io_dtype, float scale) {
+/* q = fp8(sat(f32(x) / scale)); the division is one IEEE f32 division. */
+static uint8_t quant_one(const uint8_t *src, int io_dtype, int fp8, float scale) {
   const float x = load_io_f32(src, io_dtype);
   volatile float q = x / scale; /* force an f32-rounded quotient */
-  return oracle_f32_to_e4m3(q);
+  return fp8 == D_E5M2 ? oracle_f32_to_e5m2(q) : oracle_f32_to_e4m3(q);
 }
 
 /* y = io(f32(q) * scale); the product is one IEEE f32 multiplication. */
-static void dequant_one(uint8_t q, float scale, int io_dtype, uint8_t *dst) {
-  volatile float y = oracle_e4m3_to_f32(q) * scale;
+static void dequant_one(uint8_t q, int fp8, float scale, int io_dtype, uint8_t *dst) {
+  volatile float y = (fp8 == D_E5M2 ? oracle_e5m2_to_f32(q) : oracle_e4m3_to_f32(q)) * scale;
   store_io_f32(dst, io_dtype, y);
 }
 
-void oracle_quantize_e4m3(const void *in, int io_dtype, int64_t n, float scale,
-                          uint8_t *out) {
-  const int es = dtype_size(io_dtype);
-  for (int64_t i = 0; i < n; ++i)
-    out[i] = quant_one((const uint8_t *)in + i * es, io_dtype, scale);
+/* Scale of (block b, head h); 1 without a scale. */
+static float scale_at(const oracle_scale_t *s, int64_t b, int64_t h) {
+  if (s == NULL || s->p == NULL) return 1.0f;
+  return s->p[b * s->s_block + h * s->s_head];
 }
 
-void oracle_dequantize_e4m3(const uint8_t *in, int64_t n, float scale,
-                            int io_dtype, void *out) {
+void oracle_quantize_fp8(const void *in, int io_dtype, int64_t n, float scale,
+                         int fp8_dtype, uint8_t *out) {
   const int es = dtype_size(io_dtype);
   for (int64_t i = 0; i < n; ++i)
-    dequant_one(in[i], scale, io_dtype, (uint8_t *)out + i * es);
+    out[i] = quant_one((const uint8_t *)in + i * es, io_dtype, fp8_dtype, scale);
+}
+
+void oracle_dequantize_fp8(const uint8_t *in, int64_t n, float scale, int fp8_dtype,
+                           int io_dtype, void *out) {
+  const int es = dtype_size(io_dtype);
+  for (int64_t i = 0; i < n; ++i)
+    dequant_one(in[i], fp8_dtype, scale, io_dtype, (uint8_t *)out + i * es);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -244,7 +281,8 @@ void oracle_write_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                      void *value_cache, const void *slots, int slot_is64,
                      int64_t num_tokens, int32_t heads, int32_t head_dim,
                      int32_t block_size, int32_t num_blocks, int io_dtype,
-                     int cache_dtype, float k_scale, float v_scale) {
+                     int cache_dtype, const oracle_scale_t *k_scale,
+                     const oracle_scale_t *v_scale) {
   const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
   const int quant = io_dtype != cache_dtype;
   const uint8_t *k_in = key, *v_in = value;
@@ -261,8 +299,8 @@ void oracle_write_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
         const int64_t ko = oracle_cache_offset(k_layout, k_stride, k_pack, b, o, h, d);
         const int64_t vo = oracle_cache_offset(v_layout, v_stride, v_pack, b, o, h, d);
         if (quant) {
-          kc[ko] = quant_one(k_in + idx * is, io_dtype, k_scale);
-          vc[vo] = quant_one(v_in + idx * is, io_dtype, v_scale);
+          kc[ko] = quant_one(k_in + idx * is, io_dtype, cache_dtype, scale_at(k_scale, b, h));
+          vc[vo] = quant_one(v_in + idx * is, io_dtype, cache_dtype, scale_at(v_scale, b, h));
         } else {
           memcpy(kc + ko * cs, k_in + idx * is, (size_t)cs);
           memcpy(vc + vo * cs, v_in + idx * is, (size_t)cs);
@@ -281,7 +319,7 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                       int32_t max_blocks_per_seq, int32_t max_seq_len,
                       int32_t heads, int32_t head_dim, int32_t block_size,
                       int32_t num_blocks, int cache_dtype, int io_dtype,
-                      float k_scale, float v_scale) {
+                      const oracle_scale_t *k_scale, const oracle_scale_t *v_scale) {
   const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
   const int dequant = io_dtype != cache_dtype;
   const uint8_t *kc = key_cache, *vc = value_cache;
@@ -305,8 +343,10 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
           const int64_t vo =
               oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d);
           if (dequant) {
-            dequant_one(kc[ko], k_scale, io_dtype, ko_ + idx * is);
-            dequant_one(vc[vo], v_scale, io_dtype, vo_ + idx * is);
+            dequant_one(kc[ko], cache_dtype, scale_at(k_scale, bid, h), io_dtype,
+                        ko_ + idx * is);
+            dequant_one(vc[vo], cache_dtype, scale_at(v_scale, bid, h), io_dtype,
+                        vo_ + idx * is);
           } else {
             memcpy(ko_ + idx * is, kc + ko * cs, (size_t)cs);
             memcpy(vo_ + idx * is, vc + vo * cs, (size_t)cs);
@@ -319,9 +359,9 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
 
 /* One element of a row: copy or dequantize from `src` to `dst`. */
 static void move_elem(const uint8_t *src, uint8_t *dst, int dequant, int cs, int is,
-                      int io_dtype, float scale) {
+                      int cache_dtype, int io_dtype, float scale) {
   if (dequant) {
-    dequant_one(*src, scale, io_dtype, dst);
+    dequant_one(*src, cache_dtype, scale, io_dtype, dst);
   } else {
     memcpy(dst, src, (size_t)(cs < is ? cs : is));
   }
@@ -336,7 +376,8 @@ void oracle_gather_kv_ragged(int k_layout, const int64_t *k_stride, int64_t k_pa
                              int indptr_is64, const void *seq_lens, int lens_is64,
                              int32_t seq_count, int32_t max_seq_len, int32_t heads,
                              int32_t head_dim, int32_t block_size, int32_t num_blocks,
-                             int cache_dtype, int io_dtype, float k_scale, float v_scale) {
+                             int cache_dtype, int io_dtype, const oracle_scale_t *k_scale,
+                             const oracle_scale_t *v_scale) {
   const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
   const int dequant = io_dtype != cache_dtype;
   const uint8_t *kc = key_cache, *vc = value_cache;
@@ -355,8 +396,10 @@ void oracle_gather_kv_ragged(int k_layout, const int64_t *k_stride, int64_t k_pa
           const int64_t idx = ((s * max_seq_len + t) * heads + h) * head_dim + d;
           const int64_t ko = oracle_cache_offset(k_layout, k_stride, k_pack, bid, o, h, d);
           const int64_t vo = oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d);
-          move_elem(kc + ko * cs, ko_ + idx * is, dequant, cs, is, io_dtype, k_scale);
-          move_elem(vc + vo * cs, vo_ + idx * is, dequant, cs, is, io_dtype, v_scale);
+          move_elem(kc + ko * cs, ko_ + idx * is, dequant, cs, is, cache_dtype, io_dtype,
+                    scale_at(k_scale, bid, h));
+          move_elem(vc + vo * cs, vo_ + idx * is, dequant, cs, is, cache_dtype, io_dtype,
+                    scale_at(v_scale, bid, h));
         }
       }
     }
@@ -372,7 +415,8 @@ void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_p
                               int32_t seq_count, int32_t max_blocks_per_seq,
                               int32_t max_seq_len, int32_t heads, int32_t head_dim,
                               int32_t block_size, int32_t num_blocks, int cache_dtype,
-                              int io_dtype, float k_scale, float v_scale) {
+                              int io_dtype, const oracle_scale_t *k_scale,
+                              const oracle_scale_t *v_scale) {
   const int is = dtype_size(io_dtype), cs = dtype_size(cache_dtype);
   const int dequant = io_dtype != cache_dtype;
   const uint8_t *pools[2] = {pool_primary, pool_secondary};
@@ -380,7 +424,7 @@ void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_p
   const int layouts[2] = {k_layout, v_layout};
   const int64_t *strides[2] = {k_stride, v_stride};
   const int64_t packs[2] = {k_pack, v_pack};
-  const float scales[2] = {k_scale, v_scale};
+  const oracle_scale_t *scales[2] = {k_scale, v_scale};
   for (int64_t s = 0; s < seq_count; ++s) {
     const int64_t seq_len = load_index(seq_lens, s, lens_is64);
     for (int64_t t = 0; t < max_seq_len; ++t) {
@@ -399,8 +443,8 @@ void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_p
             const int64_t idx = ((s * max_seq_len + t) * heads + h) * head_dim + d;
             const int64_t off = oracle_cache_offset(layouts[kv], strides[kv], packs[kv], 0, o,
                                                     h, d);
-            move_elem(base + off * cs, outs[kv] + idx * is, dequant, cs, is, io_dtype,
-                      scales[kv]);
+            move_elem(base + off * cs, outs[kv] + idx * is, dequant, cs, is, cache_dtype,
+                      io_dtype, scale_at(scales[kv], blk, h));
           }
         }
       }

@@ -24,23 +24,33 @@ extern "C" {
 
 /* Layout codes and dtype codes are the kvx_abi.h enum values. */
 
+/* FP8 scales: the scale of element (block b, head h) is
+ * p[b * s_block + h * s_head] (strides in elements; a per-tensor scale has
+ * both strides 0). */
+typedef struct oracle_scale {
+  const float *p;
+  int64_t s_block;
+  int64_t s_head;
+} oracle_scale_t;
+
 int64_t oracle_cache_offset(int layout, const int64_t *stride, int64_t pack,
                             int64_t block, int64_t offset, int64_t head,
                             int64_t dim);
 
 /* Element-wise write.  io and cache dtypes are equal (bit copy) or the cache
- * is F8_E4M3 and io is F16/BF16/F32 (quantize with k_scale / v_scale). */
+ * is F8_E4M3 / F8_E5M2 and io is F16/BF16/F32 (quantize with k_scale /
+ * v_scale, which may be NULL for a bit copy). */
 void oracle_write_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                      int v_layout, const int64_t *v_stride, int64_t v_pack,
                      const void *key, const void *value, void *key_cache,
                      void *value_cache, const void *slots, int slot_is64,
                      int64_t num_tokens, int32_t heads, int32_t head_dim,
                      int32_t block_size, int32_t num_blocks, int io_dtype,
-                     int cache_dtype, float k_scale, float v_scale);
+                     int cache_dtype, const oracle_scale_t *k_scale, const oracle_scale_t *v_scale);
 
 /* Element-wise gather into [seq_count, max_seq_len, H, D].  Rows not
  * written by the reference semantics are left untouched.  Dequantizes when
- * the cache is F8_E4M3 and io is F16/BF16/F32. */
+ * the cache is F8_E4M3 / F8_E5M2 and io is F16/BF16/F32. */
 void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                       int v_layout, const int64_t *v_stride, int64_t v_pack,
                       const void *key_cache, const void *value_cache,
@@ -49,7 +59,7 @@ void oracle_gather_kv(int k_layout, const int64_t *k_stride, int64_t k_pack,
                       int32_t max_blocks_per_seq, int32_t max_seq_len,
                       int32_t heads, int32_t head_dim, int32_t block_size,
                       int32_t num_blocks, int cache_dtype, int io_dtype,
-                      float k_scale, float v_scale);
+                      const oracle_scale_t *k_scale, const oracle_scale_t *v_scale);
 
 /* RAGGED table gather (KVX_SPEC.md:107-114): row t of sequence s is token
  * i = indptr[s] + t for t < min(seq_len, indptr[s+1] - indptr[s],
@@ -64,7 +74,7 @@ void oracle_gather_kv_ragged(int k_layout, const int64_t *k_stride, int64_t k_pa
                              int indptr_is64, const void *seq_lens, int lens_is64,
                              int32_t seq_count, int32_t max_seq_len, int32_t heads,
                              int32_t head_dim, int32_t block_size, int32_t num_blocks,
-                             int cache_dtype, int io_dtype, float k_scale, float v_scale);
+                             int cache_dtype, int io_dtype, const oracle_scale_t *k_scale, const oracle_scale_t *v_scale);
 
 /* KV_OFFSETS table gather (KVX_SPEC.md:116-122, KV_CACHE_LAYOUTS.md:89-94):
  * table [seq_count, 1, 2, max_blocks_per_seq] of int32 KVCacheIndex values,
@@ -81,7 +91,7 @@ void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_p
                               int32_t seq_count, int32_t max_blocks_per_seq,
                               int32_t max_seq_len, int32_t heads, int32_t head_dim,
                               int32_t block_size, int32_t num_blocks, int cache_dtype,
-                              int io_dtype, float k_scale, float v_scale);
+                              int io_dtype, const oracle_scale_t *k_scale, const oracle_scale_t *v_scale);
 
 /* Same results as the element-wise functions for bit-copy calls, with one
  * memcpy per contiguous run and OpenMP over tokens / (sequence, block); the
@@ -103,18 +113,22 @@ int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
                           int32_t heads, int32_t head_dim, int32_t block_size,
                           int32_t num_blocks, int elem_size);
 
-/* Scalar casts (OCP E4M3, bf16, f16), by nearest-value search. */
+/* Scalar casts (OCP E4M3 and E5M2, bf16, f16), by nearest-value search.
+ * FP8 casts saturate to the largest finite value (infinities included). */
 uint8_t oracle_f32_to_e4m3(float v);
 float oracle_e4m3_to_f32(uint8_t q);
+uint8_t oracle_f32_to_e5m2(float v);
+float oracle_e5m2_to_f32(uint8_t q);
 uint16_t oracle_f32_to_bf16(float v);
 uint16_t oracle_f32_to_f16(float v);
 float oracle_f16_to_f32(uint16_t h);
 
-/* Array versions for tests: out[i] = cast(in[i] / scale) etc. */
-void oracle_quantize_e4m3(const void *in, int io_dtype, int64_t n, float scale,
-                          uint8_t *out);
-void oracle_dequantize_e4m3(const uint8_t *in, int64_t n, float scale,
-                            int io_dtype, void *out);
+/* Array versions for tests: out[i] = cast(in[i] / scale) etc.; fp8_dtype is
+ * F8_E4M3 or F8_E5M2. */
+void oracle_quantize_fp8(const void *in, int io_dtype, int64_t n, float scale,
+                         int fp8_dtype, uint8_t *out);
+void oracle_dequantize_fp8(const uint8_t *in, int64_t n, float scale, int fp8_dtype,
+                           int io_dtype, void *out);
 
 #ifdef __cplusplus
 }

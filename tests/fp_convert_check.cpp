@@ -71,6 +71,45 @@ int main() {
   }
   printf("e4m3_to_f32 %ld of %ld\n", bad, n);
 
+  // f32 -> e5m2: the same input classes, around every e5m2 value and
+  // midpoint, the saturation threshold and infinity.
+  bad = n = 0;
+  auto chk5 = [&](float v) {
+    ++n;
+    if (f32_to_e5m2(v) != oracle_f32_to_e5m2(v)) {
+      if (bad < 5) fprintf(stderr, "e5m2 %08x: %02x vs %02x\n", f32_bits(v),
+                           f32_to_e5m2(v), oracle_f32_to_e5m2(v));
+      ++bad;
+    }
+  };
+  for (float s : scales) {
+    for (uint32_t h = 0; h < 65536; ++h) {
+      volatile float q1 = bf16_to_f32((uint16_t)h) / s;
+      chk5(q1);
+      volatile float q2 = oracle_f16_to_f32((uint16_t)h) / s;
+      chk5(q2);
+    }
+  }
+  for (int i = 0; i < (1 << 22); ++i) chk5(f_of((uint32_t)rng()));
+  for (int c = 0; c < 124; ++c) {
+    const float v = oracle_e5m2_to_f32((uint8_t)c);
+    around(v, 64, chk5);
+    around(-v, 64, chk5);
+    const float mid = (float)(((double)v + (double)oracle_e5m2_to_f32((uint8_t)(c + 1))) / 2);
+    if (c < 123) { around(mid, 64, chk5); around(-mid, 64, chk5); }
+  }
+  around(57344.0f, 1 << 16, chk5);
+  around(INFINITY, 4, chk5);
+  printf("f32_to_e5m2 %ld of %ld\n", bad, n);
+
+  bad = n = 0;
+  for (int c = 0; c < 256; ++c) {
+    ++n;
+    const float a = e5m2_to_f32((uint8_t)c), b = oracle_e5m2_to_f32((uint8_t)c);
+    if (f32_bits(a) != f32_bits(b)) ++bad;
+  }
+  printf("e5m2_to_f32 %ld of %ld\n", bad, n);
+
   bad = n = 0;
   auto chkb = [&](float v) {
     ++n;

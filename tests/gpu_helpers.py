@@ -11,7 +11,47 @@ from kvx_amd import paged
 from kvx_amd.abi import DType, Layout, Status, contiguous_strides
 
 TORCH_DT = {DType.F32: torch.float32, DType.F16: torch.float16,
-            DType.BF16: torch.bfloat16, DType.F8_E4M3: torch.float8_e4m3fn}
+            DType.BF16: torch.bfloat16, DType.F8_E4M3: torch.float8_e4m3fn,
+            DType.F8_E5M2: torch.float8_e5m2}
+
+
+class ScaleArg:
+    """Indexed FP8 scales for a test: `values` (float32, [H], [nb] or
+    [nb, H]) stored on the device with `stride` (elements; None =
+    contiguous), handed to the library as a paged.Scales and to the oracle
+    as an oracle.Scale with the same strides."""
+
+    def __init__(self, granularity, values, stride=None, device="cuda"):
+        from kvx_amd.abi import ScaleGranularity as SG
+
+        self.granularity = SG(granularity)
+        vals = np.asarray(values, dtype=np.float32)
+        if stride is None:
+            stride = contiguous_strides(vals.shape)
+        stride = tuple(int(x) for x in stride)
+        n = 1 + sum((d - 1) * st for d, st in zip(vals.shape, stride))
+        host = torch.full((n,), float("nan"), dtype=torch.float32)  # gaps unused
+        torch.as_strided(host, vals.shape, stride).copy_(torch.from_numpy(vals))
+        self.dev = torch.as_strided(host.to(device), vals.shape, stride)
+        flat = host.numpy()
+        if self.granularity == SG.PER_HEAD:
+            self.oracle = oracle.Scale(flat, 0, stride[0])
+        elif self.granularity == SG.PER_BLOCK:
+            self.oracle = oracle.Scale(flat, stride[0], 0)
+        else:
+            self.oracle = oracle.Scale(flat, stride[0], stride[1])
+
+    def device(self):
+        return paged.Scales(self.dev, self.granularity)
+
+
+def _dev_scale(x, device):
+    """(library scale, oracle scale) for None / float / ScaleArg."""
+    if x is None:
+        return None, 1.0
+    if isinstance(x, ScaleArg):
+        return x.device(), x.oracle
+    return torch.tensor([x], dtype=torch.float32, device=device), x
 
 
 def np_bytes(t: torch.Tensor) -> np.ndarray:
@@ -63,10 +103,8 @@ def check_write(pc, kbuf, vbuf, key, value, slots, *, io_dtype, cache_dtype,
     """Run the write on the GPU and in the oracle from identical inputs and
     require bit-identical caches (touched and untouched bytes alike)."""
     kb0, vb0 = np_bytes(kbuf.base), np_bytes(vbuf.base)
-    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
-                                                   device=key.device)
-    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
-                                                   device=key.device)
+    ks, k_or = _dev_scale(k_scale, key.device)
+    vs, v_or = _dev_scale(v_scale, key.device)
     st = paged.write_kv(pc, key, value, slots, tokens_per_seq=tokens_per_seq,
                         k_scale=ks, v_scale=vs, entry=entry, stream=stream)
     assert st == Status.OK, st
@@ -74,9 +112,7 @@ def check_write(pc, kbuf, vbuf, key, value, slots, *, io_dtype, cache_dtype,
     oracle.write_kv(kbuf.geometry(), vbuf.geometry(), np_bytes(key), np_bytes(value),
                     kb0, vb0, slots.cpu().numpy(), heads=pc.heads, head_dim=pc.head_dim,
                     block_size=pc.block_size, num_blocks=pc.num_blocks,
-                    io_dtype=io_dtype, cache_dtype=cache_dtype,
-                    k_scale=1.0 if k_scale is None else k_scale,
-                    v_scale=1.0 if v_scale is None else v_scale)
+                    io_dtype=io_dtype, cache_dtype=cache_dtype, k_scale=k_or, v_scale=v_or)
     got_k, got_v = np_bytes(kbuf.base), np_bytes(vbuf.base)
     assert np.array_equal(got_k, kb0), _first_diff(got_k, kb0)
     assert np.array_equal(got_v, vb0), _first_diff(got_v, vb0)
@@ -88,10 +124,8 @@ def check_gather(pc, kbuf, vbuf, key_out, value_out, table, lens, max_seq_len, *
     """Run the gather on the GPU and in the oracle from identical inputs (the
     outputs pre-filled with random bytes) and require bit-identical outputs."""
     ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
-    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
-                                                   device=key_out.device)
-    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
-                                                   device=key_out.device)
+    ks, k_or = _dev_scale(k_scale, key_out.device)
+    vs, v_or = _dev_scale(v_scale, key_out.device)
     st = paged.gather_kv(pc, key_out, value_out, table, lens, max_seq_len, k_scale=ks,
                          v_scale=vs, entry=entry, stream=stream)
     assert st == Status.OK, st
@@ -102,8 +136,7 @@ def check_gather(pc, kbuf, vbuf, key_out, value_out, table, lens, max_seq_len, *
                      seq_count=S, max_blocks_per_seq=mbps, max_seq_len=max_seq_len,
                      heads=pc.heads, head_dim=pc.head_dim, block_size=pc.block_size,
                      num_blocks=pc.num_blocks, cache_dtype=cache_dtype, io_dtype=io_dtype,
-                     k_scale=1.0 if k_scale is None else k_scale,
-                     v_scale=1.0 if v_scale is None else v_scale)
+                     k_scale=k_or, v_scale=v_or)
     got_k, got_v = np_bytes(key_out), np_bytes(value_out)
     assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
     assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)
@@ -114,20 +147,13 @@ def _first_diff(a: np.ndarray, b: np.ndarray) -> str:
     return f"{idx.size} bytes differ, first at {idx[:8].tolist()}"
 
 
-def _scales(k_scale, v_scale, device):
-    ks = None if k_scale is None else torch.tensor([k_scale], dtype=torch.float32,
-                                                   device=device)
-    vs = None if v_scale is None else torch.tensor([v_scale], dtype=torch.float32,
-                                                   device=device)
-    return ks, vs
-
-
 def check_gather_ragged(pc, kbuf, vbuf, key_out, value_out, table: paged.RaggedTable, lens,
                         max_seq_len, *, cache_dtype, io_dtype, k_scale=None, v_scale=None,
                         entry="launch"):
     """RAGGED-table gather on the GPU and in the oracle; bit-identical outputs."""
     ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
-    ks, vs = _scales(k_scale, v_scale, key_out.device)
+    ks, k_or = _dev_scale(k_scale, key_out.device)
+    vs, v_or = _dev_scale(v_scale, key_out.device)
     st = paged.gather_kv(pc, key_out, value_out, table, lens, max_seq_len, k_scale=ks,
                          v_scale=vs, entry=entry)
     assert st == Status.OK, st
@@ -138,8 +164,7 @@ def check_gather_ragged(pc, kbuf, vbuf, key_out, value_out, table: paged.RaggedT
                             max_seq_len=max_seq_len, heads=pc.heads, head_dim=pc.head_dim,
                             block_size=pc.block_size, num_blocks=pc.num_blocks,
                             cache_dtype=cache_dtype, io_dtype=io_dtype,
-                            k_scale=1.0 if k_scale is None else k_scale,
-                            v_scale=1.0 if v_scale is None else v_scale)
+                            k_scale=k_or, v_scale=v_or)
     got_k, got_v = np_bytes(key_out), np_bytes(value_out)
     assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
     assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)
@@ -185,7 +210,8 @@ def check_gather_offsets(pool: OffsetsPool, key_out, value_out, offsets, lens, m
     outputs."""
     pc = pool.pc
     ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
-    ks, vs = _scales(k_scale, v_scale, key_out.device)
+    ks, k_or = _dev_scale(k_scale, key_out.device)
+    vs, v_or = _dev_scale(v_scale, key_out.device)
     st = paged.gather_kv(pc, key_out, value_out, pool.table(offsets), lens, max_seq_len,
                          k_scale=ks, v_scale=vs, entry=entry)
     assert st == Status.OK, st
@@ -197,8 +223,7 @@ def check_gather_offsets(pool: OffsetsPool, key_out, value_out, offsets, lens, m
                              max_seq_len=max_seq_len, heads=pc.heads, head_dim=pc.head_dim,
                              block_size=pc.block_size, num_blocks=pc.num_blocks,
                              cache_dtype=cache_dtype, io_dtype=io_dtype,
-                             k_scale=1.0 if k_scale is None else k_scale,
-                             v_scale=1.0 if v_scale is None else v_scale)
+                             k_scale=k_or, v_scale=v_or)
     got_k, got_v = np_bytes(key_out), np_bytes(value_out)
     assert np.array_equal(got_k, ko0), _first_diff(got_k, ko0)
     assert np.array_equal(got_v, vo0), _first_diff(got_v, vo0)

@@ -90,7 +90,8 @@ def run_and_check(key, value, kc, vc, slots, bs, kv_cache_dtype="auto", ks=None,
     nb, _, H, D = kc.shape
     io_dt = TDT[key.dtype]
     fp8 = kv_cache_dtype != "auto"
-    cache_dt = DType.F8_E4M3 if fp8 else io_dt
+    e5m2 = kv_cache_dtype == "fp8_e5m2"
+    cache_dt = (DType.F8_E5M2 if e5m2 else DType.F8_E4M3) if fp8 else io_dt
     want_k = oracle_expect(kc, key, slots, bs, nb, H, D, io_dt, cache_dt,
                            ks.item() if fp8 else 1.0)
     want_v = oracle_expect(vc, value, slots, bs, nb, H, D, io_dt, cache_dt,
@@ -98,8 +99,9 @@ def run_and_check(key, value, kc, vc, slots, bs, kv_cache_dtype="auto", ks=None,
     ref_k, ref_v = kc.clone(), vc.clone()
     if fp8:
         # torch's own cast, on the CPU (IEEE f32 division), after saturation
-        qk = (key.float().cpu() / ks.cpu()).clamp(-448, 448).to(torch.float8_e4m3fn)
-        qv = (value.float().cpu() / vs.cpu()).clamp(-448, 448).to(torch.float8_e4m3fn)
+        f8, top = (torch.float8_e5m2, 57344.0) if e5m2 else (torch.float8_e4m3fn, 448.0)
+        qk = (key.float().cpu() / ks.cpu()).clamp(-top, top).to(f8)
+        qv = (value.float().cpu() / vs.cpu()).clamp(-top, top).to(f8)
         qk, qv = qk.view(torch.uint8).to(DEV), qv.view(torch.uint8).to(DEV)
         torch_scatter(ref_k, qk, slots, bs)
         torch_scatter(ref_v, qv, slots, bs)
@@ -155,8 +157,10 @@ def test_rows_past_slot_mapping_are_ignored():
     run_and_check(key, value, kc, vc, rand_slots(nb, bs, 37, torch.int64, gen), bs)
 
 
-@pytest.mark.parametrize("kv_cache_dtype", ["fp8", "fp8_e4m3"])
-@pytest.mark.parametrize("storage", [torch.uint8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("kv_cache_dtype,storage", [
+    ("fp8", torch.uint8), ("fp8", torch.float8_e4m3fn), ("fp8_e4m3", torch.uint8),
+    ("fp8_e4m3", torch.float8_e4m3fn), ("fp8_e5m2", torch.uint8),
+    ("fp8_e5m2", torch.float8_e5m2)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fp8_cache(kv_cache_dtype, storage, dtype):
     gen = torch.Generator().manual_seed(5)
@@ -166,8 +170,9 @@ def test_fp8_cache(kv_cache_dtype, storage, dtype):
     layout = "NHD" if storage == torch.uint8 else "HND"
     kc = vllm_cache(nb, bs, H, D, storage, layout, gen)
     vc = vllm_cache(nb, bs, H, D, storage, layout, gen)
-    ks = (key.float().abs().amax() / 448.0).reshape(1)
-    vs = (value.float().abs().amax() / 300.0).reshape(1)   # some values saturate
+    top = 57344.0 if kv_cache_dtype == "fp8_e5m2" else 448.0
+    ks = (key.float().abs().amax() / top).reshape(1)
+    vs = (value.float().abs().amax() / (top * 0.7)).reshape(1)   # some values saturate
     run_and_check(key, value, kc, vc, rand_slots(nb, bs, T, torch.int64, gen), bs,
                   kv_cache_dtype, ks, vs)
 
@@ -200,7 +205,9 @@ def test_argument_checks():
     one = torch.ones(1, device=DEV)
     kc8 = torch.zeros(nb, bs, H, D, dtype=torch.uint8, device=DEV)
     cases = [
-        ((key, key, kc, kc.clone(), slots, "fp8_e5m2", one, one), "kv_cache_dtype"),
+        ((key, key, kc, kc.clone(), slots, "fp8_e4m3fnuz", one, one), "kv_cache_dtype"),
+        ((key, key, kc.to(torch.float8_e4m3fn), kc.to(torch.float8_e4m3fn), slots, "fp8_e5m2",
+          one, one), "matching float8"),
         ((key, key.float(), kc, kc.clone(), slots, "auto", one, one), "key/value dtype mismatch"),
         ((key, key, kc, kc.float(), slots, "auto", one, one), "cache dtype mismatch"),
         ((key, key, kc.float(), kc.float(), slots, "auto", one, one),

@@ -60,10 +60,14 @@ def test_write_dispatch(kvx_lib):
     assert W(kvx_lib, c, None) == INV
     c.v.dtype = DType.F16
     assert W(kvx_lib, c, w) == INV                          # :478 k != v dtype
-    for dt in (DType.U8, DType.S32, DType.F8_E5M2, DType.INVALID):
+    for dt in (DType.U8, DType.S32, DType.INVALID):
         c, w = base_write()
         c.k.dtype = c.v.dtype = dt
         assert W(kvx_lib, c, w) == UNS, dt                  # :488
+    # FP8 caches are this build's extension: with bf16 io they need scales
+    for dt in (DType.F8_E4M3, DType.F8_E5M2):
+        c, w = base_write(dt=dt, io_dt=DType.BF16)
+        assert W(kvx_lib, c, w) == INV, dt
 
 
 @pytest.mark.parametrize("fn", ["kvx_launch_write_kv", "kvx_launch_write_kv_bf16"])
@@ -184,7 +188,7 @@ def test_fp8_write_validation(kvx_lib):
     w.v_scale = FAKE
     assert W(kvx_lib, c, w) == UNS
     c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
-    w.k_scale_desc = abi.scale_desc(FAKE, granularity=ScaleGranularity.PER_HEAD)
+    w.k_scale_desc = abi.scale_desc(FAKE, granularity=ScaleGranularity.NONE)
     w.v_scale = FAKE
     assert W(kvx_lib, c, w) == UNS
     c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16)
@@ -204,6 +208,52 @@ def test_fp8_write_validation(kvx_lib):
     c, w = base_write(dt=DType.F8_E4M3, io_dt=DType.BF16, T=0)
     w.k_scale = w.v_scale = FAKE
     assert W(kvx_lib, c, w) == OK
+    c, w = base_write(dt=DType.F8_E5M2, io_dt=DType.F8_E5M2, T=0)
+    assert W(kvx_lib, c, w) == OK                            # byte copy, no scale
+
+
+# base_write / base_gather caches: 4 blocks, 2 heads
+GOOD_SCALES = [(ScaleGranularity.PER_TENSOR, (1,)), (ScaleGranularity.PER_HEAD, (2,)),
+               (ScaleGranularity.PER_BLOCK, (4,)), (ScaleGranularity.PER_BLOCK_HEAD, (4, 2))]
+BAD_SHAPES = [(ScaleGranularity.PER_HEAD, (3,)), (ScaleGranularity.PER_HEAD, (2, 1)),
+              (ScaleGranularity.PER_BLOCK, (2,)), (ScaleGranularity.PER_BLOCK_HEAD, (2, 4)),
+              (ScaleGranularity.PER_BLOCK_HEAD, (4,))]
+
+
+@pytest.mark.parametrize("dt", [DType.F8_E4M3, DType.F8_E5M2])
+def test_fp8_scale_granularities(kvx_lib, dt):
+    """Scale shapes (this build's reading of KVX_SPEC.md:190-197): accepted
+    shapes resolve (empty batch -> OK, no launch), wrong shapes are
+    INVALID_ARGUMENT, other granularities and dtypes UNSUPPORTED."""
+    for gran, shape in GOOD_SCALES:
+        c, w = base_write(dt=dt, io_dt=DType.F16, T=0)
+        w.k_scale_desc = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        w.v_scale_desc = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        assert W(kvx_lib, c, w) == OK, gran
+    for gran, shape in BAD_SHAPES:
+        c, w = base_write(dt=dt, io_dt=DType.F16)
+        w.k_scale_desc = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        w.v_scale = FAKE
+        assert W(kvx_lib, c, w) == INV, (gran, shape)
+    for gran in (ScaleGranularity.NONE, 7):
+        c, w = base_write(dt=dt, io_dt=DType.F16)
+        w.k_scale_desc = abi.scale_desc(FAKE, granularity=gran)
+        w.v_scale = FAKE
+        assert W(kvx_lib, c, w) == UNS, gran
+    f = kvx_lib.kvx_launch_gather_kv_dequant
+    for gran, shape in GOOD_SCALES:
+        c, g = base_gather(dt=dt, io_dt=DType.BF16, L=0)
+        k = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        assert Status(f(abi.ref(c), abi.ref(g), abi.ref(k), abi.ref(k), None)) == OK, gran
+    for gran, shape in BAD_SHAPES:
+        c, g = base_gather(dt=dt, io_dt=DType.BF16)
+        k = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        assert Status(f(abi.ref(c), abi.ref(g), abi.ref(k), abi.ref(k), None)) == INV
+    # KV_OFFSETS has no physical block ids for block-indexed scales
+    for gran, shape in GOOD_SCALES[2:]:
+        c, g = offsets_gather(dt=dt, io_dt=DType.BF16)
+        k = abi.scale_desc(FAKE, granularity=gran, shape=shape)
+        assert Status(f(abi.ref(c), abi.ref(g), abi.ref(k), abi.ref(k), None)) == UNS
 
 
 # ---------------------------------------------------------------------------
@@ -278,7 +328,7 @@ def test_dequant_gather_validation(kvx_lib):
     c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.F8_E4M3)
     assert call(c, g) == UNS
     c, g = base_gather(dt=DType.F8_E4M3, io_dt=DType.BF16)
-    bad = abi.scale_desc(FAKE, granularity=ScaleGranularity.PER_BLOCK)
+    bad = abi.scale_desc(FAKE, granularity=ScaleGranularity.NONE)
     assert call(c, g, v=bad) == UNS
     bad = abi.scale_desc(None)
     assert call(c, g, k=bad) == INV

@@ -29,8 +29,9 @@ from kvx_amd.abi import contiguous_strides
 from conftest import REPO
 
 GOLDEN = REPO / "tests" / "golden" / "fp8_e4m3_golden.npz"
+GOLDEN_E5M2 = REPO / "tests" / "golden" / "fp8_e5m2_golden.npz"
 NP_DT = {DType.F32: np.float32, DType.F16: np.float16, DType.BF16: np.uint16,
-         DType.F8_E4M3: np.uint8}
+         DType.F8_E4M3: np.uint8, DType.F8_E5M2: np.uint8}
 
 
 def geom(layout, nb, bs, H, D, pack=8, shape_strides=None):
@@ -327,6 +328,49 @@ def test_e4m3_special_values():
     assert np.isnan(L.oracle_e4m3_to_f32(0xFF))
 
 
+@pytest.fixture(scope="module")
+def golden_e5m2():
+    return np.load(GOLDEN_E5M2, allow_pickle=False)
+
+
+def test_e5m2_quantize_matches_torch_golden(golden_e5m2):
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    for i, s in enumerate(golden_e5m2["scales"]):
+        for dt, key in [(DType.BF16, "quant_from_bf16"), (DType.F16, "quant_from_f16")]:
+            got = oracle.quantize_fp8(bits, dt, float(s), oracle.E5M2)
+            assert np.array_equal(got, golden_e5m2[key][i]), (float(s), key)
+
+
+def test_e5m2_dequantize_matches_torch_golden(golden_e5m2):
+    codes = np.arange(256, dtype=np.uint8)
+    for i, s in enumerate(golden_e5m2["scales"]):
+        for dt, key in [(DType.BF16, "dequant_bf16"), (DType.F16, "dequant_f16"),
+                        (DType.F32, "dequant_f32")]:
+            got = oracle.dequantize_fp8(codes, float(s), dt, oracle.E5M2)
+            assert np.array_equal(got, golden_e5m2[key][i]), (float(s), key)
+
+
+def test_e5m2_special_values():
+    L = oracle.lib()
+    assert L.oracle_f32_to_e5m2(57344.0) == 0x7B
+    assert L.oracle_f32_to_e5m2(61440.0) == 0x7B         # would round to inf: saturates
+    assert L.oracle_f32_to_e5m2(float("-inf")) == 0xFB
+    assert L.oracle_f32_to_e5m2(float("nan")) == 0x7E
+    assert L.oracle_f32_to_e5m2(2.0 ** -16) == 0x01      # smallest subnormal
+    assert L.oracle_f32_to_e5m2(2.0 ** -17) == 0x00      # tie -> even (0)
+    assert L.oracle_f32_to_e5m2(1.0) == 0x3C
+    assert L.oracle_f32_to_e5m2(1.125) == 0x3C           # tie -> even mantissa
+    assert L.oracle_f32_to_e5m2(1.375) == 0x3E           # tie -> even mantissa
+    assert L.oracle_e5m2_to_f32(0x7C) == float("inf")
+    assert L.oracle_e5m2_to_f32(0x7B) == 57344.0
+    assert L.oracle_e5m2_to_f32(0x04) == 2.0 ** -14
+    assert np.isnan(L.oracle_e5m2_to_f32(0xFD))
+    # E5M2 is the top byte of binary16: exact f16 values with zero low byte
+    h = np.arange(0, 0x7C00, 256, dtype=np.uint16)
+    assert all(L.oracle_f32_to_e5m2(float(v)) == (int(b) >> 8)
+               for v, b in zip(h.view(np.float16).astype(np.float32), h))
+
+
 def test_f16_cast_matches_numpy():
     rng = np.random.default_rng(3)
     x = rng.integers(0, 1 << 32, size=200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
@@ -354,7 +398,7 @@ def test_kernel_cast_source_matches_oracle(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True,
                          timeout=600).stdout
     lines = dict(l.split(" ", 1) for l in out.strip().splitlines())
-    assert set(lines) == {"f32_to_e4m3", "e4m3_to_f32", "f32_to_bf16", "f32_to_f16",
-                          "f16_to_f32"}
+    assert set(lines) == {"f32_to_e4m3", "e4m3_to_f32", "f32_to_e5m2", "e5m2_to_f32",
+                          "f32_to_bf16", "f32_to_f16", "f16_to_f32"}
     for name, rest in lines.items():
         assert rest.startswith("0 of "), (name, rest)
