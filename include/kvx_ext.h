@@ -1,25 +1,38 @@
 /*
  * Extensions to the KVX v1 ABI that kvx_abi.h cannot carry unchanged.
  *
- * FP8 (OCP E4M3, "e4m3fn") KV cache with per-tensor F32 scales:
+ * FP8 KV cache (OCP E4M3 "e4m3fn", KVX_DTYPE_F8_E4M3, or OCP E5M2,
+ * KVX_DTYPE_F8_E5M2) with F32 scales:
  *
- *   write:  kvx_launch_write_kv / kvx_launch_write_kv_prefill with a cache of
- *           dtype KVX_DTYPE_F8_E4M3 and io of dtype F16, BF16 or F32.  The
- *           scale is read from write->k_scale_desc / v_scale_desc when their
- *           `data` is non-NULL (dtype F32, granularity PER_TENSOR), otherwise
- *           from write->k_scale / v_scale as one F32 each (KVX_SPEC.md:258-259).
- *           Scale pointers are device pointers, read by the kernel.
- *             q = e4m3_rne(saturate_448(f32(x) / scale)),  NaN -> 0x7F | sign
- *           With io of dtype F8_E4M3 the bytes are copied unscaled.
+ *   write:  kvx_launch_write_kv / kvx_launch_write_kv_prefill with an FP8
+ *           cache and io of dtype F16, BF16 or F32.  The scale is read from
+ *           write->k_scale_desc / v_scale_desc when their `data` is non-NULL,
+ *           otherwise from write->k_scale / v_scale as one F32 each
+ *           (KVX_SPEC.md:258-259).  Scale pointers are device pointers, read
+ *           by the kernel.
+ *             q = fp8_rne(saturate(f32(x) / scale))
+ *           saturating to +-448 (E4M3) / +-57344 (E5M2), infinities included;
+ *           NaN -> 0x7F (E4M3) / 0x7E (E5M2).  With io of the cache's own
+ *           FP8 dtype the bytes are copied unscaled.
  *
  *   gather: kvx_launch_gather_kv_dequant below, because kvx_gather_desc_t
  *           (reference kvx_abi.h:182-188) has no scale fields.
  *             y = round_to_io_dtype(f32(q) * scale)   (RNE; NaN -> quiet NaN)
- *           kvx_launch_gather_kv with F8_E4M3 cache and io copies bytes.
+ *           kvx_launch_gather_kv with an FP8 cache and the same FP8 io copies
+ *           bytes.
+ *
+ * Scale descriptors (kvx_scale_desc_t, dtype F32; strides in elements; the
+ * field names are the spec's, KVX_SPEC.md:190-197, the shapes this build's):
+ *   PER_TENSOR      data[0]
+ *   PER_HEAD        ndim 1, shape [num_kv_heads]
+ *   PER_BLOCK       ndim 1, shape [num_blocks], indexed by physical block id
+ *   PER_BLOCK_HEAD  ndim 2, shape [num_blocks, num_kv_heads]
+ * A wrong shape is KVX_STATUS_INVALID_ARGUMENT; other granularities and
+ * dtypes, and block-indexed scales on KV_OFFSETS gathers, are
+ * KVX_STATUS_UNSUPPORTED.
  *
  * The reference has no FP8 kernels (KVX_CONFORMANCE.md:24, :35); this is new
- * functionality.  E5M2 and non-per-tensor scales return
- * KVX_STATUS_UNSUPPORTED.
+ * functionality.
  */
 #ifndef KVX_EXT_H
 #define KVX_EXT_H
@@ -30,10 +43,11 @@
 extern "C" {
 #endif
 
-/* Dequantizing gather from an F8_E4M3 paged cache into an F16/BF16/F32
- * [seq_count, max_seq_len, H, D] buffer.  Same validation order, codes and
- * untouched-row semantics as kvx_launch_gather_kv; k_scale / v_scale must be
- * non-NULL PER_TENSOR F32 descriptors whose data is a device pointer.
+/* Dequantizing gather from an F8_E4M3 or F8_E5M2 paged cache into an
+ * F16/BF16/F32 [seq_count, max_seq_len, H, D] buffer, over any block-table
+ * format.  Same validation order, codes and untouched-row semantics as
+ * kvx_launch_gather_kv; k_scale / v_scale must be non-NULL F32 scale
+ * descriptors (granularities above) whose data is a device pointer.
  * No reference counterpart (the reference gather returns UNSUPPORTED for FP8,
  * kernels/kvx_paged_kv.cu:900-909). */
 KVX_API kvx_status_t kvx_launch_gather_kv_dequant(
