@@ -144,6 +144,25 @@ kvx_status_t check_seq_lens(const kvx_seq_lens_t *s, uint32_t seq_count) {
 }
 
 // kvx_abi.c:216-311: shape must agree with the cache, strides canonical.
+// KVX_LAYOUT_BLOCK_CUSTOM ("any layout described by explicit shape and
+// stride", KVX_SPEC.md:57), as this build reads it: the axes are the logical
+// (block, token offset, head, dim) in that order, shape [num_blocks,
+// block_size, num_kv_heads, head_dim], or with dim split as (dim / x, x),
+// shape [num_blocks, block_size, num_kv_heads, head_dim / x, x]; the strides
+// place them anywhere (vLLM's [nb, H, D, bs] value cache is strides
+// {H*D*bs, 1, D*bs, bs}).
+bool custom_shape_ok(const kvx_cache_desc_t *c, const kvx_tensor_desc_t *t) {
+  const int64_t *sh = t->shape;
+  if (t->ndim == 4)
+    return sh[0] == c->num_blocks && sh[1] == c->block_size && sh[2] == c->num_kv_heads &&
+           sh[3] == c->head_dim;
+  if (t->ndim == 5)
+    return sh[4] > 0 && (int64_t)c->head_dim % sh[4] == 0 && sh[0] == c->num_blocks &&
+           sh[1] == c->block_size && sh[2] == c->num_kv_heads &&
+           sh[3] == (int64_t)c->head_dim / sh[4];
+  return false;
+}
+
 kvx_status_t check_cache_tensor(const kvx_cache_desc_t *c,
                                 const kvx_tensor_desc_t *t,
                                 kvx_layout_t layout) {
@@ -185,6 +204,10 @@ kvx_status_t check_cache_tensor(const kvx_cache_desc_t *c,
         return KVX_STATUS_UNSUPPORTED;
       return KVX_STATUS_OK;
     }
+    case KVX_LAYOUT_BLOCK_CUSTOM:
+      // The reference returns UNSUPPORTED (kvx_abi.c:307-309); this build
+      // accepts the shapes of custom_shape_ok with any strides.
+      return custom_shape_ok(c, t) ? KVX_STATUS_OK : KVX_STATUS_INVALID_ARGUMENT;
     default:
       return KVX_STATUS_UNSUPPORTED;
   }

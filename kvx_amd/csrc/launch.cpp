@@ -58,8 +58,8 @@ kvx_status_t check_io_4d(const kvx_tensor_desc_t *t, int32_t seq_count,
 
 // Descriptor -> Geom.  Status codes as reference kvx_fill_cache_params
 // (kernels/kvx_paged_kv.cu:18-52): PACKED needs pack > 0 dividing head_dim;
-// layouts other than NHD/HND/HND_PACKED are UNSUPPORTED.  Any strides are
-// honoured.
+// layouts other than NHD/HND/HND_PACKED/CUSTOM are UNSUPPORTED (the
+// reference also rejects CUSTOM).  Any strides are honoured.
 kvx_status_t fill_geom(const kvx_cache_desc_t *cache,
                        const kvx_tensor_desc_t *t, Geom *g) {
   const int64_t *s = t->stride;
@@ -91,6 +91,31 @@ kvx_status_t fill_geom(const kvx_cache_desc_t *cache,
       g->s_off = s[3];
       g->s_inner = s[4];
       g->pack = (int32_t)pack;
+      return KVX_STATUS_OK;
+    }
+    case KVX_LAYOUT_BLOCK_CUSTOM: {
+      // Axes (block, offset, head, dim) or (block, offset, head, dim / x, x)
+      // with any strides; the shape names the split (KVX_SPEC.md:57 leaves
+      // the axis meaning open; this is this build's reading).
+      const int64_t *sh = t->shape;
+      if (sh[0] != cache->num_blocks || sh[1] != cache->block_size ||
+          sh[2] != cache->num_kv_heads)
+        return KVX_STATUS_INVALID_ARGUMENT;
+      g->s_block = s[0];
+      g->s_off = s[1];
+      g->s_head = s[2];
+      if (t->ndim == 4) {
+        if (sh[3] != cache->head_dim) return KVX_STATUS_INVALID_ARGUMENT;
+        g->s_inner = s[3];
+        g->pack = (int32_t)cache->head_dim;
+        return KVX_STATUS_OK;
+      }
+      if (t->ndim != 5 || sh[4] <= 0 || (int64_t)cache->head_dim % sh[4] != 0 ||
+          sh[3] != (int64_t)cache->head_dim / sh[4])
+        return KVX_STATUS_INVALID_ARGUMENT;
+      g->s_piece = s[3];
+      g->s_inner = s[4];
+      g->pack = (int32_t)sh[4];
       return KVX_STATUS_OK;
     }
     default:

@@ -123,6 +123,15 @@ class Geometry:
         self.stride = tuple(int(x) for x in stride)
         self.pack = int(pack)
 
+    @classmethod
+    def custom(cls, stride, head_dim: int, pack: int | None = None) -> "Geometry":
+        """KVX_LAYOUT_BLOCK_CUSTOM: strides of the axes (block, offset, head,
+        dim) or (block, offset, head, dim / pack, pack)."""
+        st = tuple(int(x) for x in stride)
+        if len(st) == 4:
+            return cls(15, (st[0], st[1], st[2], 0, st[3]), head_dim)
+        return cls(15, st, pack)
+
     def args(self):
         return [self.layout, C.cast(_strides(self.stride), _I64P), self.pack]
 

@@ -25,7 +25,7 @@
 #include <omp.h>
 #endif
 
-enum { L_NHD = 1, L_HND = 2, L_PACKED = 3 };
+enum { L_NHD = 1, L_HND = 2, L_PACKED = 3, L_CUSTOM = 15 };
 enum { D_F16 = 1, D_BF16 = 2, D_F32 = 3, D_E4M3 = 4, D_E5M2 = 5 };
 
 static int dtype_size(int dt) {
@@ -51,6 +51,13 @@ int64_t oracle_cache_offset(int layout, const int64_t *s, int64_t pack,
       const int64_t pd = d / pack;
       const int64_t po = d - pd * pack;
       return b * s[0] + h * s[1] + pd * s[2] + o * s[3] + po * s[4];
+    }
+    case L_CUSTOM: {
+      /* axes (block, offset, head, dim / pack, dim % pack); a 4-axis
+       * descriptor is pack = head_dim with s[3] = 0 and s[4] its dim stride */
+      const int64_t pd = d / pack;
+      const int64_t po = d - pd * pack;
+      return b * s[0] + o * s[1] + h * s[2] + pd * s[3] + po * s[4];
     }
     default:
       return 0;
@@ -458,7 +465,7 @@ void oracle_gather_kv_offsets(int k_layout, const int64_t *k_stride, int64_t k_p
 /* Elements of one contiguous run inside a (block, offset, head) row. */
 static int64_t run_elems(int layout, const int64_t *s, int64_t pack,
                          int32_t head_dim) {
-  if (layout == L_PACKED) return s[4] == 1 ? pack : 1;
+  if (layout == L_PACKED || layout == L_CUSTOM) return s[4] == 1 ? pack : 1;
   return s[3] == 1 ? head_dim : 1;
 }
 

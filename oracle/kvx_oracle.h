@@ -22,7 +22,10 @@
 extern "C" {
 #endif
 
-/* Layout codes and dtype codes are the kvx_abi.h enum values. */
+/* Layout codes and dtype codes are the kvx_abi.h enum values.  For
+ * KVX_LAYOUT_BLOCK_CUSTOM (15) the strides are those of the axes (block,
+ * offset, head, dim / pack, dim % pack); a 4-axis custom tensor is pack =
+ * head_dim with stride[3] = 0 and stride[4] its dim stride. */
 
 /* FP8 scales: the scale of element (block b, head h) is
  * p[b * s_block + h * s_head] (strides in elements; a per-tensor scale has

@@ -91,7 +91,13 @@ def test_write_single_faults(kvx_lib, fn):
     case(UNS, lambda c, w: w.io.key.stride.__setitem__(0, 17))              # :283
     case(UNS, lambda c, w: w.io.value.stride.__setitem__(2, 2))             # :350
     case(INV, lambda c, w: setattr(w.slots, "token_count", 3))              # :357
-    case(UNS, lambda c, w: setattr(c.k, "layout", Layout.BLOCK_CUSTOM))     # :49
+    case(UNS, lambda c, w: setattr(c.k, "layout", 14))                      # :49
+    # CUSTOM is gathered and written here (the reference: UNSUPPORTED, :49);
+    # its shape must name the axes
+    case(INV, lambda c, w: (setattr(c.k, "layout", Layout.BLOCK_CUSTOM),
+                            setattr(c.k, "ndim", 3)))
+    case(INV, lambda c, w: (setattr(c.k, "layout", Layout.BLOCK_CUSTOM),
+                            c.k.shape.__setitem__(1, 5)))
     case(UNS, lambda c, w: setattr(c.v, "layout", Layout.INVALID))          # :367
     case(INV, lambda c, w: (setattr(c.k, "layout", Layout.BLOCK_HND_PACKED),
                             c.k.shape.__setitem__(4, 0)))                   # :40
@@ -121,7 +127,7 @@ def test_write_check_order(kvx_lib):
     assert W(kvx_lib, c, w) == INV
     # params (UNSUPPORTED layout) before the slot dtype (INVALID): :363 before :443
     c, w = base_write()
-    c.k.layout = Layout.BLOCK_CUSTOM
+    c.k.layout = 14
     w.slots.dtype = DType.U64
     assert W(kvx_lib, c, w) == UNS
 
@@ -280,7 +286,9 @@ def test_gather_single_faults(kvx_lib):
     case(INV, lambda c, g: setattr(g.seq_lens, "seq_count", 1))               # :795
     case(INV, lambda c, g: g.io.key.shape.__setitem__(1, 7))                  # :302
     case(UNS, lambda c, g: g.io.value.stride.__setitem__(1, 3))               # :306
-    case(UNS, lambda c, g: setattr(c.k, "layout", Layout.BLOCK_CUSTOM))       # :816
+    case(UNS, lambda c, g: setattr(c.k, "layout", 14))                        # :816
+    case(INV, lambda c, g: (setattr(c.v, "layout", Layout.BLOCK_CUSTOM),
+                            setattr(c.v, "ndim", 6)))
     case(INV, lambda c, g: setattr(g.block_table, "index_dtype", DType.S64))  # :861
     case(INV, lambda c, g: setattr(g.seq_lens, "dtype", DType.U32))           # :861
     for expect, c, g in cases:
