@@ -58,6 +58,11 @@ def parse_args():
                    help="issue the writes through kvx_launch_write_kv* (ctypes) or the "
                         "PyTorch-ROCm op _C_cache_ops.reshape_and_cache_flash_kvx "
                         "(c1, c2, c4, c5: NHD caches)")
+    p.add_argument("--layout", default=None, choices=["nhd", "hnd", "packed", "vllm"],
+                   help="c2 / c5: cache layout of K and V (default NHD).  packed: "
+                        "HND_PACKED x = 8; vllm: K HND_PACKED x = 8 and V "
+                        "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
+                        "paged-attention pair")
     p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
                    help="c4: FP8 format of the cache")
     p.add_argument("--scales", default="tensor",
@@ -106,7 +111,7 @@ class Launch:
 
 
 def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch",
-                 fp8="e4m3", scales="tensor"):
+                 fp8="e4m3", scales="tensor", layout=None):
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -126,6 +131,18 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         w.name = w.name.replace("fp8_e4m3", "fp8_e5m2")
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
+    if layout is not None:
+        if name not in ("c2", "c5"):
+            raise SystemExit("--layout applies to c2 and c5")
+        if table_fmt == "kv_offsets" or write_entry == "torch_op":
+            raise SystemExit("--layout combines with the PACKED / RAGGED gathers and the "
+                             "launch entry")
+        lay = {"nhd": (Layout.BLOCK_NHD, Layout.BLOCK_NHD),
+               "hnd": (Layout.BLOCK_HND, Layout.BLOCK_HND),
+               "packed": (Layout.BLOCK_HND_PACKED, Layout.BLOCK_HND_PACKED),
+               "vllm": (Layout.BLOCK_HND_PACKED, Layout.BLOCK_CUSTOM)}[layout]
+        w.k_layout, w.v_layout = lay
+        w.name = f"{w.name}_{layout}"
 
     if table_fmt != "packed" and name == "c3":
         raise SystemExit("c3 has no gather: --table applies to c1, c2, c4, c5")
@@ -152,8 +169,18 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
                                               wl.k_layout, wl.pack)
             fill(pool.key_cache)
             return pc, pool
-        pc = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
-                               tdt[wl.cache_dtype], dev, wl.k_layout, wl.v_layout, wl.pack)
+        if wl.v_layout == Layout.BLOCK_CUSTOM:  # --layout vllm
+            pk = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
+                                   tdt[wl.cache_dtype], dev, wl.k_layout, wl.k_layout,
+                                   wl.pack)
+            pv = paged.alloc_custom_cache(wl.num_blocks, wl.block_size, wl.heads,
+                                          wl.head_dim, tdt[wl.cache_dtype], dev, "bhdo")
+            pc = paged.PagedCache(pk.key_cache, pv.value_cache, wl.k_layout, wl.v_layout,
+                                  wl.num_blocks, wl.block_size, wl.heads, wl.head_dim)
+        else:
+            pc = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
+                                   tdt[wl.cache_dtype], dev, wl.k_layout, wl.v_layout,
+                                   wl.pack)
         for t in (pc.key_cache, pc.value_cache):
             fill(t)
         return pc, pc
@@ -326,6 +353,8 @@ def cpu_baseline(w, seconds: float):
     es = W.dtype_bytes(w.cache_dtype)
     if W.dtype_bytes(w.io_dtype) != es:
         return None  # the CPU fast path is a byte copy; no dequant baseline
+    if Layout.BLOCK_CUSTOM in (w.k_layout, w.v_layout):
+        return None  # the sample below builds canonical layouts only
     rng = np.random.default_rng(0)
     E = w.heads * w.head_dim
     blk_elems = bs * E
@@ -408,7 +437,7 @@ def main():
 
     dev = torch.device("cuda:0")
     w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table,
-                                       args.write_entry, args.fp8, args.scales)
+                                       args.write_entry, args.fp8, args.scales, args.layout)
     stream = torch.cuda.Stream(device=dev)
     sh = stream.cuda_stream
     torch.cuda.set_stream(stream)  # launches that use torch's current stream

@@ -104,6 +104,34 @@ def alloc_cache(num_blocks: int, block_size: int, heads: int, head_dim: int,
                       heads, head_dim)
 
 
+def custom_view(storage: torch.Tensor, order: str) -> torch.Tensor:
+    """The logical CUSTOM view of a cache `storage` whose axes are named by
+    `order`: a permutation of "bohd" (block, offset, head, dim) or "bohpx"
+    (dim split as dim / x, x).  E.g. order "bhdo" is vLLM's value cache
+    [num_blocks, H, D, block_size]."""
+    logical = "bohpx" if len(order) == 5 else "bohd"
+    if sorted(order) != sorted(logical):
+        raise ValueError(f"order {order!r} is not a permutation of {logical!r}")
+    return storage.permute([order.index(a) for a in logical])
+
+
+def alloc_custom_cache(num_blocks: int, block_size: int, heads: int, head_dim: int,
+                       dtype: torch.dtype, device, k_order: str = "bhdo",
+                       v_order: str | None = None, x: int = 8) -> PagedCache:
+    """K and V caches in KVX_LAYOUT_BLOCK_CUSTOM with storage axis orders
+    k_order / v_order (see custom_view; 5-letter orders split dim by x)."""
+    v_order = k_order if v_order is None else v_order
+
+    def one(order):
+        size = {"b": num_blocks, "o": block_size, "h": heads, "d": head_dim,
+                "p": head_dim // x, "x": x}
+        t = torch.empty([size[a] for a in order], dtype=dtype, device=device)
+        return custom_view(t, order)
+
+    return PagedCache(one(k_order), one(v_order), Layout.BLOCK_CUSTOM, Layout.BLOCK_CUSTOM,
+                      num_blocks, block_size, heads, head_dim)
+
+
 def alloc_block_pool(num_blocks: int, block_size: int, heads: int, head_dim: int,
                      dtype: torch.dtype, device, layout=Layout.BLOCK_NHD,
                      pack: int = 8) -> tuple[PagedCache, PagedCache]:
