@@ -898,6 +898,203 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
   }
 }
 
+// Transposing gather of dense blocks (PACKED tables).
+//
+// A dense block stores its elements in (run a, offset o, within-run w)
+// order: element e of row o sits at
+//   (e / W) * bs * W + o * W + e % W          (element units)
+// for a per-token run of W elements: W = 1 (token axis innermost, vLLM's
+// value cache [blocks, H, D, bs]), W = x (x-packed HND_PACKED), W = D (HND)
+// or W = H * D (row-major NHD).  Unless W = H * D, a row is gathered from
+// H * D / W runs bs * W elements apart, so loading rows directly wastes most
+// of every HBM transaction when runs are short.  Here a workgroup takes a
+// tile of `tw` cache bytes of every row of one block, which is the
+// contiguous region [tile * tw * bs, (tile + 1) * tw * bs) of the block:
+//   phase 1  reads the region with 16-byte loads and stores each run piece
+//            into LDS at its row (row pitch tw + 16 bytes: the 16-byte
+//            column stores of 16 consecutive rows fall on distinct banks);
+//   phase 2  reads the valid rows back in order and writes them with the
+//            chunk op (copy, or FP8 dequant), tw bytes of cache per row.
+// A row-major tensor paired with such a tensor copies its valid rows
+// straight through.  blockIdx.y selects K (0) or V (1).
+constexpr int kTileLoads = 4;  // 16-byte chunks per thread in flight
+constexpr int kTilePad = 16;   // LDS row padding, bytes
+
+struct TileTensor {
+  const char *src;    // cache tensor
+  char *dst;          // output tensor
+  int64_t s_block;    // bytes
+  ScaleRef sc;        // dequantizing ops only
+  int32_t run_log2;   // log2 bytes of a per-token run; -1 for row-major
+  int32_t pad_;
+};
+
+struct TileArgs {
+  TileTensor t[2];
+  const void *table;
+  const void *seq_lens;
+  int64_t out_row_bytes;
+  int32_t max_blocks_per_seq;
+  int32_t blocks_per_seq;
+  int32_t tiles;          // tiles per block: cache row bytes / tw
+  int32_t tw_log2;        // tile width, cache bytes per row
+  int32_t pitch;          // LDS row pitch, bytes
+  int32_t max_seq_len;
+  int32_t num_blocks;
+  int32_t head_dim;
+  int32_t row_elems;      // H * D
+  int32_t bs_log2;
+  int32_t cache_es_log2;  // log2 cache element bytes
+  int32_t io_es_log2;     // log2 output element bytes
+};
+
+// Store piece k (PIECE bytes) of a 16-byte chunk at p.
+template <int PIECE>
+__device__ __forceinline__ void put_piece(char *p, const Raw<16> &x, int k) {
+  if constexpr (PIECE == 16) {
+    st<16>(p, x);
+  } else if constexpr (PIECE == 8) {
+    Raw<8> y;
+    y.w[0] = x.w[2 * k];
+    y.w[1] = x.w[2 * k + 1];
+    st<8>(p, y);
+  } else if constexpr (PIECE == 4) {
+    Raw<4> y;
+    y.w[0] = x.w[k];
+    st<4>(p, y);
+  } else if constexpr (PIECE == 2) {
+    Raw<2> y;
+    y.w[0] = get16(x, k);
+    st<2>(p, y);
+  } else {
+    Raw<1> y;
+    y.w[0] = get8(x, k);
+    st<1>(p, y);
+  }
+}
+
+// Phase 1: region (nbytes = tw * bs cache bytes, 16-byte aligned) -> LDS
+// rows.  PIECE = min(run bytes, 16).  A chunk whose first row is not valid
+// is skipped: its later pieces are later rows of the same run, or (runs of
+// bs * run < 16 bytes) start again at row 0, which is always valid.
+template <int PIECE>
+__device__ __forceinline__ void stage_tile(const char *region, char *lds, int32_t nbytes,
+                                           int32_t run_log2, int32_t bs_log2, int32_t pitch,
+                                           int32_t rows) {
+  const int32_t bsm = (1 << bs_log2) - 1;
+  const int32_t runm = (1 << run_log2) - 1;
+  constexpr int32_t kStep = kBlockThreads * 16;
+  for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
+    Raw<16> x[kTileLoads];
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+      if (m < nbytes && ((m >> run_log2) & bsm) < rows)
+        x[u] = ld<16, kGatherNtLoad>(region + m);
+    }
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+      if (m < nbytes && ((m >> run_log2) & bsm) < rows) {
+#pragma unroll
+        for (int k = 0; k < 16 / PIECE; ++k) {
+          const int32_t mm = m + k * PIECE;
+          const int32_t o = (mm >> run_log2) & bsm;
+          const int32_t ar = mm >> (run_log2 + bs_log2);
+          put_piece<PIECE>(lds + o * pitch + (ar << run_log2) + (mm & runm), x[u], k);
+        }
+      }
+    }
+  }
+}
+
+template <class Op, bool I64>
+__global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
+  const uint32_t wg = blockIdx.x;
+  const uint32_t per_seq = (uint32_t)a.blocks_per_seq * (uint32_t)a.tiles;
+  const uint32_t su = wg / per_seq;
+  const uint32_t w = wg - su * per_seq;
+  const uint32_t lbu = w / (uint32_t)a.tiles;
+  const int32_t tile = (int32_t)(w - lbu * (uint32_t)a.tiles);
+  const int32_t lb = (int32_t)lbu;
+  const int64_t s = su;
+  if (lb >= a.max_blocks_per_seq) return;
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+  const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  const int64_t t0 = (int64_t)lb << a.bs_log2;
+  if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
+  const int64_t rem = n - t0;
+  const int32_t bs = 1 << a.bs_log2;
+  const int32_t rows = rem < bs ? (int32_t)rem : bs;
+  float uniform = 1.0f;
+  if constexpr (Op::kScaled) uniform = tt.sc.p[0];
+
+  const int32_t tw = 1 << a.tw_log2;
+  const int32_t region = tw << a.bs_log2;
+  const char *blk = tt.src + bid * tt.s_block;
+  char *out = tt.dst + (s * a.max_seq_len + t0) * a.out_row_bytes;
+  const uint32_t hd = (uint32_t)a.head_dim;
+  const uint32_t re = (uint32_t)a.row_elems;
+
+  if (tt.run_log2 < 0) {
+    // Row-major block: rows are contiguous in the cache and in the output.
+    const int32_t lo = tile * region;
+    const int64_t valid = ((int64_t)rows << a.cache_es_log2) * re;
+    const int32_t hi = (int32_t)(lo + region < valid ? lo + region : valid);
+    for (int32_t m = lo + (int32_t)threadIdx.x * Op::kSrc; m < hi; m += kBlockThreads * Op::kSrc) {
+      const uint32_t e = (uint32_t)m >> a.cache_es_log2;
+      float sc = uniform;
+      if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, bid, (e % re) / hd);
+      st<Op::kDst, kGatherNtStore>(out + ((int64_t)e << a.io_es_log2),
+                                   Op::apply(ld<Op::kSrc, kGatherNtLoad>(blk + m), sc));
+    }
+    return;
+  }
+
+  const char *src = blk + (int64_t)tile * region;
+  switch (tt.run_log2) {
+    case 0: stage_tile<1>(src, lds, region, 0, a.bs_log2, a.pitch, rows); break;
+    case 1: stage_tile<2>(src, lds, region, 1, a.bs_log2, a.pitch, rows); break;
+    case 2: stage_tile<4>(src, lds, region, 2, a.bs_log2, a.pitch, rows); break;
+    case 3: stage_tile<8>(src, lds, region, 3, a.bs_log2, a.pitch, rows); break;
+    default: stage_tile<16>(src, lds, region, tt.run_log2, a.bs_log2, a.pitch, rows); break;
+  }
+  __syncthreads();
+
+  // Phase 2: chunk c of row r covers cache bytes [c * kSrc, (c + 1) * kSrc)
+  // of the tile, i.e. row elements e0 + c * G.
+  constexpr int kSrcLog2 = Op::kSrc == 16 ? 4 : Op::kSrc == 8 ? 3 : Op::kSrc == 4 ? 2
+                           : Op::kSrc == 2 ? 1 : 0;
+  const int32_t cpr_log2 = a.tw_log2 - kSrcLog2;
+  const int32_t total = rows << cpr_log2;
+  const uint32_t e0 = ((uint32_t)tile << a.tw_log2) >> a.cache_es_log2;
+  const int32_t cm = (1 << cpr_log2) - 1;
+  for (int32_t u0 = (int32_t)threadIdx.x; u0 < total; u0 += kTileLoads * kBlockThreads) {
+    Raw<Op::kSrc> x[kTileLoads];
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if (u < total) x[k] = ld<Op::kSrc>(lds + (u >> cpr_log2) * a.pitch + ((u & cm) << kSrcLog2));
+    }
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if (u < total) {
+        const int32_t r = u >> cpr_log2;
+        const uint32_t e = e0 + ((uint32_t)((u & cm) << kSrcLog2) >> a.cache_es_log2);
+        float sc = uniform;
+        if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, bid, e / hd);
+        st<Op::kDst, kGatherNtStore>(out + (int64_t)r * a.out_row_bytes +
+                                         ((int64_t)e << a.io_es_log2),
+                                     Op::apply(x[k], sc));
+      }
+    }
+  }
+}
+
 // RAGGED and KV_OFFSETS gathers (KVX_SPEC.md:99-122).  A workgroup covers
 // `rows_per_wg` output rows of one sequence; every row resolves its own
 // source, so K and V rows come from wherever the table points:
@@ -1304,6 +1501,26 @@ void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
   }
 }
 
+template <class Op>
+void launch_tiles(const TileArgs &t, bool i64, int64_t grid, uint32_t lds, hipStream_t s) {
+  const dim3 g((uint32_t)grid, 2);
+  if (i64) {
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, true>), g, dim3(kBlockThreads), lds, s, t);
+  } else {
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, false>), g, dim3(kBlockThreads), lds, s, t);
+  }
+}
+
+template <int F8>
+void launch_tiles_dequant(int io, const TileArgs &t, bool i64, int64_t grid, uint32_t lds,
+                          hipStream_t s) {
+  switch (io) {
+    case KVX_DTYPE_F32: launch_tiles<DequantOp<8, KVX_DTYPE_F32, F8>>(t, i64, grid, lds, s); break;
+    case KVX_DTYPE_F16: launch_tiles<DequantOp<8, KVX_DTYPE_F16, F8>>(t, i64, grid, lds, s); break;
+    default: launch_tiles<DequantOp<8, KVX_DTYPE_BF16, F8>>(t, i64, grid, lds, s); break;
+  }
+}
+
 template <int IO, int F8>
 void dispatch_quant(int ge, const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   switch (ge) {
@@ -1349,6 +1566,100 @@ int log2_exact(int64_t v) {
   int lg = 0;
   while ((int64_t(1) << lg) < v) ++lg;
   return lg;
+}
+
+// Elements of one per-token contiguous run when `g` is a dense block in
+// (run, offset, within-run) order, element e of row o at
+// (e / W) * bs * W + o * W + e % W, else -1: W = H * D (row-major), D (HND),
+// x (x-packed) or 1 (token axis innermost).  Any block stride.
+int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
+  const int64_t p = g.pack;
+  const bool split = p < D;  // d = (d / p) * p + d % p with its own strides
+  if (g.s_inner == 1 && (!split || g.s_piece == p)) {
+    if (g.s_off == H * D && g.s_head == D) return H * D;
+    if (g.s_off == D && g.s_head == bs * D) return D;
+  }
+  if (split && g.s_inner == 1 && g.s_off == p && g.s_piece == bs * p && g.s_head == bs * D)
+    return p;
+  if (g.s_off == 1 && g.s_inner == bs && (!split || g.s_piece == bs * p) && g.s_head == bs * D)
+    return 1;
+  return -1;
+}
+
+// Transposing-gather plan (gather_tiles_kernel) for a PACKED-table gather of
+// dense blocks when some tensor has per-token runs shorter than
+// kTileMaxRun bytes, or false.
+#ifndef KVX_TILE_MAX_RUN
+#define KVX_TILE_MAX_RUN 64
+#endif
+#ifndef KVX_TILE_BYTES
+#define KVX_TILE_BYTES 8192
+#endif
+bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
+                int64_t *grid, uint32_t *lds_bytes) {
+  if (p.format != KVX_BLOCK_TABLE_PACKED) return false;
+  const int64_t bs = p.block_size;
+  const int64_t H = p.heads;
+  const int64_t D = p.head_dim;
+  const int64_t row_cache = H * D * cs;
+  const int bs_log2 = log2_exact(bs);
+  const int row_log2 = log2_exact(row_cache);
+  if (bs_log2 < 0 || row_log2 < 0 || row_cache < 16) return false;
+  const Geom *g[2] = {&p.gk, &p.gv};
+  const void *src[2] = {p.src_k, p.src_v};
+  void *dst[2] = {p.dst_k, p.dst_v};
+  int run_log2[2];
+  bool short_run = false;
+  int64_t min_tw = 16;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t w = dense_run_elems(*g[i], bs, H, D);
+    if (w < 0) return false;
+    run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
+    if (w != H * D) {
+      if (run_log2[i] < 0) return false;
+      if (w * cs < KVX_TILE_MAX_RUN) short_run = true;
+      if (w * cs > min_tw) min_tw = w * cs;
+    }
+    if ((reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(g[i]->s_block * cs)) % 16 != 0)
+      return false;
+    const int dst_align = src_chunk / cs * is;  // output bytes per chunk
+    if (reinterpret_cast<uintptr_t>(dst[i]) % dst_align != 0) return false;
+  }
+  if (!short_run) return false;
+  if ((D * cs) % src_chunk != 0) return false;  // chunks never straddle heads
+  int64_t tw = row_cache;
+  while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  const int64_t pitch = tw + kTilePad;
+  if (bs * pitch > 64 * 1024) return false;
+  t->table = p.block_table;
+  t->seq_lens = p.seq_lens;
+  t->out_row_bytes = H * D * is;
+  t->max_blocks_per_seq = p.max_blocks_per_seq;
+  const int64_t by_len = ((int64_t)p.max_seq_len + bs - 1) / bs;
+  t->blocks_per_seq =
+      (int32_t)(by_len < p.max_blocks_per_seq ? by_len : p.max_blocks_per_seq);
+  t->tiles = (int32_t)(row_cache / tw);
+  t->tw_log2 = log2_exact(tw);
+  t->pitch = (int32_t)pitch;
+  t->max_seq_len = p.max_seq_len;
+  t->num_blocks = p.num_blocks;
+  t->head_dim = p.head_dim;
+  t->row_elems = (int32_t)(H * D);
+  t->bs_log2 = bs_log2;
+  t->cache_es_log2 = log2_exact(cs);
+  t->io_es_log2 = log2_exact(is);
+  const ScaleRef sc[2] = {p.k_scale, p.v_scale};
+  for (int i = 0; i < 2; ++i) {
+    t->t[i].src = static_cast<const char *>(src[i]);
+    t->t[i].dst = static_cast<char *>(dst[i]);
+    t->t[i].s_block = g[i]->s_block * cs;
+    t->t[i].sc = sc[i];
+    t->t[i].run_log2 = run_log2[i];
+    t->t[i].pad_ = 0;
+  }
+  *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
+  *lds_bytes = (uint32_t)(bs * pitch);
+  return *grid <= 0x7FFFFFFF;
 }
 
 // Chunks per contiguous per-token run when `g` is a dense block (the layout's
@@ -1474,6 +1785,26 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
         reinterpret_cast<uintptr_t>(p.pool[0]) | reinterpret_cast<uintptr_t>(p.pool[1]) |
         (uintptr_t)p.bytes_per_block);
   }
+  hipStream_t s = as_stream(stream);
+  {
+    // Dense blocks with short per-token runs: the transposing gather.
+    TileArgs t;
+    int64_t tgrid = 0;
+    uint32_t tlds = 0;
+    const bool dq = p.conv == kConvDequant;
+    if (p.seq_count > 0 && plan_tiles(p, cs, is, dq ? 8 : 16, &t, &tgrid, &tlds)) {
+      if (tgrid == 0) return KVX_STATUS_OK;
+      const bool i64 = p.lens_is64 != 0;
+      if (!dq) {
+        launch_tiles<CopyOp<16>>(t, i64, tgrid, tlds, s);
+      } else if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
+        launch_tiles_dequant<KVX_DTYPE_F8_E5M2>(p.io_dtype, t, i64, tgrid, tlds, s);
+      } else {
+        launch_tiles_dequant<KVX_DTYPE_F8_E4M3>(p.io_dtype, t, i64, tgrid, tlds, s);
+      }
+      return hipGetLastError() == hipSuccess ? KVX_STATUS_OK : KVX_STATUS_INTERNAL_ERROR;
+    }
+  }
   const int ge = pick_chunk(p.gk, p.gv, base_k, base_v, cs, p.dst_k,
                             p.dst_v, is, p.head_dim, max_bytes);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
@@ -1554,7 +1885,6 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   if (a.blocks_per_seq <= 0 || p.seq_count <= 0) return KVX_STATUS_OK;
   const int64_t grid = (int64_t)p.seq_count * a.blocks_per_seq;
   if (grid > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;  // one workgroup per block
-  hipStream_t s = as_stream(stream);
 
   if (p.conv == kConvCopy) {
     switch (ge * cs) {

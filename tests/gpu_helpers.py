@@ -88,6 +88,43 @@ class CacheBuf:
                                self.pack if self.layout == Layout.BLOCK_HND_PACKED else 1)
 
 
+class CustomBuf:
+    """A KVX_LAYOUT_BLOCK_CUSTOM cache tensor: storage with axes in `order` (a
+    permutation of the logical axes b, o, h, d or b, o, h, p, x with
+    p = d / x), its last storage axis padded by `pad` elements, and the
+    logical view handed to the library."""
+
+    def __init__(self, dtype, nb, bs, H, D, order, x=None, pad=0, gen=None, device="cuda"):
+        sizes = {"b": nb, "o": bs, "h": H}
+        if x is None:
+            sizes["d"] = D
+            logical = "bohd"
+        else:
+            sizes["p"], sizes["x"] = D // x, x
+            logical = "bohpx"
+        assert sorted(order) == sorted(logical)
+        shape = [sizes[a] for a in order]
+        shape[-1] += pad
+        self.base = torch.empty(shape, dtype=TORCH_DT[dtype], device=device)
+        random_fill(self.base, gen or torch.Generator().manual_seed(0))
+        trimmed = self.base[..., : sizes[order[-1]]]
+        self.view = trimmed.permute([order.index(a) for a in logical])
+        self.x = x
+        self.D = D
+
+    def geometry(self) -> oracle.Geometry:
+        return oracle.Geometry.custom(self.view.stride(), self.D, self.x)
+
+
+def custom_cache(dtype, nb, bs, H, D, korder, vorder, kx=None, vx=None, gen=None, pad=0):
+    """PagedCache of two CUSTOM tensors (K and V storage orders korder /
+    vorder), with their CustomBufs."""
+    k = CustomBuf(dtype, nb, bs, H, D, korder, kx, pad, gen)
+    v = CustomBuf(dtype, nb, bs, H, D, vorder, vx, pad, gen)
+    pc = paged.PagedCache(k.view, v.view, Layout.BLOCK_CUSTOM, Layout.BLOCK_CUSTOM, nb, bs, H, D)
+    return pc, k, v
+
+
 def make_cache(k_layout, v_layout, dtype, nb, bs, H, D, pack=8, device="cuda",
                gen=None, k_pad=None, v_pad=None):
     gen = gen or torch.Generator().manual_seed(0)

@@ -12,49 +12,14 @@ import numpy as np
 import pytest
 import torch
 
-import oracle
 from kvx_amd import paged
-from kvx_amd.abi import DType, Layout
+from kvx_amd.abi import DType
 
-from gpu_helpers import TORCH_DT, check_gather, check_gather_ragged, check_write, random_fill
+from gpu_helpers import (TORCH_DT, check_gather, check_gather_ragged, check_write, custom_cache,
+                         random_fill)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-CUSTOM = Layout.BLOCK_CUSTOM
-
-
-class CustomBuf:
-    """A CUSTOM cache tensor: storage with axes in `order` (a permutation
-    of the logical axes b, o, h, d or b, o, h, p, x), and the logical view
-    handed to the library."""
-
-    def __init__(self, dtype, nb, bs, H, D, order, x=None, pad=0, gen=None):
-        sizes = {"b": nb, "o": bs, "h": H}
-        if x is None:
-            sizes["d"] = D
-            logical = "bohd"
-        else:
-            sizes["p"], sizes["x"] = D // x, x
-            logical = "bohpx"
-        assert sorted(order) == sorted(logical)
-        shape = [sizes[a] for a in order]
-        shape[-1] += pad
-        self.base = torch.empty(shape, dtype=TORCH_DT[dtype], device=DEV)
-        random_fill(self.base, gen)
-        trimmed = self.base[..., : sizes[order[-1]]]
-        self.view = trimmed.permute([order.index(a) for a in logical])
-        self.x = x
-        self.D = D
-
-    def geometry(self):
-        return oracle.Geometry.custom(self.view.stride(), self.D, self.x)
-
-
-def custom_cache(dtype, nb, bs, H, D, korder, vorder, kx=None, vx=None, gen=None, pad=0):
-    k = CustomBuf(dtype, nb, bs, H, D, korder, kx, pad, gen)
-    v = CustomBuf(dtype, nb, bs, H, D, vorder, vx, pad, gen)
-    pc = paged.PagedCache(k.view, v.view, CUSTOM, CUSTOM, nb, bs, H, D)
-    return pc, k, v
 
 
 ORDERS = [
