@@ -62,7 +62,7 @@ def parse_args():
                    help="c2 / c5: cache layout of K and V (default NHD).  packed: "
                         "HND_PACKED x = 8; vllm: K HND_PACKED x = 8 and V "
                         "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
-                        "paged-attention pair")
+                        "paged-attention pair (PACKED / RAGGED tables only)")
     p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
                    help="c4: FP8 format of the cache")
     p.add_argument("--scales", default="tensor",
@@ -134,9 +134,10 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
     if layout is not None:
         if name not in ("c2", "c5"):
             raise SystemExit("--layout applies to c2 and c5")
-        if table_fmt == "kv_offsets" or write_entry == "torch_op":
-            raise SystemExit("--layout combines with the PACKED / RAGGED gathers and the "
-                             "launch entry")
+        if write_entry == "torch_op":
+            raise SystemExit("--layout combines with the launch entry")
+        if table_fmt == "kv_offsets" and layout == "vllm":
+            raise SystemExit("KV_OFFSETS pools hold K and V blocks of one layout")
         lay = {"nhd": (Layout.BLOCK_NHD, Layout.BLOCK_NHD),
                "hnd": (Layout.BLOCK_HND, Layout.BLOCK_HND),
                "packed": (Layout.BLOCK_HND_PACKED, Layout.BLOCK_HND_PACKED),

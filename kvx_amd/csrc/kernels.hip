@@ -906,8 +906,9 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
 // for a per-token run of W elements: W = 1 (token axis innermost, vLLM's
 // value cache [blocks, H, D, bs]), W = x (x-packed HND_PACKED), W = D (HND)
 // or W = H * D (row-major NHD).  Unless W = H * D, a row is gathered from
-// H * D / W runs bs * W elements apart, so loading rows directly wastes most
-// of every HBM transaction when runs are short.  Here a workgroup takes a
+// H * D / W runs bs * W elements apart: loading rows directly uses a
+// fraction of every HBM transaction when runs are short (and measures slower
+// than this kernel even for HND's 256-byte runs).  Here a workgroup takes a
 // tile of `tw` cache bytes of every row of one block, which is the
 // contiguous region [tile * tw * bs, (tile + 1) * tw * bs) of the block:
 //   phase 1  reads the region with 16-byte loads and stores each run piece
@@ -916,7 +917,9 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
 //   phase 2  reads the valid rows back in order and writes them with the
 //            chunk op (copy, or FP8 dequant), tw bytes of cache per row.
 // A row-major tensor paired with such a tensor copies its valid rows
-// straight through.  blockIdx.y selects K (0) or V (1).
+// straight through.  blockIdx.y selects K (0) or V (1).  PACKED tables give
+// the block id of (sequence, logical block); KV_OFFSETS tables give K's and
+// V's block addresses separately (pool + index * bytes_per_block).
 constexpr int kTileLoads = 4;  // 16-byte chunks per thread in flight
 constexpr int kTilePad = 16;   // LDS row padding, bytes
 
@@ -933,6 +936,8 @@ struct TileArgs {
   TileTensor t[2];
   const void *table;
   const void *seq_lens;
+  const char *pool[2];      // KV_OFFSETS primary / secondary
+  int64_t bytes_per_block;  // KV_OFFSETS
   int64_t out_row_bytes;
   int32_t max_blocks_per_seq;
   int32_t blocks_per_seq;
@@ -1008,7 +1013,7 @@ __device__ __forceinline__ void stage_tile(const char *region, char *lds, int32_
   }
 }
 
-template <class Op, bool I64>
+template <class Op, int FMT, bool I64>
 __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
@@ -1022,10 +1027,24 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
   const int64_t s = su;
   if (lb >= a.max_blocks_per_seq) return;
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
-  const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+  int64_t bid;
+  const char *blk;
+  if constexpr (FMT == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    // table [seq, beam = 1, {K, V}, max_blocks_per_seq] of KVCacheIndex
+    const uint32_t ent = reinterpret_cast<const uint32_t *>(
+        a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
+    const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
+    bid = ent & 0x7FFFFFFFu;
+    if (pool == nullptr || bid >= a.num_blocks) return;
+    blk = pool + bid * a.bytes_per_block;
+  } else {
+    bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+    if (bid < 0 || bid >= a.num_blocks) return;
+    blk = tt.src + bid * tt.s_block;
+  }
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int64_t t0 = (int64_t)lb << a.bs_log2;
-  if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
+  if (t0 >= n) return;
   const int64_t rem = n - t0;
   const int32_t bs = 1 << a.bs_log2;
   const int32_t rows = rem < bs ? (int32_t)rem : bs;
@@ -1034,7 +1053,6 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
 
   const int32_t tw = 1 << a.tw_log2;
   const int32_t region = tw << a.bs_log2;
-  const char *blk = tt.src + bid * tt.s_block;
   char *out = tt.dst + (s * a.max_seq_len + t0) * a.out_row_bytes;
   const uint32_t hd = (uint32_t)a.head_dim;
   const uint32_t re = (uint32_t)a.row_elems;
@@ -1501,23 +1519,39 @@ void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
   }
 }
 
-template <class Op>
-void launch_tiles(const TileArgs &t, bool i64, int64_t grid, uint32_t lds, hipStream_t s) {
+template <class Op, int FMT>
+void launch_tiles_fmt(const TileArgs &t, bool i64, int64_t grid, uint32_t lds, hipStream_t s) {
   const dim3 g((uint32_t)grid, 2);
   if (i64) {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, true>), g, dim3(kBlockThreads), lds, s, t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, true>), g, dim3(kBlockThreads), lds, s, t);
   } else {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, false>), g, dim3(kBlockThreads), lds, s, t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, false>), g, dim3(kBlockThreads), lds, s, t);
+  }
+}
+
+template <class Op>
+void launch_tiles(const TileArgs &t, int fmt, bool i64, int64_t grid, uint32_t lds,
+                  hipStream_t s) {
+  if (fmt == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_KV_OFFSETS>(t, i64, grid, lds, s);
+  } else {
+    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_PACKED>(t, i64, grid, lds, s);
   }
 }
 
 template <int F8>
-void launch_tiles_dequant(int io, const TileArgs &t, bool i64, int64_t grid, uint32_t lds,
-                          hipStream_t s) {
+void launch_tiles_dequant(int io, const TileArgs &t, int fmt, bool i64, int64_t grid,
+                          uint32_t lds, hipStream_t s) {
   switch (io) {
-    case KVX_DTYPE_F32: launch_tiles<DequantOp<8, KVX_DTYPE_F32, F8>>(t, i64, grid, lds, s); break;
-    case KVX_DTYPE_F16: launch_tiles<DequantOp<8, KVX_DTYPE_F16, F8>>(t, i64, grid, lds, s); break;
-    default: launch_tiles<DequantOp<8, KVX_DTYPE_BF16, F8>>(t, i64, grid, lds, s); break;
+    case KVX_DTYPE_F32:
+      launch_tiles<DequantOp<8, KVX_DTYPE_F32, F8>>(t, fmt, i64, grid, lds, s);
+      break;
+    case KVX_DTYPE_F16:
+      launch_tiles<DequantOp<8, KVX_DTYPE_F16, F8>>(t, fmt, i64, grid, lds, s);
+      break;
+    default:
+      launch_tiles<DequantOp<8, KVX_DTYPE_BF16, F8>>(t, fmt, i64, grid, lds, s);
+      break;
   }
 }
 
@@ -1587,17 +1621,18 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 }
 
 // Transposing-gather plan (gather_tiles_kernel) for a PACKED-table gather of
-// dense blocks when some tensor has per-token runs shorter than
-// kTileMaxRun bytes, or false.
-#ifndef KVX_TILE_MAX_RUN
-#define KVX_TILE_MAX_RUN 64
-#endif
+// dense blocks of which at least one is not row-major, or false.  On MI355X
+// (c2 shapes, bf16) it beats the row kernel for every run length measured:
+// token-innermost 2.45 -> 5.90 TB/s, x-packed 4.66 -> 5.88, HND (256-byte
+// runs) 5.14 -> 5.87.  KVX_TILE_BYTES is the cache bytes per tensor of one
+// tile (8 KiB measured best against 4 and 16 KiB).
 #ifndef KVX_TILE_BYTES
 #define KVX_TILE_BYTES 8192
 #endif
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
-  if (p.format != KVX_BLOCK_TABLE_PACKED) return false;
+  const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
+  if (p.format != KVX_BLOCK_TABLE_PACKED && !offsets) return false;
   const int64_t bs = p.block_size;
   const int64_t H = p.heads;
   const int64_t D = p.head_dim;
@@ -1609,7 +1644,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   const void *src[2] = {p.src_k, p.src_v};
   void *dst[2] = {p.dst_k, p.dst_v};
   int run_log2[2];
-  bool short_run = false;
+  bool transposed = false;
   int64_t min_tw = 16;
   for (int i = 0; i < 2; ++i) {
     const int64_t w = dense_run_elems(*g[i], bs, H, D);
@@ -1617,15 +1652,19 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
     if (w != H * D) {
       if (run_log2[i] < 0) return false;
-      if (w * cs < KVX_TILE_MAX_RUN) short_run = true;
+      transposed = true;
       if (w * cs > min_tw) min_tw = w * cs;
     }
-    if ((reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(g[i]->s_block * cs)) % 16 != 0)
-      return false;
+    // block addresses: base + index * pitch, all 16-byte aligned
+    const uintptr_t base =
+        offsets ? reinterpret_cast<uintptr_t>(p.pool[0]) | reinterpret_cast<uintptr_t>(p.pool[1]) |
+                      (uintptr_t)p.bytes_per_block
+                : reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(g[i]->s_block * cs);
+    if (base % 16 != 0) return false;
     const int dst_align = src_chunk / cs * is;  // output bytes per chunk
     if (reinterpret_cast<uintptr_t>(dst[i]) % dst_align != 0) return false;
   }
-  if (!short_run) return false;
+  if (!transposed) return false;
   if ((D * cs) % src_chunk != 0) return false;  // chunks never straddle heads
   int64_t tw = row_cache;
   while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
@@ -1633,6 +1672,9 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   if (bs * pitch > 64 * 1024) return false;
   t->table = p.block_table;
   t->seq_lens = p.seq_lens;
+  t->pool[0] = p.pool[0];
+  t->pool[1] = p.pool[1];
+  t->bytes_per_block = p.bytes_per_block;
   t->out_row_bytes = H * D * is;
   t->max_blocks_per_seq = p.max_blocks_per_seq;
   const int64_t by_len = ((int64_t)p.max_seq_len + bs - 1) / bs;
@@ -1787,7 +1829,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   }
   hipStream_t s = as_stream(stream);
   {
-    // Dense blocks with short per-token runs: the transposing gather.
+    // Dense blocks that are not all row-major: the transposing gather.
     TileArgs t;
     int64_t tgrid = 0;
     uint32_t tlds = 0;
@@ -1796,11 +1838,11 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       if (tgrid == 0) return KVX_STATUS_OK;
       const bool i64 = p.lens_is64 != 0;
       if (!dq) {
-        launch_tiles<CopyOp<16>>(t, i64, tgrid, tlds, s);
+        launch_tiles<CopyOp<16>>(t, p.format, i64, tgrid, tlds, s);
       } else if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
-        launch_tiles_dequant<KVX_DTYPE_F8_E5M2>(p.io_dtype, t, i64, tgrid, tlds, s);
+        launch_tiles_dequant<KVX_DTYPE_F8_E5M2>(p.io_dtype, t, p.format, i64, tgrid, tlds, s);
       } else {
-        launch_tiles_dequant<KVX_DTYPE_F8_E4M3>(p.io_dtype, t, i64, tgrid, tlds, s);
+        launch_tiles_dequant<KVX_DTYPE_F8_E4M3>(p.io_dtype, t, p.format, i64, tgrid, tlds, s);
       }
       return hipGetLastError() == hipSuccess ? KVX_STATUS_OK : KVX_STATUS_INTERNAL_ERROR;
     }
