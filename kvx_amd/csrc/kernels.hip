@@ -29,6 +29,10 @@ constexpr int kWavesPerBlock = kBlockThreads / kWave;
 // Chunk offsets each lane keeps in registers; rows with more chunks per lane
 // compute the rest on the fly.
 constexpr int kMaxChunksPerLane = 4;
+// LDS tile kernels (gather_tiles_kernel, write_tiles_kernel): 16-byte chunks
+// per thread in flight, and LDS row padding in bytes.
+constexpr int kTileLoads = 4;
+constexpr int kTilePad = 16;
 // Compile-time tuning knobs of the contiguous-block gather (defaults are the
 // measured best on MI355X): chunks per lane in flight, and non-temporal
 // (streaming) loads of the cache / stores of the output.
@@ -502,106 +506,20 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 // When the `bs` consecutive tokens of a group fill one cache block in order
 // (slot = b * bs + o for o = 0..bs-1, the usual prefill pattern), the
 // group's source rows are one contiguous io region and each cache tensor's
-// destination is one contiguous block region, only permuted: a dense block
-// stores chunks in (run, offset, chunk-in-run) order,
-//   unit u = (a * bs + o) * Bc + w,   row chunk c = a * Bc + w,
-// where Bc is the chunks per contiguous per-token run: the whole row for
-// NHD, head_dim / G for HND, pack / G for HND_PACKED.  A row-dense tensor
-// (Bc = row chunks) is copied straight through; any other is staged in LDS
-// (rows padded by one chunk so the strided LDS reads are bank-conflict
-// free) so that both the HBM reads and the HBM writes are fully coalesced.
-// Groups that do not fill a block take the per-token path.
+// destination is one contiguous block region, only permuted.
+// write_tiles_kernel moves such groups through LDS so that both the io
+// reads and the cache writes are coalesced 16-byte accesses; groups that do
+// not fill a block take the per-token path.
 
-struct BlockWriteArgs {
-  int32_t bs_log2;
-  int32_t nchunks_log2;  // row chunks
-  int32_t k_bc_log2;     // K chunks per contiguous per-token run
-  int32_t v_bc_log2;
-  int32_t pitch;         // LDS row pitch in chunks (row chunks + 1)
-  int32_t pad_;
-};
-
-constexpr int kBlockUnroll = 4;
-
-// One tensor of a full block: src = the group's io rows, dst = the block.
-template <class Op>
-__device__ __forceinline__ void write_dense_block(const char *src, char *dst,
-                                                  int bc_log2,
-                                                  const BlockWriteArgs &bw,
-                                                  float scale, char *lds) {
-  const int n_log2 = bw.nchunks_log2;
-  const int total = 1 << (bw.bs_log2 + n_log2);
-  const int tid = (int)threadIdx.x;
-  if (bc_log2 == n_log2) {  // row-dense: destination order == source order
-    int f = tid;
-    for (; f + (kBlockUnroll - 1) * kBlockThreads < total;
-         f += kBlockUnroll * kBlockThreads) {
-      Raw<Op::kSrc> x[kBlockUnroll];
-#pragma unroll
-      for (int u = 0; u < kBlockUnroll; ++u)
-        x[u] = ld<Op::kSrc>(src + (int64_t)(f + u * kBlockThreads) * Op::kSrc);
-#pragma unroll
-      for (int u = 0; u < kBlockUnroll; ++u)
-        st<Op::kDst>(dst + (int64_t)(f + u * kBlockThreads) * Op::kDst,
-                     Op::apply(x[u], scale));
-    }
-    for (; f < total; f += kBlockThreads)
-      st<Op::kDst>(dst + (int64_t)f * Op::kDst,
-                   Op::apply(ld<Op::kSrc>(src + (int64_t)f * Op::kSrc), scale));
-    return;
-  }
-  // Stage the rows in LDS: chunk c of row o at lds[o * pitch + c].
-  const int nmask = (1 << n_log2) - 1;
-  int f = tid;
-  for (; f + (kBlockUnroll - 1) * kBlockThreads < total;
-       f += kBlockUnroll * kBlockThreads) {
-    Raw<Op::kSrc> x[kBlockUnroll];
-#pragma unroll
-    for (int u = 0; u < kBlockUnroll; ++u)
-      x[u] = ld<Op::kSrc>(src + (int64_t)(f + u * kBlockThreads) * Op::kSrc);
-#pragma unroll
-    for (int u = 0; u < kBlockUnroll; ++u) {
-      const int g = f + u * kBlockThreads;
-      st<Op::kSrc>(lds + ((g >> n_log2) * bw.pitch + (g & nmask)) * Op::kSrc, x[u]);
-    }
-  }
-  for (; f < total; f += kBlockThreads)
-    st<Op::kSrc>(lds + ((f >> n_log2) * bw.pitch + (f & nmask)) * Op::kSrc,
-                 ld<Op::kSrc>(src + (int64_t)f * Op::kSrc));
-  __syncthreads();
-  const int bcmask = (1 << bc_log2) - 1;
-  const int bsmask = (1 << bw.bs_log2) - 1;
-  for (int u = tid; u < total; u += kBlockThreads) {
-    const int w = u & bcmask;
-    const int q = u >> bc_log2;
-    const int o = q & bsmask;
-    const int c = ((q >> bw.bs_log2) << bc_log2) + w;
-    st<Op::kDst>(dst + (int64_t)u * Op::kDst,
-                 Op::apply(ld<Op::kSrc>(lds + (o * bw.pitch + c) * Op::kSrc), scale));
-  }
-  __syncthreads();  // the LDS tile is reused by the next tensor
-}
-
-template <class Op>
-__global__ __launch_bounds__(kBlockThreads) void write_blocks_kernel(WriteArgs a,
-                                                                     BlockWriteArgs bw) {
-  extern __shared__ __attribute__((aligned(16))) char lds[];
-  __shared__ int64_t s_block;
-  __shared__ int32_t s_full;
-  const int bs = 1 << bw.bs_log2;
-  const int64_t t0 = (int64_t)blockIdx.x << bw.bs_log2;
+// Wave 0 tests whether tokens [t0, t0 + bs) hold slots b * bs + 0 .. bs - 1
+// in order with b < num_blocks; the answer and b go to *full / *block (LDS),
+// read after the caller's __syncthreads().
+__device__ __forceinline__ void group_fills_block(const WriteArgs &a, int64_t t0, int bs_log2,
+                                                  int32_t *full, int64_t *block) {
   const int tid = (int)threadIdx.x;
   const int lane = tid & (kWave - 1);
-
-  // Per-tensor scales only: the host keeps indexed scales on write_kernel.
-  float ks = 1.0f;
-  float vs = 1.0f;
-  if constexpr (Op::kScaled) {
-    ks = a.ksc.p[0];
-    vs = a.vsc.p[0];
-  }
-
-  if (tid < kWave) {  // wave 0 checks that the group fills one block in order
+  const int bs = 1 << bs_log2;
+  if (tid < kWave) {
     const int64_t t = t0 + lane;
     int64_t slot = -1;
     if (lane < bs && t < a.num_tokens) slot = load_index(a.slots, t, a.slot_is64);
@@ -613,26 +531,22 @@ __global__ __launch_bounds__(kBlockThreads) void write_blocks_kernel(WriteArgs a
     const uint64_t all = __ballot(in_order);
     if (lane == 0) {
       const bool base = first >= 0 && (first & (bs - 1)) == 0 &&
-                        (first >> bw.bs_log2) < a.num_blocks;
-      s_full = (all == ~0ull) && base;
-      s_block = first >> bw.bs_log2;
+                        (first >> bs_log2) < a.num_blocks;
+      *full = (all == ~0ull) && base;
+      *block = first >> bs_log2;
     }
   }
-  __syncthreads();
+}
 
-  if (s_full) {
-    const int64_t b = s_block;
-    const int64_t src0 = t0 * a.row_bytes;
-    write_dense_block<Op>(a.src_k + src0, a.dst_k + b * a.gk.s_block, bw.k_bc_log2, bw,
-                          ks, lds);
-    write_dense_block<Op>(a.src_v + src0, a.dst_v + b * a.gv.s_block, bw.v_bc_log2, bw,
-                          vs, lds);
-    return;
-  }
-
-  // Per-token path: wave w takes tokens w, w + 4, ... of the group.
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  for (int o = wave; o < bs; o += kWavesPerBlock) {
+// Per-token write of the tokens [t0, t0 + bs) of a group that does not fill
+// a block, shared by `nwaves` waves: this workgroup's wave w is wave
+// wave0 + w of them and takes tokens wave0 + w, wave0 + w + nwaves, ...
+template <class Op>
+__device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t0, int bs,
+                                                   float ks, float vs, int wave0, int nwaves) {
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  for (int o = wave0 + wave; o < bs; o += nwaves) {
     const int64_t t = t0 + o;
     if (t >= a.num_tokens) break;
     const int64_t slot = load_index(a.slots, t, a.slot_is64);
@@ -651,6 +565,161 @@ __global__ __launch_bounds__(kBlockThreads) void write_blocks_kernel(WriteArgs a
       st<Op::kDst>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim), Op::apply(xk, ks));
       st<Op::kDst>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim), Op::apply(xv, vs));
     }
+  }
+}
+
+// Tiled block write: the inverse of gather_tiles_kernel (below) for groups
+// of bs tokens that fill one cache block in order.  A workgroup takes tile
+// `tile` (tw cache bytes of every row) of one tensor (blockIdx.y: K 0, V 1)
+// of one group:
+//   phase 1  reads the tile's columns of the bs source rows, applies the
+//            chunk op (copy, or FP8 quantization with a per-tensor scale)
+//            and stores the cache bytes in LDS rows (pitch tw + 16 bytes);
+//   phase 2  assembles each 16-byte chunk of the block region
+//            [tile * tw * bs, (tile + 1) * tw * bs) from its run pieces and
+//            stores it, so the cache side is written in whole 16-byte lanes.
+// A row-major tensor copies its rows straight through.  A group that does
+// not fill a block is written token by token (K and V rows together), its
+// tokens spread over the waves of all 2 * tiles workgroups of the group.
+struct WriteTileArgs {
+  int32_t tiles;          // tiles per block: cache row bytes / tw
+  int32_t tw_log2;        // tile width, cache bytes per row
+  int32_t pitch;          // LDS row pitch, bytes
+  int32_t bs_log2;
+  int32_t run_log2[2];    // K, V: log2 bytes of a per-token run; -1 row-major
+  int32_t cache_es_log2;  // log2 cache element bytes
+  int32_t io_es_log2;     // log2 io element bytes
+};
+
+// Piece k (PIECE bytes) of a 16-byte chunk, read from p into x (x's other
+// pieces untouched; x starts zeroed for PIECE < 4).
+template <int PIECE>
+__device__ __forceinline__ void get_piece(const char *p, Raw<16> &x, int k) {
+  if constexpr (PIECE == 16) {
+    x = ld<16>(p);
+  } else if constexpr (PIECE == 8) {
+    const Raw<8> y = ld<8>(p);
+    x.w[2 * k] = y.w[0];
+    x.w[2 * k + 1] = y.w[1];
+  } else if constexpr (PIECE == 4) {
+    x.w[k] = ld<4>(p).w[0];
+  } else if constexpr (PIECE == 2) {
+    put16(x, k, ld<2>(p).w[0]);
+  } else {
+    put8(x, k, ld<1>(p).w[0]);
+  }
+}
+
+// Phase 2 of the tiled write: LDS rows -> region (nbytes = tw * bs cache
+// bytes, 16-byte aligned).  PIECE = min(run bytes, 16).
+template <int PIECE>
+__device__ __forceinline__ void unstage_tile(char *region, const char *lds, int32_t nbytes,
+                                             int32_t run_log2, int32_t bs_log2, int32_t pitch) {
+  const int32_t bsm = (1 << bs_log2) - 1;
+  const int32_t runm = (1 << run_log2) - 1;
+  constexpr int32_t kStep = kBlockThreads * 16;
+  for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
+    Raw<16> x[kTileLoads];
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[u].w[i] = 0;
+      if (m < nbytes) {
+#pragma unroll
+        for (int k = 0; k < 16 / PIECE; ++k) {
+          const int32_t mm = m + k * PIECE;
+          const int32_t o = (mm >> run_log2) & bsm;
+          const int32_t ar = mm >> (run_log2 + bs_log2);
+          get_piece<PIECE>(lds + o * pitch + (ar << run_log2) + (mm & runm), x[u], k);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+      if (m < nbytes) st<16>(region + m, x[u]);
+    }
+  }
+}
+
+// Op: the tile's chunk op (16-byte cache chunks); TokOp: the per-token
+// path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
+template <class Op, class TokOp>
+__global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
+                                                                    WriteTileArgs wt) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ int64_t s_block;
+  __shared__ int32_t s_full;
+  const uint32_t gu = blockIdx.x / (uint32_t)wt.tiles;
+  const int32_t tile = (int32_t)(blockIdx.x - gu * (uint32_t)wt.tiles);
+  const int64_t t0 = (int64_t)gu << wt.bs_log2;
+  const bool v = blockIdx.y != 0;
+  float ks = 1.0f;  // per-tensor scales only
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
+  }
+  group_fills_block(a, t0, wt.bs_log2, &s_full, &s_block);
+  __syncthreads();
+  if (!s_full) {
+    write_group_tokens<TokOp>(a, t0, 1 << wt.bs_log2, ks, vs,
+                              ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
+                              2 * wt.tiles * kWavesPerBlock);
+    return;
+  }
+  const char *src = (v ? a.src_v : a.src_k) + t0 * a.row_bytes;
+  char *blk = v ? a.dst_v + s_block * a.gv.s_block : a.dst_k + s_block * a.gk.s_block;
+  const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
+  const float scale = v ? vs : ks;
+  const int32_t region = (1 << wt.tw_log2) << wt.bs_log2;
+  char *dst = blk + (int64_t)tile * region;
+  const int tid = (int)threadIdx.x;
+
+  if (run_log2 < 0) {
+    // Row-major block: the block region is the same span of the source rows.
+    const int32_t lo = tile * region;
+    for (int32_t m = lo + tid * Op::kDst; m < lo + region; m += kBlockThreads * Op::kDst) {
+      const uint32_t e = (uint32_t)m >> wt.cache_es_log2;
+      st<Op::kDst>(blk + m, Op::apply(ld<Op::kSrc>(src + ((int64_t)e << wt.io_es_log2)), scale));
+    }
+    return;
+  }
+
+  // Phase 1: chunk c of row r holds the row's io elements e0 + c * G.
+  constexpr int kDstLog2 = Op::kDst == 16 ? 4 : Op::kDst == 8 ? 3 : Op::kDst == 4 ? 2
+                           : Op::kDst == 2 ? 1 : 0;
+  const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
+  const int32_t total = 1 << (wt.bs_log2 + cpr_log2);
+  const int32_t cm = (1 << cpr_log2) - 1;
+  const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
+  for (int32_t u0 = tid; u0 < total; u0 += kTileLoads * kBlockThreads) {
+    Raw<Op::kSrc> x[kTileLoads];
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if (u < total) {
+        const uint32_t e = e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
+        x[k] = ld<Op::kSrc>(src + (int64_t)(u >> cpr_log2) * a.row_bytes +
+                            ((int64_t)e << wt.io_es_log2));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if (u < total)
+        st<Op::kDst>(lds + (u >> cpr_log2) * wt.pitch + ((u & cm) << kDstLog2),
+                     Op::apply(x[k], scale));
+    }
+  }
+  __syncthreads();
+  switch (run_log2) {
+    case 0: unstage_tile<1>(dst, lds, region, 0, wt.bs_log2, wt.pitch); break;
+    case 1: unstage_tile<2>(dst, lds, region, 1, wt.bs_log2, wt.pitch); break;
+    case 2: unstage_tile<4>(dst, lds, region, 2, wt.bs_log2, wt.pitch); break;
+    case 3: unstage_tile<8>(dst, lds, region, 3, wt.bs_log2, wt.pitch); break;
+    default: unstage_tile<16>(dst, lds, region, run_log2, wt.bs_log2, wt.pitch); break;
   }
 }
 
@@ -920,8 +989,6 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
 // straight through.  blockIdx.y selects K (0) or V (1).  PACKED tables give
 // the block id of (sequence, logical block); KV_OFFSETS tables give K's and
 // V's block addresses separately (pool + index * bytes_per_block).
-constexpr int kTileLoads = 4;  // 16-byte chunks per thread in flight
-constexpr int kTilePad = 16;   // LDS row padding, bytes
 
 struct TileTensor {
   const char *src;    // cache tensor
@@ -1454,21 +1521,36 @@ int lpt_log2_for(int nchunks) {
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
-// How a write launches: the per-token kernel, or the block kernel with its
-// LDS tile size and one workgroup per `bs` tokens.
+// How a write launches: the per-token kernel, or the tiled block kernel
+// (one workgroup per tile of a group's block, per tensor) with its LDS
+// tile size.
 struct WriteLaunch {
   int grid;
-  bool blocks;
-  BlockWriteArgs bw;
-  int64_t block_grid;
-  uint32_t lds_bytes;
+  bool tiles;
+  WriteTileArgs wt;
+  int64_t tile_grid;
+  uint32_t tile_lds;
+};
+
+// The tiled write moves 16-byte cache chunks: a copy of 16 bytes, or a
+// quantization of 8 elements.
+template <class Op>
+struct TileOpOf;
+template <int B>
+struct TileOpOf<CopyOp<B>> {
+  using type = CopyOp<16>;
+};
+template <int G, int IO, int F8>
+struct TileOpOf<QuantOp<G, IO, F8>> {
+  using type = QuantOp<8, IO, F8>;
 };
 
 template <class Op>
 void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
-  if (w.blocks) {
-    hipLaunchKernelGGL(write_blocks_kernel<Op>, dim3((uint32_t)w.block_grid),
-                       dim3(kBlockThreads), w.lds_bytes, s, a, w.bw);
+  if (w.tiles) {
+    hipLaunchKernelGGL((write_tiles_kernel<typename TileOpOf<Op>::type, Op>),
+                       dim3((uint32_t)w.tile_grid, 2), dim3(kBlockThreads), w.tile_lds, s, a,
+                       w.wt);
   } else {
     hipLaunchKernelGGL(write_kernel<Op>, dim3(w.grid), dim3(kBlockThreads), 0, s, a);
   }
@@ -1704,42 +1786,59 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   return *grid <= 0x7FFFFFFF;
 }
 
-// Chunks per contiguous per-token run when `g` is a dense block (the layout's
-// canonical in-block strides, any block stride), else -1.
-int64_t dense_run_chunks(const Geom &g, int64_t bs, int64_t H, int64_t D, int ge) {
-  if (g.s_inner != 1) return -1;
-  const int64_t E = H * D;
-  const int64_t p = g.pack;
-  if (p == D && g.s_piece == 0 && g.s_head == D && g.s_off == E) return E / ge;  // NHD
-  if (p == D && g.s_piece == 0 && g.s_off == D && g.s_head == bs * D) return D / ge;  // HND
-  if (p < D && g.s_off == p && g.s_piece == bs * p && g.s_head == (D / p) * bs * p)
-    return p / ge;  // HND_PACKED
-  return -1;
-}
-
-// Use the block kernel when some tensor is not row-dense (it needs the
-// in-block permutation), both are dense blocks with power-of-two shapes, and
-// the LDS tile fits in 64 KiB.
-bool plan_block_write(const WritePlan &p, int ge, int nchunks, int src_chunk_bytes,
-                      BlockWriteArgs *bw, int64_t *grid, uint32_t *lds_bytes) {
+// Tiled block write plan (write_tiles_kernel): per-tensor scales, at least
+// bs tokens, power-of-two bs (<= one wave) and cache row bytes, dense
+// blocks of which at least one is not row-major, 16-byte aligned block
+// addresses and io rows aligned to the tile op's source chunk.
+// KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile; on MI355X (c3
+// shapes) 16 KiB measured best against 8 and 32 KiB, and 0-5% faster than
+// staging whole blocks of K and V in one workgroup (x-packed / HND), 5x for
+// the token-innermost value cache.
+#ifndef KVX_WRITE_TILE_BYTES
+#define KVX_WRITE_TILE_BYTES 16384
+#endif
+bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int64_t *grid,
+                      uint32_t *lds_bytes) {
   const int64_t bs = p.block_size;
-  if (bs > kWave || p.num_tokens < bs) return false;
-  const int64_t kbc = dense_run_chunks(p.gk, bs, p.heads, p.head_dim, ge);
-  const int64_t vbc = dense_run_chunks(p.gv, bs, p.heads, p.head_dim, ge);
-  if (kbc < 0 || vbc < 0) return false;
-  if (kbc == nchunks && vbc == nchunks) return false;  // both row-major: per-token kernel
-  bw->bs_log2 = log2_exact(bs);
-  bw->nchunks_log2 = log2_exact(nchunks);
-  bw->k_bc_log2 = log2_exact(kbc);
-  bw->v_bc_log2 = log2_exact(vbc);
-  if (bw->bs_log2 < 0 || bw->nchunks_log2 < 0 || bw->k_bc_log2 < 0 || bw->v_bc_log2 < 0)
-    return false;
-  bw->pitch = nchunks + 1;
-  bw->pad_ = 0;
-  const int64_t lds = bs * (int64_t)bw->pitch * src_chunk_bytes;
-  if (lds > 64 * 1024) return false;
-  *lds_bytes = (uint32_t)lds;
-  *grid = (p.num_tokens + bs - 1) / bs;
+  const int64_t H = p.heads;
+  const int64_t D = p.head_dim;
+  const int64_t row_cache = H * D * cs;
+  const int bs_log2 = log2_exact(bs);
+  if (bs_log2 < 0 || bs > kWave || p.num_tokens < bs) return false;
+  if (log2_exact(row_cache) < 0 || row_cache < 16) return false;
+  const int src_chunk = p.conv == kConvQuant ? 8 * is : 16;
+  const Geom *g[2] = {&p.gk, &p.gv};
+  const void *src[2] = {p.src_k, p.src_v};
+  const void *dst[2] = {p.dst_k, p.dst_v};
+  bool transposed = false;
+  int64_t min_tw = 16;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t w = dense_run_elems(*g[i], bs, H, D);
+    if (w < 0) return false;
+    wt->run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
+    if (w != H * D) {
+      if (wt->run_log2[i] < 0) return false;
+      transposed = true;
+      if (w * cs > min_tw) min_tw = w * cs;
+    }
+    if ((reinterpret_cast<uintptr_t>(dst[i]) | (uintptr_t)(g[i]->s_block * cs)) % 16 != 0)
+      return false;
+    if ((reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(H * D * is)) % src_chunk != 0)
+      return false;
+  }
+  if (!transposed) return false;
+  int64_t tw = row_cache;
+  while (tw * bs > KVX_WRITE_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  const int64_t pitch = tw + kTilePad;
+  if (bs * pitch > 64 * 1024) return false;
+  wt->tiles = (int32_t)(row_cache / tw);
+  wt->tw_log2 = log2_exact(tw);
+  wt->pitch = (int32_t)pitch;
+  wt->bs_log2 = bs_log2;
+  wt->cache_es_log2 = log2_exact(cs);
+  wt->io_es_log2 = log2_exact(is);
+  *grid = (p.num_tokens + bs - 1) / bs * wt->tiles;
+  *lds_bytes = (uint32_t)(bs * pitch);
   return *grid <= 0x7FFFFFFF;
 }
 
@@ -1790,9 +1889,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   wl.grid = (int)(want < 2048 ? want : 2048);
   // The block kernel applies per-tensor scales only.
   const bool indexed = p.k_scale.indexed || p.v_scale.indexed;
-  wl.blocks = !indexed &&
-              plan_block_write(p, ge, a.nchunks, (p.conv == kConvQuant) ? ge * is : ge * cs,
-                               &wl.bw, &wl.block_grid, &wl.lds_bytes);
+  wl.tiles = !indexed && plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   hipStream_t s = as_stream(stream);
 
   if (p.conv == kConvCopy) {

@@ -1,22 +1,26 @@
-"""GPU parity of the transposing gather (gather_tiles_kernel): PACKED-table
-gathers of dense blocks whose per-token runs are short — token axis
-innermost (vLLM's value cache [num_blocks, H, D, block_size]), x-packed
-HND_PACKED, HND with short heads — through the C ABI, bit-identical to the
-CPU oracle (kernels/kvx_paged_kv.cu:226-267 semantics).
+"""GPU parity of the LDS tile kernels: the transposing gather
+(gather_tiles_kernel) and the tiled block write (write_tiles_kernel), for
+dense blocks that are not row-major — token axis innermost (vLLM's value
+cache [num_blocks, H, D, block_size]), x-packed HND_PACKED, HND — through
+the C ABI, bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:93-124
+write and :226-267 gather semantics).
 
-Cases cover every LDS piece size (1, 2, 4, 8, 16 bytes), runs shorter than
-one 16-byte load (block_size * run < 16), blocks split into several tiles,
-a row-major partner tensor, partial last blocks, block ids < 0 and
->= num_blocks, seq_len beyond max_seq_len, int64 indices, and the FP8
-dequantizing gather with per-tensor, per-head and per-block-head scales.
+Gather cases cover every LDS piece size (1, 2, 4, 8, 16 bytes), runs
+shorter than one 16-byte load (block_size * run < 16), blocks split into
+several tiles, a row-major partner tensor, partial last blocks, block ids
+< 0 and >= num_blocks, seq_len beyond max_seq_len, int64 indices, and the
+FP8 dequantizing gather with per-tensor, per-head and per-block-head
+scales.  Write cases cover the same layouts with groups that fill a block
+in order, groups that do not (partial, out of order, invalid slots, a
+ragged tail), and the quantizing FP8 write.
 """
 import pytest
 import torch
 
 from kvx_amd.abi import DType, Layout, ScaleGranularity as SG
 
-from gpu_helpers import (TORCH_DT, ScaleArg, check_gather, custom_cache, make_cache,
-                         random_fill)
+from gpu_helpers import (TORCH_DT, ScaleArg, check_gather, check_write, custom_cache,
+                         make_cache, random_fill)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -101,3 +105,72 @@ def test_tiles_hnd_packed_layouts(entry):
     vo = random_fill(torch.empty_like(ko), gen)
     check_gather(pc, kb, vb, ko, vo, table.to(DEV), lens.to(DEV), L, cache_dtype=DType.BF16,
                  io_dtype=DType.BF16, entry=entry)
+
+
+def _prefill_slots(gen, nb, bs, groups, tail, spoil):
+    """Slots of `groups` full blocks in order (random distinct blocks), then
+    `tail` tokens; `spoil` groups get one slot changed (-1, a swap, or a
+    block past the end) so that they take the per-token path."""
+    blocks = torch.randperm(nb, generator=gen)[: groups + 1]
+    slots = (blocks[:groups, None] * bs + torch.arange(bs)).reshape(-1)
+    slots = torch.cat([slots, blocks[groups] * bs + torch.arange(tail)])
+    for i, g in enumerate(torch.randperm(groups, generator=gen)[:spoil].tolist()):
+        o = int(torch.randint(0, bs, (1,), generator=gen))
+        if i % 3 == 0:
+            slots[g * bs + o] = -1
+        elif i % 3 == 1 and bs > 1:
+            a, b = g * bs + o, g * bs + (o + 1) % bs
+            slots[a], slots[b] = slots[b].clone(), slots[a].clone()
+        else:
+            slots[g * bs + o] = nb * bs + o
+    return slots
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+@pytest.mark.parametrize("slot64", [False, True])
+def test_tiles_write(case, slot64):
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    gen = torch.Generator().manual_seed(200 + CASES.index(case) * 2 + int(slot64))
+    nb = 48
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    groups = 12
+    slots = _prefill_slots(gen, nb, bs, groups, tail=max(1, bs // 2 - 1), spoil=3)
+    T = slots.numel()
+    key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    slots = slots.to(torch.int64 if slot64 else torch.int32).to(DEV)
+    check_write(pc, kb, vb, key, val, slots, io_dtype=dt, cache_dtype=dt)
+
+
+@pytest.mark.parametrize("fp8", [DType.F8_E4M3, DType.F8_E5M2])
+@pytest.mark.parametrize("io", [DType.BF16, DType.F16, DType.F32])
+def test_tiles_quantizing_write(fp8, io):
+    """K token-innermost, V x-packed x = 16: the tile op quantizes 8
+    elements per chunk; per-tensor scales (indexed scales use the per-token
+    kernel)."""
+    gen = torch.Generator().manual_seed(300 + int(fp8) * 10 + int(io))
+    H, D, bs, nb = 8, 128, 16, 40
+    pc, kb, vb = custom_cache(fp8, nb, bs, H, D, "bhdo", "bhpox", None, 16, gen)
+    slots = _prefill_slots(gen, nb, bs, groups=10, tail=5, spoil=2)
+    T = slots.numel()
+    key = (torch.randn((T, H, D), generator=gen) * 4).to(TORCH_DT[io]).to(DEV)
+    val = (torch.randn((T, H, D), generator=gen) * 0.5).to(TORCH_DT[io]).to(DEV)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=fp8,
+                k_scale=0.011, v_scale=0.0021)
+
+
+@pytest.mark.parametrize("entry", ["launch", "prefill", "abi"])
+def test_tiles_write_x_packed_entries(entry):
+    """c3's pairing (K HND_PACKED x = 8, V NHD) through kvx_launch_write_kv,
+    the prefill entry and (same layout code for K and V) kvx_write_kv."""
+    gen = torch.Generator().manual_seed(320 + ["launch", "prefill", "abi"].index(entry))
+    H, D, bs, nb = 8, 128, 16, 64
+    vl = Layout.BLOCK_HND_PACKED if entry == "abi" else Layout.BLOCK_NHD
+    pc, kb, vb = make_cache(Layout.BLOCK_HND_PACKED, vl, DType.BF16, nb, bs, H, D, 8, gen=gen)
+    slots = _prefill_slots(gen, nb, bs, groups=16, tail=0, spoil=1)
+    T = slots.numel()
+    key = random_fill(torch.empty((T, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    kw = dict(tokens_per_seq=64) if entry == "prefill" else {}
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16,
+                cache_dtype=DType.BF16, entry="abi" if entry == "abi" else "launch", **kw)
