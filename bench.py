@@ -171,13 +171,14 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
             fill(pool.key_cache)
             return pc, pool
         if wl.v_layout == Layout.BLOCK_CUSTOM:  # --layout vllm
-            pk = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
-                                   tdt[wl.cache_dtype], dev, wl.k_layout, wl.k_layout,
-                                   wl.pack)
-            pv = paged.alloc_custom_cache(wl.num_blocks, wl.block_size, wl.heads,
-                                          wl.head_dim, tdt[wl.cache_dtype], dev, "bhdo")
-            pc = paged.PagedCache(pk.key_cache, pv.value_cache, wl.k_layout, wl.v_layout,
-                                  wl.num_blocks, wl.block_size, wl.heads, wl.head_dim)
+            kc = torch.empty(paged.cache_shape(wl.k_layout, wl.num_blocks, wl.block_size,
+                                               wl.heads, wl.head_dim, wl.pack),
+                             dtype=tdt[wl.cache_dtype], device=dev)
+            vstore = torch.empty((wl.num_blocks, wl.heads, wl.head_dim, wl.block_size),
+                                 dtype=tdt[wl.cache_dtype], device=dev)
+            pc = paged.PagedCache(kc, paged.custom_view(vstore, "bhdo"), wl.k_layout,
+                                  wl.v_layout, wl.num_blocks, wl.block_size, wl.heads,
+                                  wl.head_dim)
         else:
             pc = paged.alloc_cache(wl.num_blocks, wl.block_size, wl.heads, wl.head_dim,
                                    tdt[wl.cache_dtype], dev, wl.k_layout, wl.v_layout,
