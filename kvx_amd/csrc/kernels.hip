@@ -1008,7 +1008,11 @@ __global__ __launch_bounds__(kBlockThreads) void gather_rows_kernel(GatherArgs a
 // A row-major tensor paired with such a tensor copies its valid rows
 // straight through.  blockIdx.y selects K (0) or V (1).  PACKED tables give
 // the block id of (sequence, logical block); KV_OFFSETS tables give K's and
-// V's block addresses separately (pool + index * bytes_per_block).
+// V's block addresses separately (pool + index * bytes_per_block).  RAGGED
+// tables give every row its own block id: a tile's rows t0 .. t0 + bs - 1
+// sit at offsets 0 .. bs - 1 of their blocks, so a tile whose rows all name
+// one block is gathered like a PACKED one, and any other tile reads each
+// row's pieces from that row's block (the first wave compares the ids).
 
 struct TileTensor {
   const char *src;    // cache tensor
@@ -1023,6 +1027,8 @@ struct TileArgs {
   TileTensor t[2];
   const void *table;
   const void *seq_lens;
+  const void *indptr;       // RAGGED
+  int64_t table_count;      // RAGGED: entries of `table`
   const char *pool[2];      // KV_OFFSETS primary / secondary
   int64_t bytes_per_block;  // KV_OFFSETS
   int64_t out_row_bytes;
@@ -1100,9 +1106,34 @@ __device__ __forceinline__ void stage_tile(const char *region, char *lds, int32_
   }
 }
 
-template <class Op, int FMT, bool I64>
+// Phase 1 for a RAGGED tile whose rows name different blocks: every piece
+// is loaded from its own row's block, ids[o] (< 0: row skipped); `off` is
+// the tile's region offset within a block.
+template <int PIECE>
+__device__ __forceinline__ void stage_tile_rows(const char *src, int64_t s_block, int32_t off,
+                                                const int64_t *ids, char *lds, int32_t nbytes,
+                                                int32_t run_log2, int32_t bs_log2, int32_t pitch,
+                                                int32_t rows) {
+  const int32_t bsm = (1 << bs_log2) - 1;
+  const int32_t runm = (1 << run_log2) - 1;
+  for (int32_t mm = (int32_t)threadIdx.x * PIECE; mm < nbytes; mm += kBlockThreads * PIECE) {
+    const int32_t o = (mm >> run_log2) & bsm;
+    if (o >= rows) continue;
+    const int64_t id = ids[o];
+    if (id < 0) continue;
+    const int32_t ar = mm >> (run_log2 + bs_log2);
+    st<PIECE>(lds + o * pitch + (ar << run_log2) + (mm & runm),
+              ld<PIECE, kGatherNtLoad>(src + id * s_block + off + mm));
+  }
+}
+
+// I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
+// indptr dtype.
+template <class Op, int FMT, bool I64, bool P64>
 __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
+  __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
   const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
   const uint32_t wg = blockIdx.x;
   const uint32_t per_seq = (uint32_t)a.blocks_per_seq * (uint32_t)a.tiles;
@@ -1112,28 +1143,64 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
   const int32_t tile = (int32_t)(w - lbu * (uint32_t)a.tiles);
   const int32_t lb = (int32_t)lbu;
   const int64_t s = su;
-  if (lb >= a.max_blocks_per_seq) return;
-  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
-  int64_t bid;
-  const char *blk;
-  if constexpr (FMT == KVX_BLOCK_TABLE_KV_OFFSETS) {
-    // table [seq, beam = 1, {K, V}, max_blocks_per_seq] of KVCacheIndex
-    const uint32_t ent = reinterpret_cast<const uint32_t *>(
-        a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
-    const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
-    bid = ent & 0x7FFFFFFFu;
-    if (pool == nullptr || bid >= a.num_blocks) return;
-    blk = pool + bid * a.bytes_per_block;
-  } else {
-    bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
-    if (bid < 0 || bid >= a.num_blocks) return;
-    blk = tt.src + bid * tt.s_block;
-  }
-  const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
   const int64_t t0 = (int64_t)lb << a.bs_log2;
-  if (t0 >= n) return;
-  const int64_t rem = n - t0;
   const int32_t bs = 1 << a.bs_log2;
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  int64_t bid;
+  const char *blk = nullptr;
+  bool mixed = false;  // RAGGED tile whose rows name different blocks
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    // row t is token start + t (KVX_SPEC.md:107-114), at offset t % bs
+    const int64_t start = load_idx<P64>(a.indptr, s);
+    const int64_t end = load_idx<P64>(a.indptr, s + 1);
+    int64_t cnt = end - start;
+    const int64_t left = a.table_count - start;  // entries the table holds
+    cnt = left < cnt ? left : cnt;
+    n = cnt < n ? cnt : n;
+    if (start < 0) n = 0;
+    if (t0 >= n) return;
+    const int64_t rem = n - t0;
+    const int32_t rws = rem < bs ? (int32_t)rem : bs;
+    if (threadIdx.x < kWave) {
+      const int lane = (int)threadIdx.x;
+      int64_t id = -1;
+      if (lane < rws) {
+        id = load_idx<I64>(a.table, start + t0 + lane);
+        if (id < 0 || id >= a.num_blocks) id = -1;
+        s_ids[lane] = id;
+      }
+      const int64_t first =
+          (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(id >> 32)) << 32) |
+                    (uint32_t)__builtin_amdgcn_readfirstlane((int)id));
+      const uint64_t same = __ballot(lane >= rws || id == first);
+      if (lane == 0) s_same = same == ~0ull;
+    }
+    __syncthreads();
+    bid = s_ids[0];
+    mixed = !s_same;
+    if (!mixed) {
+      if (bid < 0) return;  // every row skipped
+      blk = tt.src + bid * tt.s_block;
+    }
+  } else {
+    if (lb >= a.max_blocks_per_seq) return;
+    if constexpr (FMT == KVX_BLOCK_TABLE_KV_OFFSETS) {
+      // table [seq, beam = 1, {K, V}, max_blocks_per_seq] of KVCacheIndex
+      const uint32_t ent = reinterpret_cast<const uint32_t *>(
+          a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
+      const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
+      bid = ent & 0x7FFFFFFFu;
+      if (pool == nullptr || bid >= a.num_blocks) return;
+      blk = pool + bid * a.bytes_per_block;
+    } else {
+      bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+      if (bid < 0 || bid >= a.num_blocks) return;
+      blk = tt.src + bid * tt.s_block;
+    }
+    if (t0 >= n) return;
+  }
+  const int64_t rem = n - t0;
   const int32_t rows = rem < bs ? (int32_t)rem : bs;
   float uniform = 1.0f;
   if constexpr (Op::kScaled) uniform = tt.sc.p[0];
@@ -1151,21 +1218,41 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     const int32_t hi = (int32_t)(lo + region < valid ? lo + region : valid);
     for (int32_t m = lo + (int32_t)threadIdx.x * Op::kSrc; m < hi; m += kBlockThreads * Op::kSrc) {
       const uint32_t e = (uint32_t)m >> a.cache_es_log2;
+      int64_t rb = bid;
+      const char *b = blk;
+      if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+        if (mixed) {
+          rb = s_ids[e / re];
+          if (rb < 0) continue;
+          b = tt.src + rb * tt.s_block;
+        }
+      }
       float sc = uniform;
-      if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, bid, (e % re) / hd);
+      if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, rb, (e % re) / hd);
       st<Op::kDst, kGatherNtStore>(out + ((int64_t)e << a.io_es_log2),
-                                   Op::apply(ld<Op::kSrc, kGatherNtLoad>(blk + m), sc));
+                                   Op::apply(ld<Op::kSrc, kGatherNtLoad>(b + m), sc));
     }
     return;
   }
 
-  const char *src = blk + (int64_t)tile * region;
-  switch (tt.run_log2) {
-    case 0: stage_tile<1>(src, lds, region, 0, a.bs_log2, a.pitch, rows); break;
-    case 1: stage_tile<2>(src, lds, region, 1, a.bs_log2, a.pitch, rows); break;
-    case 2: stage_tile<4>(src, lds, region, 2, a.bs_log2, a.pitch, rows); break;
-    case 3: stage_tile<8>(src, lds, region, 3, a.bs_log2, a.pitch, rows); break;
-    default: stage_tile<16>(src, lds, region, tt.run_log2, a.bs_log2, a.pitch, rows); break;
+  if (mixed) {
+    const int32_t off = tile * region;
+    switch (tt.run_log2) {
+      case 0: stage_tile_rows<1>(tt.src, tt.s_block, off, s_ids, lds, region, 0, a.bs_log2, a.pitch, rows); break;
+      case 1: stage_tile_rows<2>(tt.src, tt.s_block, off, s_ids, lds, region, 1, a.bs_log2, a.pitch, rows); break;
+      case 2: stage_tile_rows<4>(tt.src, tt.s_block, off, s_ids, lds, region, 2, a.bs_log2, a.pitch, rows); break;
+      case 3: stage_tile_rows<8>(tt.src, tt.s_block, off, s_ids, lds, region, 3, a.bs_log2, a.pitch, rows); break;
+      default: stage_tile_rows<16>(tt.src, tt.s_block, off, s_ids, lds, region, tt.run_log2, a.bs_log2, a.pitch, rows); break;
+    }
+  } else {
+    const char *src = blk + (int64_t)tile * region;
+    switch (tt.run_log2) {
+      case 0: stage_tile<1>(src, lds, region, 0, a.bs_log2, a.pitch, rows); break;
+      case 1: stage_tile<2>(src, lds, region, 1, a.bs_log2, a.pitch, rows); break;
+      case 2: stage_tile<4>(src, lds, region, 2, a.bs_log2, a.pitch, rows); break;
+      case 3: stage_tile<8>(src, lds, region, 3, a.bs_log2, a.pitch, rows); break;
+      default: stage_tile<16>(src, lds, region, tt.run_log2, a.bs_log2, a.pitch, rows); break;
+    }
   }
   __syncthreads();
 
@@ -1189,9 +1276,16 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
       const int32_t u = u0 + k * kBlockThreads;
       if (u < total) {
         const int32_t r = u >> cpr_log2;
+        int64_t rb = bid;
+        if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+          if (mixed) {
+            rb = s_ids[r];
+            if (rb < 0) continue;
+          }
+        }
         const uint32_t e = e0 + ((uint32_t)((u & cm) << kSrcLog2) >> a.cache_es_log2);
         float sc = uniform;
-        if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, bid, e / hd);
+        if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, rb, e / hd);
         st<Op::kDst, kGatherNtStore>(out + (int64_t)r * a.out_row_bytes +
                                          ((int64_t)e << a.io_es_log2),
                                      Op::apply(x[k], sc));
@@ -1621,38 +1715,46 @@ void launch_gather_op(const GatherArgs &a, int64_t grid, hipStream_t s) {
   }
 }
 
-template <class Op, int FMT>
+template <class Op, int FMT, bool P64>
 void launch_tiles_fmt(const TileArgs &t, bool i64, int64_t grid, uint32_t lds, hipStream_t s) {
   const dim3 g((uint32_t)grid, 2);
   if (i64) {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, true>), g, dim3(kBlockThreads), lds, s, t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, true, P64>), g, dim3(kBlockThreads), lds, s,
+                       t);
   } else {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, false>), g, dim3(kBlockThreads), lds, s, t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, false, P64>), g, dim3(kBlockThreads), lds,
+                       s, t);
   }
 }
 
 template <class Op>
-void launch_tiles(const TileArgs &t, int fmt, bool i64, int64_t grid, uint32_t lds,
+void launch_tiles(const TileArgs &t, int fmt, bool i64, bool p64, int64_t grid, uint32_t lds,
                   hipStream_t s) {
   if (fmt == KVX_BLOCK_TABLE_KV_OFFSETS) {
-    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_KV_OFFSETS>(t, i64, grid, lds, s);
+    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_KV_OFFSETS, false>(t, i64, grid, lds, s);
+  } else if (fmt == KVX_BLOCK_TABLE_RAGGED) {
+    if (p64) launch_tiles_fmt<Op, KVX_BLOCK_TABLE_RAGGED, true>(t, i64, grid, lds, s);
+    else launch_tiles_fmt<Op, KVX_BLOCK_TABLE_RAGGED, false>(t, i64, grid, lds, s);
   } else {
-    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_PACKED>(t, i64, grid, lds, s);
+    launch_tiles_fmt<Op, KVX_BLOCK_TABLE_PACKED, false>(t, i64, grid, lds, s);
   }
 }
 
 template <int F8>
-void launch_tiles_dequant(int io, const TileArgs &t, int fmt, bool i64, int64_t grid,
+void launch_tiles_dequant(int io, const TileArgs &t, int fmt, bool i64, bool p64, int64_t grid,
                           uint32_t lds, hipStream_t s) {
   switch (io) {
     case KVX_DTYPE_F32:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F32, F8>>(t, fmt, i64, grid, lds, s);
+      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F32, F8>>(t, fmt, i64, p64, grid, lds,
+                                                                    s);
       break;
     case KVX_DTYPE_F16:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F16, F8>>(t, fmt, i64, grid, lds, s);
+      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F16, F8>>(t, fmt, i64, p64, grid, lds,
+                                                                    s);
       break;
     default:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_BF16, F8>>(t, fmt, i64, grid, lds, s);
+      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_BF16, F8>>(t, fmt, i64, p64, grid, lds,
+                                                                     s);
       break;
   }
 }
@@ -1737,7 +1839,8 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
   const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
-  if (p.format != KVX_BLOCK_TABLE_PACKED && !offsets) return false;
+  const bool ragged = p.format == KVX_BLOCK_TABLE_RAGGED;
+  if (ragged && p.block_size > kWave) return false;  // one wave compares a tile's ids
   const int64_t bs = p.block_size;
   const int64_t H = p.heads;
   const int64_t D = p.head_dim;
@@ -1777,14 +1880,17 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   if (bs * pitch > 64 * 1024) return false;
   t->table = p.block_table;
   t->seq_lens = p.seq_lens;
+  t->indptr = p.indptr;
+  t->table_count = p.table_count;
   t->pool[0] = p.pool[0];
   t->pool[1] = p.pool[1];
   t->bytes_per_block = p.bytes_per_block;
   t->out_row_bytes = H * D * is;
   t->max_blocks_per_seq = p.max_blocks_per_seq;
   const int64_t by_len = ((int64_t)p.max_seq_len + bs - 1) / bs;
-  t->blocks_per_seq =
-      (int32_t)(by_len < p.max_blocks_per_seq ? by_len : p.max_blocks_per_seq);
+  // RAGGED rows do not use max_blocks_per_seq
+  t->blocks_per_seq = (int32_t)(ragged || by_len < p.max_blocks_per_seq ? by_len
+                                                                       : p.max_blocks_per_seq);
   t->tiles = (int32_t)(row_cache / tw);
   t->tw_log2 = log2_exact(tw);
   t->pitch = (int32_t)pitch;
@@ -1957,12 +2063,15 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     if (p.seq_count > 0 && plan_tiles(p, cs, is, dq ? KVX_DEQUANT_CHUNK : 16, &t, &tgrid, &tlds)) {
       if (tgrid == 0) return KVX_STATUS_OK;
       const bool i64 = p.lens_is64 != 0;
+      const bool p64 = p.indptr_is64 != 0;
       if (!dq) {
-        launch_tiles<CopyOp<16>>(t, p.format, i64, tgrid, tlds, s);
+        launch_tiles<CopyOp<16>>(t, p.format, i64, p64, tgrid, tlds, s);
       } else if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
-        launch_tiles_dequant<KVX_DTYPE_F8_E5M2>(p.io_dtype, t, p.format, i64, tgrid, tlds, s);
+        launch_tiles_dequant<KVX_DTYPE_F8_E5M2>(p.io_dtype, t, p.format, i64, p64, tgrid, tlds,
+                                                s);
       } else {
-        launch_tiles_dequant<KVX_DTYPE_F8_E4M3>(p.io_dtype, t, p.format, i64, tgrid, tlds, s);
+        launch_tiles_dequant<KVX_DTYPE_F8_E4M3>(p.io_dtype, t, p.format, i64, p64, tgrid, tlds,
+                                                s);
       }
       return hipGetLastError() == hipSuccess ? KVX_STATUS_OK : KVX_STATUS_INTERNAL_ERROR;
     }

@@ -10,17 +10,22 @@ shorter than one 16-byte load (block_size * run < 16), blocks split into
 several tiles, a row-major partner tensor, partial last blocks, block ids
 < 0 and >= num_blocks, seq_len beyond max_seq_len, int64 indices, and the
 FP8 dequantizing gather with per-tensor, per-head and per-block-head
-scales.  Write cases cover the same layouts with groups that fill a block
+scales.  RAGGED cases cover tiles whose rows all name one block, tiles whose
+rows name different blocks or invalid ones, short indptr ranges and int64
+indptr.  Write cases cover the same layouts with groups that fill a block
 in order, groups that do not (partial, out of order, invalid slots, a
 ragged tail), and the quantizing FP8 write.
 """
+import numpy as np
 import pytest
 import torch
 
 from kvx_amd.abi import DType, Layout, ScaleGranularity as SG
 
-from gpu_helpers import (TORCH_DT, ScaleArg, check_gather, check_write, custom_cache,
-                         make_cache, random_fill)
+from kvx_amd import paged
+
+from gpu_helpers import (TORCH_DT, ScaleArg, check_gather, check_gather_ragged, check_write,
+                         custom_cache, make_cache, random_fill)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -174,3 +179,61 @@ def test_tiles_write_x_packed_entries(entry):
     kw = dict(tokens_per_seq=64) if entry == "prefill" else {}
     check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16,
                 cache_dtype=DType.BF16, entry="abi" if entry == "abi" else "launch", **kw)
+
+
+def _ragged_from_blocks(rng, S, L, bs, nb, spoil_frac, idx_dtype, ptr_dtype):
+    """Per-token block ids of S sequences laid out block by block (so most
+    tiles' rows name one block), a fraction of tokens given another id
+    (another block, -1 or >= num_blocks); per-sequence counts around L."""
+    counts = rng.integers(max(1, L - 2 * bs), L + bs, size=S)
+    ids = []
+    for c in counts:
+        blocks = rng.integers(-1, nb + 1, size=(int(c) + bs - 1) // bs)
+        tok = np.repeat(blocks, bs)[: int(c)]
+        spoil = rng.random(int(c)) < spoil_frac
+        tok[spoil] = rng.integers(-1, nb + 2, size=int(spoil.sum()))
+        ids.append(tok)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(ptr_dtype)
+    return np.concatenate(ids).astype(idx_dtype), indptr
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+@pytest.mark.parametrize("spoil", [0.0, 0.05, 1.0])
+def test_tiles_ragged_gather(case, spoil):
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    seed = 400 + CASES.index(case) * 3 + int(spoil * 20)
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    nb = 40
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    S, L = 6, 4 * bs + 3
+    wide = CASES.index(case) % 2 == 1
+    indices, indptr = _ragged_from_blocks(rng, S, L, bs, nb, spoil,
+                                          np.int64 if wide else np.int32,
+                                          np.int64 if not wide else np.int32)
+    table = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    lens = torch.from_numpy(rng.integers(0, L + 3, size=S).astype(indices.dtype)).to(DEV)
+    lens[0] = L + 3
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("fp8", [DType.F8_E4M3, DType.F8_E5M2])
+@pytest.mark.parametrize("kind", ["tensor", SG.PER_BLOCK_HEAD])
+def test_tiles_ragged_dequant(fp8, kind):
+    """Per-block-head scales follow each row's own block in mixed tiles."""
+    seed = 450 + int(fp8) * 2 + (kind != "tensor")
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    H, D, bs, nb = 8, 128, 16, 40
+    pc, kb, vb = custom_cache(fp8, nb, bs, H, D, "bhdo", "bhpox", None, 8, gen)
+    S, L = 5, 70
+    indices, indptr = _ragged_from_blocks(rng, S, L, bs, nb, 0.1, np.int32, np.int64)
+    table = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    lens = torch.tensor([70, 64, 33, 1, 0], dtype=torch.int32, device=DEV)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=fp8,
+                        io_dtype=DType.BF16, k_scale=_scale(kind, gen, nb, H),
+                        v_scale=_scale(kind, gen, nb, H))
