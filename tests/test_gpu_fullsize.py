@@ -2,7 +2,8 @@
 that do not need the CPU oracle to run at that size:
 
   - write -> gather round trip: every written row comes back bit-exact at its
-    sequence position;
+    sequence position (c2 also on vLLM's x-packed K / token-innermost V pair,
+    with PACKED and RAGGED tables);
   - the whole gather equals an independent implementation (torch advanced
     indexing of the paged cache on int16 views), row by row, and rows past
     seq_len keep the output's prior contents;
@@ -38,8 +39,9 @@ def i16(t: torch.Tensor) -> torch.Tensor:
 
 
 def block_view(cache: torch.Tensor, layout: Layout, pack: int) -> torch.Tensor:
-    """[nb, bs, H, D] view (element order) of a canonical cache tensor."""
-    if layout == Layout.BLOCK_NHD:
+    """[nb, bs, H, D] view (element order) of a canonical cache tensor, or of a
+    4-axis CUSTOM tensor (already that logical view)."""
+    if layout == Layout.BLOCK_NHD or (layout == Layout.BLOCK_CUSTOM and cache.dim() == 4):
         return cache
     if layout == Layout.BLOCK_HND:
         return cache.permute(0, 2, 1, 3)
@@ -106,6 +108,48 @@ def test_c2_full_decode_write_then_gather():
     assert paged.gather_kv(pc, ko, vo, table, lens, L) == Status.OK
     torch.cuda.synchronize()
     # round trip: the new token of every non-padded sequence is at position len - 1
+    seqs = torch.nonzero(ok).flatten()
+    last = lens.long()[seqs] - 1
+    assert torch.equal(i16(ko[seqs, last]), i16(key[seqs]))
+    assert torch.equal(i16(vo[seqs, last]), i16(val[seqs]))
+    check_gather_against_indexing(pc, w, ko, vo, kb, vb)
+
+
+@pytest.mark.parametrize("table_fmt", ["packed", "ragged"])
+def test_c2_full_vllm_layouts_write_then_gather(table_fmt):
+    """c2 at full size on vLLM's paged-attention pair: K HND_PACKED x = 8 and
+    V as CUSTOM [num_blocks, H, D, block_size] (token axis innermost), so the
+    gather runs the LDS tile kernel on both tensors."""
+    w = workloads.c2_llama8b_decode()
+    H, D, bs, nb = w.heads, w.head_dim, w.block_size, w.num_blocks
+    kc = torch.empty(paged.cache_shape(Layout.BLOCK_HND_PACKED, nb, bs, H, D, 8),
+                     dtype=torch.bfloat16, device=DEV).normal_()
+    vstore = torch.empty((nb, H, D, bs), dtype=torch.bfloat16, device=DEV).normal_()
+    pc = paged.PagedCache(kc, paged.custom_view(vstore, "bhdo"), Layout.BLOCK_HND_PACKED,
+                          Layout.BLOCK_CUSTOM, nb, bs, H, D)
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots) == Status.OK
+    torch.cuda.synchronize()
+    ok = slots >= 0
+    blk, off = slots[ok] // bs, slots[ok] % bs
+    kview, vview = block_view(kc, Layout.BLOCK_HND_PACKED, 8), pc.value_cache
+    assert torch.equal(i16(kview[blk, off]), i16(key[ok]))
+    assert torch.equal(i16(vview[blk, off]), i16(val[ok]))
+
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16, 3)
+    kb, vb = ko.clone(), vo.clone()
+    lens = torch.tensor(w.seq_lens, device=DEV)
+    if table_fmt == "packed":
+        table = torch.tensor(w.block_table, device=DEV)
+    else:  # the same table, one block id per gathered token
+        indices, indptr = workloads.ragged_table(w)
+        table = paged.RaggedTable(torch.from_numpy(indices).to(DEV),
+                                  torch.from_numpy(indptr).to(DEV))
+    assert paged.gather_kv(pc, ko, vo, table, lens, L) == Status.OK
+    torch.cuda.synchronize()
     seqs = torch.nonzero(ok).flatten()
     last = lens.long()[seqs] - 1
     assert torch.equal(i16(ko[seqs, last]), i16(key[seqs]))
