@@ -63,6 +63,9 @@ def parse_args():
                         "HND_PACKED x = 8; vllm: K HND_PACKED x = 8 and V "
                         "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
                         "paged-attention pair (PACKED / RAGGED tables only)")
+    p.add_argument("--heads", type=int, default=None,
+                   help="c2 / c5: KV heads per GPU (one tensor-parallel rank's shard: "
+                        "8 / TP); the block table, lengths and slots are unchanged")
     p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
                    help="c4: FP8 format of the cache")
     p.add_argument("--scales", default="tensor",
@@ -111,7 +114,7 @@ class Launch:
 
 
 def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch",
-                 fp8="e4m3", scales="tensor", layout=None):
+                 fp8="e4m3", scales="tensor", layout=None, heads=None):
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -131,6 +134,11 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         w.name = w.name.replace("fp8_e4m3", "fp8_e5m2")
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
+    if heads is not None:
+        if name not in ("c2", "c5") or heads <= 0 or w.heads % heads != 0:
+            raise SystemExit("--heads applies to c2 and c5 and must divide 8")
+        w.heads = heads
+        w.name = f"{w.name}_h{heads}"
     if layout is not None:
         if name not in ("c2", "c5"):
             raise SystemExit("--layout applies to c2 and c5")
@@ -400,7 +408,16 @@ def cpu_baseline(w, seconds: float):
             break
     med = statistics.median(times)
     nbytes = W.write_bytes(sub) + W.gather_bytes(sub)
+    # the same sample on one thread, three runs
+    prev = oracle.set_threads(1)
+    try:
+        one = statistics.median(once()[0] for _ in range(3))
+    finally:
+        oracle.set_threads(prev)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": int(threads),
+            "single_thread": {"value": round(nbytes / one / 1e9, 3), "unit": "GB/s",
+                              "cores": 1, "seconds_per_run": round(one, 4)},
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
             "kind": "port",
             "sample": (f"{w.name} one layer: first {n_s} of {w.seq_count} sequences "
                        f"(gather {sub.gathered_tokens()} tokens, write "
@@ -409,6 +426,41 @@ def cpu_baseline(w, seconds: float):
                        f"median of {len(times)} runs"),
             "tokens_per_s": round((sub.gathered_tokens() + sub.valid_write_tokens()) / med, 1),
             "seconds_per_run": round(med, 4)}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def copy_reference(stream, nbytes: int = 1 << 30, reps: int = 5):
+    """torch's device-to-device copy_ of `nbytes` on `stream` (read plus
+    write bytes per second): a plain copy beside the roofline, for the same
+    box and run."""
+    import torch
+
+    a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(7)
+    b = torch.empty_like(a)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            b.copy_(a)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record(stream)
+            b.copy_(a)
+            e1.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in ev)
+    del a, b
+    torch.cuda.empty_cache()
+    return {"kernel": "torch copy_ device to device", "bytes_per_copy": 2 * nbytes,
+            "GBps": round(2 * nbytes / (ms / 1e3) / 1e9, 1), "reps": reps}
 
 
 def load_traffic(kernel: str, workload: str):
@@ -439,7 +491,8 @@ def main():
 
     dev = torch.device("cuda:0")
     w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table,
-                                       args.write_entry, args.fp8, args.scales, args.layout)
+                                       args.write_entry, args.fp8, args.scales, args.layout,
+                                       args.heads)
     stream = torch.cuda.Stream(device=dev)
     sh = stream.cuda_stream
     torch.cuda.set_stream(stream)  # launches that use torch's current stream
@@ -503,6 +556,7 @@ def main():
                 "traffic": load_traffic(dom, w.name), "kernel": dom,
                 "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]}
 
+    copy_ref = None if args.profile_only else copy_reference(stream)
     cpu = None
     if not args.no_cpu_baseline and not args.profile_only:
         cpu = cpu_baseline(w, args.cpu_seconds)
@@ -523,6 +577,7 @@ def main():
                          for k_, v in step_tokens.items()},
         "kernels": kernels,
         "roofline": roofline,
+        "copy_reference": copy_ref,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }

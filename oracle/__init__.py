@@ -78,6 +78,8 @@ def lib() -> C.CDLL:
         L.oracle_gather_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32,
                                                           i32, i32, i32, i32, i32, i32, i]
         L.oracle_gather_kv_fast.restype = i
+        L.oracle_set_threads.argtypes = [i]
+        L.oracle_set_threads.restype = i
         L.oracle_gather_kv_ragged.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, vp, i,
                                                             vp, i, i32, i32, i32, i32, i32,
                                                             i32, i, i, sp, sp]
@@ -229,6 +231,12 @@ def gather_kv_fast(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out,
                                        int(block_table.dtype == np.int64), seq_count,
                                        max_blocks_per_seq, max_seq_len, heads, head_dim,
                                        block_size, num_blocks, elem_size)
+
+
+def set_threads(n: int) -> int:
+    """Threads of write_kv_fast / gather_kv_fast from now on; returns the
+    previous count."""
+    return lib().oracle_set_threads(int(n))
 
 
 E4M3, E5M2 = 4, 5  # kvx_abi.h dtype codes of the FP8 formats

@@ -477,6 +477,18 @@ static int threads_used(void) {
 #endif
 }
 
+/* Threads of the *_fast functions from now on (n > 0); returns the previous
+   count.  Builds without OpenMP always use 1. */
+int oracle_set_threads(int n) {
+  const int prev = threads_used();
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+  return prev;
+}
+
 int oracle_write_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
                          int v_layout, const int64_t *v_stride, int64_t v_pack,
                          const void *key, const void *value, void *key_cache,

@@ -116,6 +116,10 @@ int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
                           int32_t heads, int32_t head_dim, int32_t block_size,
                           int32_t num_blocks, int elem_size);
 
+/* Threads of the *_fast functions from now on (n > 0); returns the previous
+ * count (always 1 without OpenMP). */
+int oracle_set_threads(int n);
+
 /* Scalar casts (OCP E4M3 and E5M2, bf16, f16), by nearest-value search.
  * FP8 casts saturate to the largest finite value (infinities included). */
 uint8_t oracle_f32_to_e4m3(float v);
