@@ -86,6 +86,21 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+BENCH_SRC = CSRC / "kvx_bench.cpp"
+BENCH_BIN = PKG_DIR / "kvx_bench"
+
+
+def build_bench(verbose: bool = False) -> Path:
+    """Compile the kvx_bench command line (host code over libkvx_amd.so,
+    found next to it at run time)."""
+    cc = hipcc()
+    tmp = BENCH_BIN.with_suffix(".tmp")
+    _run([cc, "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}", str(BENCH_SRC),
+          "-o", str(tmp), f"-L{PKG_DIR}", "-lkvx_amd", "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, BENCH_BIN)
+    return BENCH_BIN
+
+
 TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
 TORCH_OPS_LIB = PKG_DIR / "libkvx_amd_torch.so"
 
@@ -117,4 +132,5 @@ def build_torch_ops(verbose: bool = False) -> Path:
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_bench(verbose="-v" in sys.argv))
     print(build_torch_ops(verbose="-v" in sys.argv))
