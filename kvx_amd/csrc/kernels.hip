@@ -533,30 +533,56 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 // reads and the cache writes are coalesced 16-byte accesses; groups that do
 // not fill a block take the per-token path.
 
-// Wave 0 tests whether tokens [t0, t0 + bs) hold slots b * bs + 0 .. bs - 1
-// in order with b < num_blocks; the answer and b go to *full / *block (LDS),
-// read after the caller's __syncthreads().
-__device__ __forceinline__ void group_fills_block(const WriteArgs &a, int64_t t0, int bs_log2,
-                                                  int32_t *full, int64_t *block) {
+// A run of a group: tokens [t0 + tok, t0 + tok + hi - lo) hold the slots
+// block * bs + lo .. block * bs + hi - 1, in order.
+struct GroupRun {
+  int64_t block;
+  int32_t lo;
+  int32_t hi;
+  int32_t tok;
+  int32_t pad_;
+};
+
+// Runs a group's tokens may form and still be written through LDS: a prefill
+// chunk of bs consecutive positions covers the end of one block and the
+// start of the next.
+constexpr int kMaxRuns = 2;
+
+// Wave 0 splits tokens [t0, t0 + bs) into runs of consecutive offsets of one
+// block and writes them to runs[] (LDS); *nruns = their count, or 0 when a
+// token's slot is < 0 or past the blocks or there are more than kMaxRuns
+// runs (the group is then written token by token).  Read after the caller's
+// __syncthreads().
+__device__ __forceinline__ void group_runs(const WriteArgs &a, int64_t t0, int bs_log2,
+                                           GroupRun *runs, int32_t *nruns) {
   const int tid = (int)threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int bs = 1 << bs_log2;
-  if (tid < kWave) {
-    const int64_t t = t0 + lane;
-    int64_t slot = -1;
-    if (lane < bs && t < a.num_tokens) slot = load_index(a.slots, t, a.slot_is64);
-    const int64_t first =
-        (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32))
-                   << 32) |
-                  (uint32_t)__builtin_amdgcn_readfirstlane((int)slot));
-    const bool in_order = lane >= bs || (t < a.num_tokens && slot == first + lane);
-    const uint64_t all = __ballot(in_order);
-    if (lane == 0) {
-      const bool base = first >= 0 && (first & (bs - 1)) == 0 &&
-                        (first >> bs_log2) < a.num_blocks;
-      *full = (all == ~0ull) && base;
-      *block = first >> bs_log2;
-    }
+  if (tid >= kWave) return;
+  const int lane = tid;
+  const int64_t left = a.num_tokens - t0;
+  const int n = left < (1 << bs_log2) ? (int)left : (1 << bs_log2);
+  int64_t slot = -1;
+  if (lane < n) slot = load_index(a.slots, t0 + lane, a.slot_is64);
+  const int64_t blk = slot >> bs_log2;
+  const int32_t off = (int32_t)(slot & ((1 << bs_log2) - 1));
+  const bool ok = lane >= n || (slot >= 0 && blk < a.num_blocks);
+  const int64_t prev = (int64_t)(((uint64_t)(uint32_t)__shfl_up((int)(slot >> 32), 1) << 32) |
+                                 (uint32_t)__shfl_up((int)slot, 1));
+  const bool start = lane < n && (lane == 0 || off == 0 || slot != prev + 1);
+  const uint64_t bad = __ballot(!ok);
+  const uint64_t starts = __ballot(start);
+  const int count = __popcll(starts);
+  const bool take = bad == 0 && count <= kMaxRuns;
+  if (lane == 0) *nruns = take ? count : 0;
+  if (take && start) {
+    const uint64_t later = lane == kWave - 1 ? 0ull : starts & (~0ull << (lane + 1));
+    const int end = later ? __ffsll((long long)later) - 1 : n;
+    GroupRun r;
+    r.block = blk;
+    r.lo = off;
+    r.hi = off + (end - lane);
+    r.tok = lane;
+    r.pad_ = 0;
+    runs[__popcll(starts & ((1ull << lane) - 1ull))] = r;
   }
 }
 
@@ -592,19 +618,22 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
   }
 }
 
-// Tiled block write: the inverse of gather_tiles_kernel (below) for groups
-// of bs tokens that fill one cache block in order.  A workgroup takes tile
-// `tile` (tw cache bytes of every row) of one tensor (blockIdx.y: K 0, V 1)
-// of one group:
-//   phase 1  reads the tile's columns of the bs source rows, applies the
+// Tiled block write: the inverse of gather_tiles_kernel (below).  A group
+// is `bs` consecutive tokens; when their slots form at most kMaxRuns runs of
+// consecutive offsets of one block each (a whole block in order, or a
+// prefill chunk that starts inside a block), a workgroup takes tile `tile`
+// (tw cache bytes of every row) of one tensor (blockIdx.y: K 0, V 1) and,
+// run by run:
+//   phase 1  reads the tile's columns of the run's source rows, applies the
 //            chunk op (copy, or FP8 quantization with a per-tensor scale)
 //            and stores the cache bytes in LDS rows (pitch tw + 16 bytes);
 //   phase 2  assembles each 16-byte chunk of the block region
 //            [tile * tw * bs, (tile + 1) * tw * bs) from its run pieces and
-//            stores it, so the cache side is written in whole 16-byte lanes.
-// A row-major tensor copies its rows straight through.  A group that does
-// not fill a block is written token by token (K and V rows together), its
-// tokens spread over the waves of all 2 * tiles workgroups of the group.
+//            stores it; chunks holding rows outside the run store those
+//            rows' pieces only.
+// A row-major tensor copies its rows straight through.  Any other group is
+// written token by token (K and V rows together), its tokens spread over
+// the waves of all 2 * tiles workgroups of the group.
 struct WriteTileArgs {
   int32_t tiles;          // tiles per block: cache row bytes / tw
   int32_t tw_log2;        // tile width, cache bytes per row
@@ -635,88 +664,112 @@ __device__ __forceinline__ void get_piece(const char *p, Raw<16> &x, int k) {
 }
 
 // Phase 2 of the tiled write: LDS rows -> region (nbytes = tw * bs cache
-// bytes, 16-byte aligned).  PIECE = min(run bytes, 16).
-template <int PIECE>
+// bytes, 16-byte aligned), rows [lo, hi) only.  PIECE = min(run bytes, 16).
+// A 16-byte chunk whose pieces all belong to rows in [lo, hi) is stored
+// whole; a chunk that mixes rows (runs shorter than 16 bytes, partial
+// blocks) stores the pieces of its rows in range one by one.  FULL: every
+// row is in range (a whole block), and the row tests are compiled out.
+template <int PIECE, bool FULL>
 __device__ __forceinline__ void unstage_tile(char *region, const char *lds, int32_t nbytes,
-                                             int32_t run_log2, int32_t bs_log2, int32_t pitch) {
+                                             int32_t run_log2, int32_t bs_log2, int32_t pitch,
+                                             int32_t lo, int32_t hi) {
   const int32_t bsm = (1 << bs_log2) - 1;
   const int32_t runm = (1 << run_log2) - 1;
   constexpr int32_t kStep = kBlockThreads * 16;
   for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
     Raw<16> x[kTileLoads];
+    bool whole[kTileLoads];
 #pragma unroll
     for (int u = 0; u < kTileLoads; ++u) {
       const int32_t m = m0 + u * kStep;
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[u].w[i] = 0;
+      whole[u] = m < nbytes;
       if (m < nbytes) {
 #pragma unroll
         for (int k = 0; k < 16 / PIECE; ++k) {
           const int32_t mm = m + k * PIECE;
           const int32_t o = (mm >> run_log2) & bsm;
           const int32_t ar = mm >> (run_log2 + bs_log2);
-          get_piece<PIECE>(lds + o * pitch + (ar << run_log2) + (mm & runm), x[u], k);
+          const char *p = lds + o * pitch + (ar << run_log2) + (mm & runm);
+          if (FULL || (o >= lo && o < hi)) {
+            get_piece<PIECE>(p, x[u], k);
+          } else {
+            whole[u] = false;
+          }
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < kTileLoads; ++u) {
       const int32_t m = m0 + u * kStep;
-      if (m < nbytes) st<16, kWriteNtStore>(region + m, x[u]);
+      if (whole[u]) {
+        st<16, kWriteNtStore>(region + m, x[u]);
+      } else if (!FULL && m < nbytes) {
+#pragma unroll
+        for (int k = 0; k < 16 / PIECE; ++k) {
+          const int32_t mm = m + k * PIECE;
+          const int32_t o = (mm >> run_log2) & bsm;
+          if (o >= lo && o < hi) {
+            const int32_t ar = mm >> (run_log2 + bs_log2);
+            st<PIECE, kWriteNtStore>(region + mm,
+                                     ld<PIECE>(lds + o * pitch + (ar << run_log2) + (mm & runm)));
+          }
+        }
+      }
     }
   }
 }
 
-// Op: the tile's chunk op (16-byte cache chunks); TokOp: the per-token
-// path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
-template <class Op, class TokOp>
-__global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
-                                                                    WriteTileArgs wt) {
-  extern __shared__ __attribute__((aligned(16))) char lds[];
-  __shared__ int64_t s_block;
-  __shared__ int32_t s_full;
-  const uint32_t gu = blockIdx.x / (uint32_t)wt.tiles;
-  const int32_t tile = (int32_t)(blockIdx.x - gu * (uint32_t)wt.tiles);
-  const int64_t t0 = (int64_t)gu << wt.bs_log2;
-  const bool v = blockIdx.y != 0;
-  float ks = 1.0f;  // per-tensor scales only
-  float vs = 1.0f;
-  if constexpr (Op::kScaled) {
-    ks = a.ksc.p[0];
-    vs = a.vsc.p[0];
+template <bool FULL>
+__device__ __forceinline__ void unstage_any(char *dst, const char *lds, int32_t region,
+                                            int32_t run_log2, const WriteTileArgs &wt,
+                                            const GroupRun &r) {
+  switch (run_log2) {
+    case 0: unstage_tile<1, FULL>(dst, lds, region, 0, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
+    case 1: unstage_tile<2, FULL>(dst, lds, region, 1, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
+    case 2: unstage_tile<4, FULL>(dst, lds, region, 2, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
+    case 3: unstage_tile<8, FULL>(dst, lds, region, 3, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
+    default:
+      unstage_tile<16, FULL>(dst, lds, region, run_log2, wt.bs_log2, wt.pitch, r.lo, r.hi);
+      break;
   }
-  group_fills_block(a, t0, wt.bs_log2, &s_full, &s_block);
-  __syncthreads();
-  if (!s_full) {
-    write_group_tokens<TokOp>(a, t0, 1 << wt.bs_log2, ks, vs,
-                              ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
-                              2 * wt.tiles * kWavesPerBlock);
-    return;
-  }
-  const char *src = (v ? a.src_v : a.src_k) + t0 * a.row_bytes;
-  char *blk = v ? a.dst_v + s_block * a.gv.s_block : a.dst_k + s_block * a.gk.s_block;
+}
+
+// One run of a group through one tile of one tensor: rows [r.lo, r.hi) of
+// block r.block from the io rows of tokens t0 + r.tok, ...
+template <class Op>
+__device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTileArgs &wt,
+                                               const GroupRun &r, int64_t t0, int32_t tile,
+                                               bool v, float scale, char *lds) {
+  const char *src = (v ? a.src_v : a.src_k) + (t0 + r.tok) * a.row_bytes;
+  char *blk = v ? a.dst_v + r.block * a.gv.s_block : a.dst_k + r.block * a.gk.s_block;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
-  const float scale = v ? vs : ks;
   const int32_t region = (1 << wt.tw_log2) << wt.bs_log2;
-  char *dst = blk + (int64_t)tile * region;
   const int tid = (int)threadIdx.x;
 
   if (run_log2 < 0) {
-    // Row-major block: the block region is the same span of the source rows.
-    const int32_t lo = tile * region;
-    for (int32_t m = lo + tid * Op::kDst; m < lo + region; m += kBlockThreads * Op::kDst) {
-      const uint32_t e = (uint32_t)m >> wt.cache_es_log2;
+    // Row-major block: rows [lo, hi) are one span of the block and of the
+    // source rows.
+    const int32_t row_bytes_c = (int32_t)wt.tiles << wt.tw_log2;
+    const int32_t span_lo = r.lo * row_bytes_c;
+    const int32_t span_hi = r.hi * row_bytes_c;
+    const int32_t lo = tile * region > span_lo ? tile * region : span_lo;
+    const int32_t hi = (tile + 1) * region < span_hi ? (tile + 1) * region : span_hi;
+    for (int32_t m = lo + tid * Op::kDst; m < hi; m += kBlockThreads * Op::kDst) {
+      const uint32_t e = (uint32_t)(m - span_lo) >> wt.cache_es_log2;
       st<Op::kDst, kWriteNtStore>(
-          blk + m, Op::apply(ld<Op::kSrc, kWriteNtLoad>(src + ((int64_t)e << wt.io_es_log2)), scale));
+          blk + m, Op::apply(ld<Op::kSrc, kWriteNtLoad>(src + ((int64_t)e << wt.io_es_log2)),
+                             scale));
     }
     return;
   }
 
-  // Phase 1: chunk c of row r holds the row's io elements e0 + c * G.
+  // Phase 1: chunk c of row lo + q holds the row's io elements e0 + c * G.
   constexpr int kDstLog2 = Op::kDst == 16 ? 4 : Op::kDst == 8 ? 3 : Op::kDst == 4 ? 2
                            : Op::kDst == 2 ? 1 : 0;
   const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
-  const int32_t total = 1 << (wt.bs_log2 + cpr_log2);
+  const int32_t total = (r.hi - r.lo) << cpr_log2;
   const int32_t cm = (1 << cpr_log2) - 1;
   const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
   for (int32_t u0 = tid; u0 < total; u0 += kTileLoads * kBlockThreads) {
@@ -734,17 +787,49 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
     for (int k = 0; k < kTileLoads; ++k) {
       const int32_t u = u0 + k * kBlockThreads;
       if (u < total)
-        st<Op::kDst>(lds + (u >> cpr_log2) * wt.pitch + ((u & cm) << kDstLog2),
+        st<Op::kDst>(lds + (r.lo + (u >> cpr_log2)) * wt.pitch + ((u & cm) << kDstLog2),
                      Op::apply(x[k], scale));
     }
   }
   __syncthreads();
-  switch (run_log2) {
-    case 0: unstage_tile<1>(dst, lds, region, 0, wt.bs_log2, wt.pitch); break;
-    case 1: unstage_tile<2>(dst, lds, region, 1, wt.bs_log2, wt.pitch); break;
-    case 2: unstage_tile<4>(dst, lds, region, 2, wt.bs_log2, wt.pitch); break;
-    case 3: unstage_tile<8>(dst, lds, region, 3, wt.bs_log2, wt.pitch); break;
-    default: unstage_tile<16>(dst, lds, region, run_log2, wt.bs_log2, wt.pitch); break;
+  char *dst = blk + (int64_t)tile * region;
+  if (r.lo == 0 && r.hi == (1 << wt.bs_log2)) {
+    unstage_any<true>(dst, lds, region, run_log2, wt, r);
+  } else {
+    unstage_any<false>(dst, lds, region, run_log2, wt, r);
+  }
+}
+
+// Op: the tile's chunk op (16-byte cache chunks); TokOp: the per-token
+// path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
+template <class Op, class TokOp>
+__global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
+                                                                    WriteTileArgs wt) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ GroupRun s_runs[kMaxRuns];
+  __shared__ int32_t s_nruns;
+  const uint32_t gu = blockIdx.x / (uint32_t)wt.tiles;
+  const int32_t tile = (int32_t)(blockIdx.x - gu * (uint32_t)wt.tiles);
+  const int64_t t0 = (int64_t)gu << wt.bs_log2;
+  const bool v = blockIdx.y != 0;
+  float ks = 1.0f;  // per-tensor scales only
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
+  }
+  group_runs(a, t0, wt.bs_log2, s_runs, &s_nruns);
+  __syncthreads();
+  const int32_t nruns = s_nruns;
+  if (nruns == 0) {
+    write_group_tokens<TokOp>(a, t0, 1 << wt.bs_log2, ks, vs,
+                              ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
+                              2 * wt.tiles * kWavesPerBlock);
+    return;
+  }
+  for (int32_t i = 0; i < nruns; ++i) {
+    if (i > 0) __syncthreads();  // the LDS tile is reused
+    write_tile_run<Op>(a, wt, s_runs[i], t0, tile, v, v ? vs : ks, lds);
   }
 }
 

@@ -237,3 +237,69 @@ def test_tiles_ragged_dequant(fp8, kind):
     check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=fp8,
                         io_dtype=DType.BF16, k_scale=_scale(kind, gen, nb, H),
                         v_scale=_scale(kind, gen, nb, H))
+
+
+def _chunk_slots(gen, nb, bs, S, chunk):
+    """Slots of S prefill chunks of `chunk` consecutive positions, each
+    starting at a random offset inside its first block, every sequence on
+    its own random blocks."""
+    nblk = (chunk + bs - 1) // bs + 1
+    blocks = torch.randperm(nb, generator=gen)[: S * nblk].reshape(S, nblk)
+    out = []
+    for s in range(S):
+        start = int(torch.randint(0, bs, (1,), generator=gen))
+        pos = torch.arange(start, start + chunk)
+        out.append(blocks[s, pos // bs] * bs + pos % bs)
+    return torch.cat(out)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+def test_tiles_write_chunks_inside_blocks(case):
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    gen = torch.Generator().manual_seed(500 + CASES.index(case))
+    nb = 64
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    slots = _chunk_slots(gen, nb, bs, S=5, chunk=2 * bs + bs // 2 + 1)
+    T = slots.numel()
+    key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=dt, cache_dtype=dt)
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[5] >= 4],
+                         ids=[_ids(c) for c in CASES if c[5] >= 4])
+def test_tiles_write_two_runs(case):
+    """Full groups of two runs in different blocks (the tail of one block
+    from offset 3, the head of another from offset 2), then a last, short
+    group of two runs inside one block around a gap (offsets [1, bs/2) and
+    [bs/2 + 1, bs): rows 0 and bs/2 keep their contents)."""
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    gen = torch.Generator().manual_seed(550 + CASES.index(case))
+    nb = 32
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    blocks = [int(b) for b in torch.randperm(nb, generator=gen)[:7]]
+    sl = []
+    for g in range(3):
+        b0, b1 = blocks[2 * g], blocks[2 * g + 1]
+        first = bs - 3
+        sl += [b0 * bs + o for o in range(3, bs)] + [b1 * bs + 2 + i for i in range(bs - first)]
+    h = bs // 2
+    sl += [blocks[6] * bs + o for o in list(range(1, h)) + list(range(h + 1, bs))]
+    slots = torch.tensor(sl)
+    T = slots.numel()
+    key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=dt, cache_dtype=dt)
+
+
+@pytest.mark.parametrize("fp8", [DType.F8_E4M3, DType.F8_E5M2])
+def test_tiles_quantizing_write_chunks(fp8):
+    gen = torch.Generator().manual_seed(580 + int(fp8))
+    H, D, bs, nb = 8, 128, 32, 40
+    pc, kb, vb = custom_cache(fp8, nb, bs, H, D, "bhdo", "bhpox", None, 16, gen)
+    slots = _chunk_slots(gen, nb, bs, S=4, chunk=bs)
+    T = slots.numel()
+    key = (torch.randn((T, H, D), generator=gen) * 3).to(torch.bfloat16).to(DEV)
+    val = (torch.randn((T, H, D), generator=gen) * 0.3).to(torch.bfloat16).to(DEV)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16, cache_dtype=fp8,
+                k_scale=0.009, v_scale=0.0013)
