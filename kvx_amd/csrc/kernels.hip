@@ -1,12 +1,14 @@
 // Paged KV write (scatter) and gather kernels for gfx950 (CDNA4, wave64).
 //
-// Data movement only, plus an optional FP8 E4M3 cast.  The unit of work is a
-// *chunk*: G consecutive elements of one contiguous cache piece (a head row
-// for NHD/HND, an x-element pack for HND_PACKED), moved with one 1..16-byte
-// load and one store per lane.  The host picks the widest chunk that every
-// pointer and stride allows, so NHD/HND bf16 rows move as 16-byte
+// Data movement only, plus optional FP8 (E4M3 / E5M2) casts.  The unit of
+// work is a *chunk*: G consecutive elements of one contiguous cache piece (a
+// head row for NHD/HND, an x-element pack for HND_PACKED), moved with one
+// 1..16-byte load and one store per lane.  The host picks the widest chunk
+// that every pointer and stride allows, so NHD/HND bf16 rows move as 16-byte
 // global_load_dwordx4 / global_store_dwordx4 and a wave covers 1 KiB of a row
-// per instruction.
+// per instruction.  Blocks stored in another dense order (x-packed, HND,
+// token axis innermost) are transposed through LDS by the tile kernels, so
+// that both HBM sides stay 16-byte coalesced whatever the layout.
 //
 // Semantics follow the reference kernels:
 //   write  kernels/kvx_paged_kv.cu:93-124 (slot < 0 and block >= num_blocks
@@ -836,9 +838,12 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
 // ---------------------------------------------------------------------------
 // Gather.
 //
-// One workgroup per (sequence, logical block).  When the cache rows of a
-// block are contiguous (canonical NHD) gather_flat_kernel streams the block
-// as one flat copy; other layouts use gather_rows_kernel.
+// PACKED tables: when the cache rows of a block are contiguous (canonical
+// NHD) gather_flat_kernel streams row ranges of the block as flat copies;
+// dense blocks in other orders (x-packed, HND, token-innermost) take
+// gather_tiles_kernel's LDS transpose; any other strides take
+// gather_rows_kernel.  RAGGED and KV_OFFSETS tables have their own kernels
+// (gather_indexed_flat_kernel, gather_indexed_kernel) besides the tile one.
 
 struct GatherArgs {
   const char *src_k;
@@ -2104,7 +2109,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
   WriteLaunch wl;
   wl.grid = (int)(want < 2048 ? want : 2048);
-  // The block kernel applies per-tensor scales only.
+  // The tiled write applies per-tensor scales only.
   const bool indexed = p.k_scale.indexed || p.v_scale.indexed;
   wl.tiles = !indexed && plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   hipStream_t s = as_stream(stream);

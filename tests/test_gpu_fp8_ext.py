@@ -126,7 +126,7 @@ def test_indexed_scale_write_then_gather(kind, fp8, io):
 
 @pytest.mark.parametrize("fp8", FP8)
 def test_indexed_scale_prefill_entry(fp8):
-    """Full-block prefill groups: the block kernel takes per-tensor scales
+    """Full-block prefill groups: the tiled write takes per-tensor scales
     only, so indexed scales run on the per-token kernel."""
     gen = torch.Generator().manual_seed(40 + int(fp8))
     H, D, bs, nb = 8, 128, 16, 32
