@@ -2012,12 +2012,19 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
 // bs tokens, power-of-two bs (<= one wave) and cache row bytes, dense
 // blocks of which at least one is not row-major, 16-byte aligned block
 // addresses and io rows aligned to the tile op's source chunk.
-// KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile; on MI355X (c3
-// shapes) 16 KiB measured best against 8 and 32 KiB, and 0-5% faster than
+// KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile of a copying
+// write; KVX_QUANT_TILE_BYTES the same for the FP8 quantizing write (whose
+// io rows are 2-4x its cache bytes).  On MI355X (c3 shapes, inputs not
+// cache-resident) 8 KiB measured 1.5-3% faster than 16 KiB for copies, and
+// 4-5% faster than 32 or 64 KiB; the quantizing write is 4-8% faster with
+// 16 KiB; 4 KiB is 25-30% slower for both.  Tiles are 0-5% faster than
 // staging whole blocks of K and V in one workgroup (x-packed / HND), 5x for
 // the token-innermost value cache.
 #ifndef KVX_WRITE_TILE_BYTES
-#define KVX_WRITE_TILE_BYTES 16384
+#define KVX_WRITE_TILE_BYTES 8192
+#endif
+#ifndef KVX_QUANT_TILE_BYTES
+#define KVX_QUANT_TILE_BYTES 16384
 #endif
 bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int64_t *grid,
                       uint32_t *lds_bytes) {
@@ -2049,8 +2056,10 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
       return false;
   }
   if (!transposed) return false;
+  const int64_t tile_bytes =
+      p.conv == kConvQuant ? KVX_QUANT_TILE_BYTES : KVX_WRITE_TILE_BYTES;
   int64_t tw = row_cache;
-  while (tw * bs > KVX_WRITE_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  while (tw * bs > tile_bytes && tw / 2 >= min_tw) tw /= 2;
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
   wt->tiles = (int32_t)(row_cache / tw);
