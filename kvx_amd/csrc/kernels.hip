@@ -89,6 +89,7 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #define KVX_WRITE_NT_STORE 1
 #endif
 constexpr bool kWriteNtLoad = KVX_WRITE_NT_LOAD != 0;
+
 constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
 constexpr int kIndexedUnroll = KVX_INDEXED_UNROLL;
@@ -369,6 +370,23 @@ __device__ __forceinline__ int64_t load_idx(const void *base, int64_t i) {
 
 // Scale of (block b, head h): the workgroup's per-tensor value, or the
 // indexed entry.
+// Scale of row element e (of a row of heads of head_dim elements) in block
+// b.  The head's division is done only for indexed scales: an integer
+// division by a run-time value is a long instruction sequence on the GPU.
+__device__ __forceinline__ float scale_at(const ScaleRef &r, float uniform, int64_t b,
+                                          uint32_t e, uint32_t head_dim) {
+  if (!r.indexed) return uniform;
+  return r.p[b * r.s_block + (int64_t)(e / head_dim) * r.s_head];
+}
+
+// The same for element e of a run of whole rows of row_elems elements.
+__device__ __forceinline__ float scale_in_rows(const ScaleRef &r, float uniform, int64_t b,
+                                               uint32_t e, uint32_t row_elems,
+                                               uint32_t head_dim) {
+  if (!r.indexed) return uniform;
+  return r.p[b * r.s_block + (int64_t)((e % row_elems) / head_dim) * r.s_head];
+}
+
 __device__ __forceinline__ float scale_of(const ScaleRef &r, float uniform, int64_t b,
                                           uint32_t h) {
   return r.indexed ? r.p[b * r.s_block + (int64_t)h * r.s_head] : uniform;
@@ -591,7 +609,7 @@ __device__ __forceinline__ void group_runs(const WriteArgs &a, int64_t t0, int b
 // Per-token write of the tokens [t0, t0 + bs) of a group that does not fill
 // a block, shared by `nwaves` waves: this workgroup's wave w is wave
 // wave0 + w of them and takes tokens wave0 + w, wave0 + w + nwaves, ...
-template <class Op>
+template <class Op, bool IDX>
 __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t0, int bs,
                                                    float ks, float vs, int wave0, int nwaves) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
@@ -612,10 +630,16 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
       const Raw<Op::kSrc> xk = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
       const Raw<Op::kSrc> xv = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
+      float sk = ks;
+      float sv = vs;
+      if constexpr (Op::kScaled && IDX) {
+        sk = scale_at(a.ksc, ks, b, e, (uint32_t)a.head_dim);
+        sv = scale_at(a.vsc, vs, b, e, (uint32_t)a.head_dim);
+      }
       st<Op::kDst, kWriteNtStore>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim),
-                                  Op::apply(xk, ks));
+                                  Op::apply(xk, sk));
       st<Op::kDst, kWriteNtStore>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim),
-                                  Op::apply(xv, vs));
+                                  Op::apply(xv, sv));
     }
   }
 }
@@ -627,7 +651,8 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
 // (tw cache bytes of every row) of one tensor (blockIdx.y: K 0, V 1) and,
 // run by run:
 //   phase 1  reads the tile's columns of the run's source rows, applies the
-//            chunk op (copy, or FP8 quantization with a per-tensor scale)
+//            chunk op (copy, or FP8 quantization with the scale of the
+//            run's block and the chunk's head)
 //            and stores the cache bytes in LDS rows (pitch tw + 16 bytes);
 //   phase 2  assembles each 16-byte chunk of the block region
 //            [tile * tw * bs, (tile + 1) * tw * bs) from its run pieces and
@@ -740,10 +765,12 @@ __device__ __forceinline__ void unstage_any(char *dst, const char *lds, int32_t 
 
 // One run of a group through one tile of one tensor: rows [r.lo, r.hi) of
 // block r.block from the io rows of tokens t0 + r.tok, ...
-template <class Op>
+template <class Op, bool IDX>
 __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTileArgs &wt,
                                                const GroupRun &r, int64_t t0, int32_t tile,
-                                               bool v, float scale, char *lds) {
+                                               bool v, float uniform, char *lds) {
+  const ScaleRef &sr = v ? a.vsc : a.ksc;
+  const uint32_t hd = (uint32_t)a.head_dim;
   const char *src = (v ? a.src_v : a.src_k) + (t0 + r.tok) * a.row_bytes;
   char *blk = v ? a.dst_v + r.block * a.gv.s_block : a.dst_k + r.block * a.gk.s_block;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
@@ -758,11 +785,14 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
     const int32_t span_hi = r.hi * row_bytes_c;
     const int32_t lo = tile * region > span_lo ? tile * region : span_lo;
     const int32_t hi = (tile + 1) * region < span_hi ? (tile + 1) * region : span_hi;
+    const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
     for (int32_t m = lo + tid * Op::kDst; m < hi; m += kBlockThreads * Op::kDst) {
       const uint32_t e = (uint32_t)(m - span_lo) >> wt.cache_es_log2;
+      float sc = uniform;
+      if constexpr (Op::kScaled && IDX) sc = scale_in_rows(sr, uniform, r.block, e, re, hd);
       st<Op::kDst, kWriteNtStore>(
           blk + m, Op::apply(ld<Op::kSrc, kWriteNtLoad>(src + ((int64_t)e << wt.io_es_log2)),
-                             scale));
+                             sc));
     }
     return;
   }
@@ -788,9 +818,15 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
       const int32_t u = u0 + k * kBlockThreads;
-      if (u < total)
+      if (u < total) {
+        float sc = uniform;
+        if constexpr (Op::kScaled && IDX) {
+          const uint32_t e = e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
+          sc = scale_at(sr, uniform, r.block, e, hd);
+        }
         st<Op::kDst>(lds + (r.lo + (u >> cpr_log2)) * wt.pitch + ((u & cm) << kDstLog2),
-                     Op::apply(x[k], scale));
+                     Op::apply(x[k], sc));
+      }
     }
   }
   __syncthreads();
@@ -804,7 +840,9 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
 
 // Op: the tile's chunk op (16-byte cache chunks); TokOp: the per-token
 // path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
-template <class Op, class TokOp>
+// IDX: indexed (per-head / per-block) scales are looked up per chunk; the
+// per-tensor instances carry no lookup code (registers decide occupancy).
+template <class Op, class TokOp, bool IDX>
 __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
                                                                     WriteTileArgs wt) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -814,7 +852,7 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
   const int32_t tile = (int32_t)(blockIdx.x - gu * (uint32_t)wt.tiles);
   const int64_t t0 = (int64_t)gu << wt.bs_log2;
   const bool v = blockIdx.y != 0;
-  float ks = 1.0f;  // per-tensor scales only
+  float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
     ks = a.ksc.p[0];
@@ -824,14 +862,14 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
   __syncthreads();
   const int32_t nruns = s_nruns;
   if (nruns == 0) {
-    write_group_tokens<TokOp>(a, t0, 1 << wt.bs_log2, ks, vs,
+    write_group_tokens<TokOp, IDX>(a, t0, 1 << wt.bs_log2, ks, vs,
                               ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
                               2 * wt.tiles * kWavesPerBlock);
     return;
   }
   for (int32_t i = 0; i < nruns; ++i) {
     if (i > 0) __syncthreads();  // the LDS tile is reused
-    write_tile_run<Op>(a, wt, s_runs[i], t0, tile, v, v ? vs : ks, lds);
+    write_tile_run<Op, IDX>(a, wt, s_runs[i], t0, tile, v, v ? vs : ks, lds);
   }
 }
 
@@ -1323,7 +1361,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
         }
       }
       float sc = uniform;
-      if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, rb, (e % re) / hd);
+      if constexpr (Op::kScaled) sc = scale_in_rows(tt.sc, uniform, rb, e, re, hd);
       st<Op::kDst, kGatherNtStore>(out + ((int64_t)e << a.io_es_log2),
                                    Op::apply(ld<Op::kSrc, kGatherNtLoad>(b + m), sc));
     }
@@ -1380,7 +1418,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
         }
         const uint32_t e = e0 + ((uint32_t)((u & cm) << kSrcLog2) >> a.cache_es_log2);
         float sc = uniform;
-        if constexpr (Op::kScaled) sc = scale_of(tt.sc, uniform, rb, e / hd);
+        if constexpr (Op::kScaled) sc = scale_at(tt.sc, uniform, rb, e, hd);
         st<Op::kDst, kGatherNtStore>(out + (int64_t)r * a.out_row_bytes +
                                          ((int64_t)e << a.io_es_log2),
                                      Op::apply(x[k], sc));
@@ -1757,9 +1795,17 @@ struct TileOpOf<QuantOp<G, IO, F8>> {
 template <class Op>
 void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   if (w.tiles) {
-    hipLaunchKernelGGL((write_tiles_kernel<typename TileOpOf<Op>::type, Op>),
-                       dim3((uint32_t)w.tile_grid, 2), dim3(kBlockThreads), w.tile_lds, s, a,
-                       w.wt);
+    using TOp = typename TileOpOf<Op>::type;
+    const dim3 g((uint32_t)w.tile_grid, 2);
+    if constexpr (Op::kScaled) {
+      if (a.ksc.indexed || a.vsc.indexed) {
+        hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true>), g, dim3(kBlockThreads),
+                           w.tile_lds, s, a, w.wt);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false>), g, dim3(kBlockThreads), w.tile_lds,
+                       s, a, w.wt);
   } else {
     hipLaunchKernelGGL(write_kernel<Op>, dim3(w.grid), dim3(kBlockThreads), 0, s, a);
   }
@@ -2008,10 +2054,11 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   return *grid <= 0x7FFFFFFF;
 }
 
-// Tiled block write plan (write_tiles_kernel): per-tensor scales, at least
-// bs tokens, power-of-two bs (<= one wave) and cache row bytes, dense
-// blocks of which at least one is not row-major, 16-byte aligned block
-// addresses and io rows aligned to the tile op's source chunk.
+// Tiled block write plan (write_tiles_kernel): at least bs tokens,
+// power-of-two bs (<= one wave) and cache row bytes, dense blocks of which
+// at least one is not row-major, 16-byte aligned block addresses, io rows
+// aligned to the tile op's source chunk, and (quantizing) heads a whole
+// number of 8-element chunks, so that every chunk has one scale.
 // KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile of a copying
 // write; KVX_QUANT_TILE_BYTES the same for the FP8 quantizing write (whose
 // io rows are 2-4x its cache bytes).  On MI355X (c3 shapes, inputs not
@@ -2036,6 +2083,7 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   if (bs_log2 < 0 || bs > kWave || p.num_tokens < bs) return false;
   if (log2_exact(row_cache) < 0 || row_cache < 16) return false;
   const int src_chunk = p.conv == kConvQuant ? 8 * is : 16;
+  if (p.conv == kConvQuant && D % 8 != 0) return false;
   const Geom *g[2] = {&p.gk, &p.gv};
   const void *src[2] = {p.src_k, p.src_v};
   const void *dst[2] = {p.dst_k, p.dst_v};
@@ -2118,9 +2166,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
   WriteLaunch wl;
   wl.grid = (int)(want < 2048 ? want : 2048);
-  // The tiled write applies per-tensor scales only.
-  const bool indexed = p.k_scale.indexed || p.v_scale.indexed;
-  wl.tiles = !indexed && plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
+  wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   hipStream_t s = as_stream(stream);
 
   if (p.conv == kConvCopy) {

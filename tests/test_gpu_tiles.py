@@ -303,3 +303,38 @@ def test_tiles_quantizing_write_chunks(fp8):
     val = (torch.randn((T, H, D), generator=gen) * 0.3).to(torch.bfloat16).to(DEV)
     check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16, cache_dtype=fp8,
                 k_scale=0.009, v_scale=0.0013)
+
+
+@pytest.mark.parametrize("kind", [SG.PER_HEAD, SG.PER_BLOCK, SG.PER_BLOCK_HEAD])
+@pytest.mark.parametrize("layouts", [("bhdo", None, "bhpox", 16), ("bhpox", 16, "bohd", None)])
+def test_tiles_quantizing_write_indexed_scales(kind, layouts):
+    """Indexed scales through the tiled write: whole blocks, chunks that
+    start inside blocks (the scale follows each run's block) and spoiled
+    groups (per-token path)."""
+    ko_, kx, vo_, vx = layouts
+    gen = torch.Generator().manual_seed(600 + int(kind) * 3 + (kx is None))
+    H, D, bs, nb = 8, 128, 16, 64
+    pc, kb, vb = custom_cache(DType.F8_E4M3, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    # whole blocks in [0, nb / 2), two groups spoiled (a -1 slot, a swap);
+    # chunks starting inside blocks of [nb / 2, nb): no slot is written twice
+    blocks = torch.randperm(nb // 2, generator=gen)[:6]
+    full = (blocks[:, None] * bs + torch.arange(bs)).reshape(-1)
+    full[3] = -1
+    full[2 * bs + 5], full[2 * bs + 6] = full[2 * bs + 6].clone(), full[2 * bs + 5].clone()
+    chunks = _chunk_slots(gen, nb // 2, bs, S=3, chunk=2 * bs + 5) + (nb // 2) * bs
+    slots = torch.cat([full, chunks])
+    T = slots.numel()
+    key = (torch.randn((T, H, D), generator=gen) * 4).to(torch.bfloat16).to(DEV)
+    val = (torch.randn((T, H, D), generator=gen) * 0.5).to(torch.bfloat16).to(DEV)
+
+    def arg():
+        if kind == SG.PER_HEAD:
+            return ScaleArg(kind, torch.empty(H).uniform_(0.002, 0.05, generator=gen).numpy(),
+                            stride=(3,))
+        if kind == SG.PER_BLOCK:
+            return ScaleArg(kind, torch.empty(nb).uniform_(0.002, 0.05, generator=gen).numpy())
+        return ScaleArg(kind, torch.empty(nb, H).uniform_(0.002, 0.05, generator=gen).numpy(),
+                        stride=(1, nb))
+
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16,
+                cache_dtype=DType.F8_E4M3, k_scale=arg(), v_scale=arg())
