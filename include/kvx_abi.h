@@ -27,6 +27,16 @@ extern "C" {
 #define KVX_ABI_VERSION_MAJOR 1
 #define KVX_ABI_VERSION_MINOR 1
 
+/* Enumerations are 32-bit.  C++ callers (and this library) see a fixed
+ * underlying type, so that a field holding a value outside the enumerators
+ * (a caller error the validators report) is an ordinary value to read, as it
+ * is in C; the layout is unchanged. */
+#ifdef __cplusplus
+#define KVX_ENUM_BASE : int32_t
+#else
+#define KVX_ENUM_BASE
+#endif
+
 /* Export decoration: empty on ELF platforms, as in reference kvx_abi.h:14-24. */
 #if defined(_WIN32)
 #if defined(KVX_BUILD_DLL)
@@ -41,7 +51,7 @@ extern "C" {
 #endif
 
 /* Status codes (reference kvx_abi.h:26-33). */
-typedef enum kvx_status {
+typedef enum kvx_status KVX_ENUM_BASE {
   KVX_STATUS_OK = 0,
   KVX_STATUS_INVALID_ARGUMENT = 1,
   KVX_STATUS_UNSUPPORTED = 2,
@@ -59,7 +69,7 @@ typedef struct kvx_version {
 } kvx_version_t;
 
 /* Element types (reference kvx_abi.h:42-54). */
-typedef enum kvx_dtype {
+typedef enum kvx_dtype KVX_ENUM_BASE {
   KVX_DTYPE_INVALID = 0,
   KVX_DTYPE_F16 = 1,
   KVX_DTYPE_BF16 = 2,
@@ -74,7 +84,7 @@ typedef enum kvx_dtype {
 } kvx_dtype_t;
 
 /* Where a buffer lives (reference kvx_abi.h:56-61). */
-typedef enum kvx_memory_type {
+typedef enum kvx_memory_type KVX_ENUM_BASE {
   KVX_MEMORY_UNKNOWN = 0,
   KVX_MEMORY_HOST = 1,
   KVX_MEMORY_DEVICE = 2,
@@ -87,7 +97,7 @@ typedef enum kvx_memory_type {
  *   HND        [num_blocks, heads, block_size, head_dim]
  *   HND_PACKED [num_blocks, heads, head_dim / x, block_size, x], x = shape[4]
  */
-typedef enum kvx_layout {
+typedef enum kvx_layout KVX_ENUM_BASE {
   KVX_LAYOUT_INVALID = 0,
   KVX_LAYOUT_BLOCK_NHD = 1,
   KVX_LAYOUT_BLOCK_HND = 2,
@@ -131,7 +141,7 @@ typedef struct kvx_cache_desc {
 } kvx_cache_desc_t;
 
 /* reference kvx_abi.h:103-108 */
-typedef enum kvx_block_table_format {
+typedef enum kvx_block_table_format KVX_ENUM_BASE {
   KVX_BLOCK_TABLE_INVALID = 0,
   KVX_BLOCK_TABLE_PACKED = 1,
   KVX_BLOCK_TABLE_RAGGED = 2,
@@ -139,7 +149,7 @@ typedef enum kvx_block_table_format {
 } kvx_block_table_format_t;
 
 /* reference kvx_abi.h:110-113 */
-typedef enum kvx_block_table_flags {
+typedef enum kvx_block_table_flags KVX_ENUM_BASE {
   KVX_BLOCK_TABLE_FLAG_NONE = 0,
   KVX_BLOCK_TABLE_FLAG_KVCACHEINDEX = 1 << 0
 } kvx_block_table_flags_t;
@@ -188,7 +198,7 @@ typedef struct kvx_kv_io_desc {
 } kvx_kv_io_desc_t;
 
 /* reference kvx_abi.h:154-160 */
-typedef enum kvx_scale_granularity {
+typedef enum kvx_scale_granularity KVX_ENUM_BASE {
   KVX_SCALE_NONE = 0,
   KVX_SCALE_PER_TENSOR = 1,
   KVX_SCALE_PER_BLOCK = 2,
