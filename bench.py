@@ -25,6 +25,10 @@ summary (profiles/) when present.
 
 cpu_baseline: the CPU oracle's row-memcpy write + gather (oracle/, OpenMP)
 timed on this host's cores over a bounded sample of the same workload.
+
+Outside the timed region: copy_reference (torch's device copy of 1 GiB on
+the same stream) and write_graph (the workload's writes captured in one HIP
+graph and replayed: device time per write without per-call launch cost).
 """
 from __future__ import annotations
 
@@ -463,6 +467,42 @@ def copy_reference(stream, nbytes: int = 1 << 30, reps: int = 5):
             "GBps": round(2 * nbytes / (ms / 1e3) / 1e9, 1), "reps": reps}
 
 
+def write_graph(steps, stream, reps: int = 10, min_launches: int = 32):
+    """The workload's cache writes replayed from a HIP graph: every write
+    launch of every step, repeated to at least `min_launches` launches, is
+    captured once on the bench stream, so the per-call host cost of the
+    launch path (descriptor checks, planning, the launch itself) is paid at
+    capture only, as under vLLM's graph-mode decode.  `reps` replays are
+    queued back to back between two events, so the device never waits for
+    the host; reports the mean device time per write."""
+    import torch
+
+    writes = [l for s in steps for l in s if l.kind == "write"]
+    if not writes:
+        return None
+    rounds = -(-min_launches // len(writes))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(rounds):
+            for l in writes:
+                l(stream.cuda_stream)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    n = reps * rounds * len(writes)
+    ms = e0.elapsed_time(e1) / n
+    del g
+    return {"launches_per_graph": rounds * len(writes), "replays": reps,
+            "us_per_write": round(ms * 1e3, 3),
+            "GBps": round(writes[0].nbytes / (ms / 1e3) / 1e9, 1)}
+
+
 def load_traffic(kernel: str, workload: str):
     """HBM bytes per launch from the committed rocprofv3 counter summary."""
     p = REPO / "profiles" / f"traffic_{kernel}_{workload}.json"
@@ -557,6 +597,7 @@ def main():
                 "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]}
 
     copy_ref = None if args.profile_only else copy_reference(stream)
+    graph = None if args.profile_only else write_graph(steps, stream)
     cpu = None
     if not args.no_cpu_baseline and not args.profile_only:
         cpu = cpu_baseline(w, args.cpu_seconds)
@@ -578,6 +619,7 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
         "copy_reference": copy_ref,
+        "write_graph": graph,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }
