@@ -77,18 +77,23 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #ifndef KVX_RAGGED_DEQUANT_CHUNK
 #define KVX_RAGGED_DEQUANT_CHUNK 16
 #endif
-// Non-temporal io-row loads of the tiled block write, and non-temporal cache
-// stores of every write kernel.  On MI355X (c3 shapes) non-temporal stores
-// make the tiled write 2-9% faster and the per-token prefill write 14%
-// faster (decode writes are unchanged); non-temporal loads make the tiled
-// write 10-20% slower.
+// Non-temporal io-row loads of the tiled block write and of the per-token
+// write, and non-temporal cache stores of every write kernel.  On MI355X
+// (c3 shapes) non-temporal stores make the tiled write 2-9% faster and the
+// per-token prefill write 14% faster (decode writes are unchanged);
+// non-temporal loads make the tiled write 10-20% slower and the per-token
+// prefill write 2-5% faster.
 #ifndef KVX_WRITE_NT_LOAD
 #define KVX_WRITE_NT_LOAD 0
+#endif
+#ifndef KVX_TOKEN_WRITE_NT_LOAD
+#define KVX_TOKEN_WRITE_NT_LOAD 1
 #endif
 #ifndef KVX_WRITE_NT_STORE
 #define KVX_WRITE_NT_STORE 1
 #endif
 constexpr bool kWriteNtLoad = KVX_WRITE_NT_LOAD != 0;
+constexpr bool kTokenWriteNtLoad = KVX_TOKEN_WRITE_NT_LOAD != 0;
 
 constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
@@ -499,8 +504,8 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
       for (int k = 0; k < kMaxChunksPerLane; ++k) {
         const int c = l + k * lpt;
         if (c < a.nchunks) {
-          xk[k] = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
-          xv[k] = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
+          xk[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sk + (int64_t)c * Op::kSrc);
+          xv[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sv + (int64_t)c * Op::kSrc);
         }
       }
     }
@@ -532,8 +537,8 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
     for (int c = l + kMaxChunksPerLane * lpt; c < a.nchunks; c += lpt) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
       const uint32_t h = e / (uint32_t)a.head_dim;
-      const Raw<Op::kSrc> yk = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
-      const Raw<Op::kSrc> yv = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
+      const Raw<Op::kSrc> yk = ld<Op::kSrc, kTokenWriteNtLoad>(sk + (int64_t)c * Op::kSrc);
+      const Raw<Op::kSrc> yv = ld<Op::kSrc, kTokenWriteNtLoad>(sv + (int64_t)c * Op::kSrc);
       st<Op::kDst, kWriteNtStore>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim),
                                   Op::apply(yk, scale_of(a.ksc, ks, b, h)));
       st<Op::kDst, kWriteNtStore>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim),
@@ -838,6 +843,104 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
   }
 }
 
+// Whole-block fast path of write_tiles_kernel, for the usual prefill group:
+// its bs slots are block * bs + 0 .. bs - 1 in token order.  The group's
+// source rows do not depend on the slots, so every thread issues the loads
+// of its (at most kTileLoads) chunks of the tile first; each wave then
+// loads the bs slots itself (one per lane) and tests them with a ballot, so
+// the slot latency overlaps the data loads and no barrier is needed to
+// share the test.  Every wave reaches the same answer from the same slots.
+// Returns false, having stored nothing, when the group is not such a block
+// (or is the short last group, or its tile needs more than one pass): the
+// caller then runs the general run analysis.  The speculative loads stay
+// within the io rows of tokens [t0, t0 + bs) < num_tokens.
+template <class Op, bool IDX>
+__device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const WriteTileArgs &wt,
+                                                 int64_t t0, int32_t tile, bool v,
+                                                 float uniform, char *lds) {
+  constexpr int kDstLog2 = Op::kDst == 16 ? 4 : Op::kDst == 8 ? 3 : Op::kDst == 4 ? 2
+                           : Op::kDst == 2 ? 1 : 0;
+  const int32_t bs = 1 << wt.bs_log2;
+  const int32_t region = (1 << wt.tw_log2) << wt.bs_log2;  // cache bytes of the tile
+  const int32_t total = region >> kDstLog2;                // chunks of the tile
+  if (t0 + bs > a.num_tokens || total > kTileLoads * kBlockThreads) return false;
+  const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
+  const char *src = (v ? a.src_v : a.src_k) + t0 * a.row_bytes;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  int64_t slot = -1;
+  if (lane < bs) slot = load_index(a.slots, t0 + lane, a.slot_is64);
+
+  // Source of chunk u.  Row-major cache: the tile is bytes
+  // [tile * region, (tile + 1) * region) of the block, which hold io
+  // elements e = byte >> cache_es_log2 counted from row t0.  Otherwise:
+  // chunk u is chunk (u & cm) of the tile's columns of row u >> cpr_log2.
+  const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
+  const int32_t cm = (1 << cpr_log2) - 1;
+  const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
+  auto elem = [&](int32_t u) -> uint32_t {  // io element of chunk u within its row run
+    return run_log2 < 0
+               ? (uint32_t)((tile * region + (u << kDstLog2)) >> wt.cache_es_log2)
+               : e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
+  };
+  auto src_of = [&](int32_t u) -> const char * {
+    return run_log2 < 0 ? src + ((int64_t)elem(u) << wt.io_es_log2)
+                        : src + (int64_t)(u >> cpr_log2) * a.row_bytes +
+                              ((int64_t)elem(u) << wt.io_es_log2);
+  };
+  Raw<Op::kSrc> x[kTileLoads];
+#pragma unroll
+  for (int k = 0; k < kTileLoads; ++k) {
+    const int32_t u = tid + k * kBlockThreads;
+    if (u < total) x[k] = ld<Op::kSrc, kWriteNtLoad>(src_of(u));
+  }
+
+  const int64_t first =
+      (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32)) << 32) |
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)slot));
+  const bool in_order = lane >= bs || slot == first + lane;
+  const int64_t block = first >> wt.bs_log2;
+  if (__ballot(!in_order) != 0 || first < 0 || (first & (bs - 1)) != 0 ||
+      block >= a.num_blocks)
+    return false;
+
+  const ScaleRef &sr = v ? a.vsc : a.ksc;
+  const uint32_t hd = (uint32_t)a.head_dim;
+  char *blk = v ? a.dst_v + block * a.gv.s_block : a.dst_k + block * a.gk.s_block;
+  if (run_log2 < 0) {
+    const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = tid + k * kBlockThreads;
+      if (u < total) {
+        float sc = uniform;
+        if constexpr (Op::kScaled && IDX) sc = scale_in_rows(sr, uniform, block, elem(u), re, hd);
+        st<Op::kDst, kWriteNtStore>(blk + tile * region + (u << kDstLog2), Op::apply(x[k], sc));
+      }
+    }
+    return true;
+  }
+#pragma unroll
+  for (int k = 0; k < kTileLoads; ++k) {
+    const int32_t u = tid + k * kBlockThreads;
+    if (u < total) {
+      float sc = uniform;
+      if constexpr (Op::kScaled && IDX) sc = scale_at(sr, uniform, block, elem(u), hd);
+      st<Op::kDst>(lds + (u >> cpr_log2) * wt.pitch + ((u & cm) << kDstLog2),
+                   Op::apply(x[k], sc));
+    }
+  }
+  __syncthreads();
+  GroupRun r;
+  r.block = block;
+  r.lo = 0;
+  r.hi = bs;
+  r.tok = 0;
+  r.pad_ = 0;
+  unstage_any<true>(blk + (int64_t)tile * region, lds, region, run_log2, wt, r);
+  return true;
+}
+
 // Op: the tile's chunk op (16-byte cache chunks); TokOp: the per-token
 // path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
 // IDX: indexed (per-head / per-block) scales are looked up per chunk; the
@@ -858,6 +961,7 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
+  if (write_tile_block<Op, IDX>(a, wt, t0, tile, v, v ? vs : ks, lds)) return;
   group_runs(a, t0, wt.bs_log2, s_runs, &s_nruns);
   __syncthreads();
   const int32_t nruns = s_nruns;
@@ -2165,7 +2269,10 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   a.num_groups = (p.num_tokens + tpw - 1) / tpw;
   const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
   WriteLaunch wl;
-  wl.grid = (int)(want < 2048 ? want : 2048);
+  // One wave per token group up to 65536 workgroups, then a grid-stride
+  // loop: on MI355X a 2048-workgroup cap made c3-sized NHD prefill writes
+  // 2-4% slower (8% with blocks in ascending order).
+  wl.grid = (int)(want < 65536 ? want : 65536);
   wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   hipStream_t s = as_stream(stream);
 
