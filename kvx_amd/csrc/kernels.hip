@@ -1531,6 +1531,47 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
   }
 }
 
+// Rows of sequence s that exist (t < n) for an indexed-format workgroup,
+// plus RAGGED's first token index; false when the workgroup's rows
+// [t0, ...) are all past the end.  seq_len, the indptr pair and (TILE) the
+// KV_OFFSETS entries ek / ev of K and V at logical block lb are independent
+// loads, issued together.
+template <int FMT, bool I64, bool P64, bool TILE = false>
+__device__ __forceinline__ bool indexed_extent(const GatherArgs &a, int64_t s, int64_t t0,
+                                               int64_t &n, int64_t &start, uint32_t lb = 0,
+                                               uint32_t *ek = nullptr, uint32_t *ev = nullptr) {
+  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
+  int64_t end = 0;
+  start = 0;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    start = load_idx<P64>(a.indptr, s);
+    end = load_idx<P64>(a.indptr, s + 1);
+  }
+  if constexpr (TILE) {
+    const int32_t *row =
+        reinterpret_cast<const int32_t *>(a.table) + s * 2 * (int64_t)a.max_blocks_per_seq;
+    *ek = (uint32_t)row[lb];
+    *ev = (uint32_t)row[a.max_blocks_per_seq + lb];
+    // consumed here, so the loads are not sunk below the length test
+    asm volatile("" ::"s"(*ek), "s"(*ev));
+  }
+  // Keep the loads above ahead of their uses, so that they are in flight
+  // together.
+  __builtin_amdgcn_sched_barrier(0);
+  n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
+  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+    int64_t cnt = end - start;
+    const int64_t left = a.table_count - start;  // entries the table holds
+    cnt = left < cnt ? left : cnt;
+    n = cnt < n ? cnt : n;
+    if (start < 0) n = 0;
+  } else {
+    const int64_t cap = (int64_t)a.max_blocks_per_seq * a.block_size;
+    n = cap < n ? cap : n;
+  }
+  return t0 < n;
+}
+
 // RAGGED and KV_OFFSETS gathers (KVX_SPEC.md:99-122).  A workgroup covers
 // `rows_per_wg` output rows of one sequence; every row resolves its own
 // source, so K and V rows come from wherever the table points:
@@ -1639,47 +1680,6 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
                                scale_of(a.vsc, vs, sb, h)));
     }
   }
-}
-
-// Rows of sequence s that exist (t < n) for an indexed-format workgroup,
-// plus RAGGED's first token index; false when the workgroup's rows
-// [t0, ...) are all past the end.  seq_len, the indptr pair and (TILE) the
-// KV_OFFSETS entries ek / ev of K and V at logical block lb are independent
-// loads, issued together.
-template <int FMT, bool I64, bool P64, bool TILE = false>
-__device__ __forceinline__ bool indexed_extent(const GatherArgs &a, int64_t s, int64_t t0,
-                                               int64_t &n, int64_t &start, uint32_t lb = 0,
-                                               uint32_t *ek = nullptr, uint32_t *ev = nullptr) {
-  const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
-  int64_t end = 0;
-  start = 0;
-  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
-    start = load_idx<P64>(a.indptr, s);
-    end = load_idx<P64>(a.indptr, s + 1);
-  }
-  if constexpr (TILE) {
-    const int32_t *row =
-        reinterpret_cast<const int32_t *>(a.table) + s * 2 * (int64_t)a.max_blocks_per_seq;
-    *ek = (uint32_t)row[lb];
-    *ev = (uint32_t)row[a.max_blocks_per_seq + lb];
-    // consumed here, so the loads are not sunk below the length test
-    asm volatile("" ::"s"(*ek), "s"(*ev));
-  }
-  // Keep the loads above ahead of their uses, so that they are in flight
-  // together.
-  __builtin_amdgcn_sched_barrier(0);
-  n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
-  if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
-    int64_t cnt = end - start;
-    const int64_t left = a.table_count - start;  // entries the table holds
-    cnt = left < cnt ? left : cnt;
-    n = cnt < n ? cnt : n;
-    if (start < 0) n = 0;
-  } else {
-    const int64_t cap = (int64_t)a.max_blocks_per_seq * a.block_size;
-    n = cap < n ? cap : n;
-  }
-  return t0 < n;
 }
 
 // Cache address of row t (sequence s) of K (v = false) or V, or nullptr

@@ -181,6 +181,52 @@ def test_tiles_write_x_packed_entries(entry):
                 cache_dtype=DType.BF16, entry="abi" if entry == "abi" else "launch", **kw)
 
 
+def _whole_block_edge_slots(gen, nb, bs, slot64):
+    """Groups aimed at the whole-block test of the tiled write: in order in
+    the block past the end (skipped), in the last and the first block, in
+    reverse order, one slot repeated, and for int64 slots an in-order group
+    at 2**32 (its block id needs the slot's high word); ordinary whole
+    blocks in between."""
+    pool = torch.randperm(nb - 2, generator=gen)[:4] + 1  # blocks other than 0, nb - 1
+    ar = torch.arange(bs)
+    groups = [
+        pool[0] * bs + ar,
+        nb * bs + ar,                 # in order, block == num_blocks
+        pool[1] * bs + ar,
+        (nb - 1) * bs + ar,           # last block
+        0 * bs + ar,                  # first block
+        pool[2] * bs + ar.flip(0),    # reversed
+        pool[3] * bs + torch.where(ar == bs - 1, ar - 1, ar),  # one offset twice
+    ]
+    if slot64:
+        groups.append((1 << 32) + ar)  # in order, aligned, block id >= 2**28
+    return torch.cat(groups)
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[3]],
+                         ids=[_ids(c) for c in (CASES[0], CASES[2], CASES[3])])
+@pytest.mark.parametrize("slot64", [False, True])
+def test_tiles_write_whole_block_edges(case, slot64):
+    """The whole-block path of write_tiles_kernel takes a group only when its
+    slots are block * bs + 0 .. bs - 1 in token order with block < num_blocks;
+    every other group falls back to the run analysis or the per-token path."""
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    gen = torch.Generator().manual_seed(330 + CASES.index(case) * 2 + int(slot64))
+    nb = 24
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    slots = _whole_block_edge_slots(gen, nb, bs, slot64)
+    T = slots.numel()
+    io = DType.BF16 if dt == DType.F8_E4M3 else dt
+    key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+    val = random_fill(torch.empty_like(key), gen)
+    if dt == DType.F8_E4M3:  # finite io values for the quantizing write
+        key = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+        val = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+    scales = dict(k_scale=0.013, v_scale=0.007) if dt == DType.F8_E4M3 else {}
+    slots = slots.to(torch.int64 if slot64 else torch.int32).to(DEV)
+    check_write(pc, kb, vb, key, val, slots, io_dtype=io, cache_dtype=dt, **scales)
+
+
 def _ragged_from_blocks(rng, S, L, bs, nb, spoil_frac, idx_dtype, ptr_dtype):
     """Per-token block ids of S sequences laid out block by block (so most
     tiles' rows name one block), a fraction of tokens given another id
