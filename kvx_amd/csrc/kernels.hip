@@ -38,9 +38,9 @@ constexpr int kTilePad = 16;
 // Compile-time tuning knobs of the contiguous-block gather (defaults are the
 // measured best on MI355X): chunks per lane in flight for the copy and for
 // the FP8 dequantizing gather, and non-temporal (streaming) loads of the
-// cache / stores of the output.  With 4 KiB tiles a lane moves one K and one
-// V chunk; loading both before storing either made the bf16 copy (c2) 7%
-// slower and the dequantizing gather (c4) 2% faster.
+// cache / stores of the output.  A lane moves one K and one V chunk;
+// loading both before storing either made the bf16 copy (c2) 7% slower and
+// the dequantizing gather (c4) 2% faster (256-thread, 4 KiB tiles).
 #ifndef KVX_FLAT_UNROLL
 #define KVX_FLAT_UNROLL 1
 #endif
@@ -53,10 +53,21 @@ constexpr int kTilePad = 16;
 #ifndef KVX_GATHER_NT_STORE
 #define KVX_GATHER_NT_STORE 1
 #endif
-// Cache bytes per tensor one contiguous-block gather workgroup copies: a
-// block is split into power-of-two row ranges of about this size (at least
-// one row).  Many small tiles keep the set of HBM addresses being written
-// at any moment compact, which measures faster than fewer large tiles.
+// Contiguous-block gather (gather_flat_kernel): threads per workgroup and
+// cache bytes per tensor per workgroup.  A block's valid chunks are split
+// into power-of-two ranges of about this size, so that each lane copies one
+// 16-byte chunk of K and one of V.  On MI355X (c2, same box) 128 threads and
+// 2 KiB measured 3.7% faster than 256 threads and 4 KiB, 64 threads and
+// 1 KiB 1% slower (2% faster on c5's 64 KiB blocks); tiles that leave a
+// lane one chunk, or give it more than two, were 5-40% slower.
+#ifndef KVX_FLAT_THREADS
+#define KVX_FLAT_THREADS 128
+#endif
+#ifndef KVX_FLAT_TILE_BYTES
+#define KVX_FLAT_TILE_BYTES 2048
+#endif
+// Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about this
+// many cache bytes of each tensor.
 #ifndef KVX_GATHER_TILE_BYTES
 #define KVX_GATHER_TILE_BYTES 4096
 #endif
@@ -103,6 +114,7 @@ constexpr bool kTokenWriteNtLoad = KVX_TOKEN_WRITE_NT_LOAD != 0;
 
 constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
+constexpr int kFlatThreads = KVX_FLAT_THREADS;
 constexpr int kFlatUnrollDequant = KVX_FLAT_UNROLL_DEQUANT;
 constexpr int kIndexedUnroll = KVX_INDEXED_UNROLL;
 constexpr bool kGatherNtLoad = KVX_GATHER_NT_LOAD != 0;
@@ -1077,9 +1089,10 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
 
 // Canonical-NHD gather: the valid rows of a block are one contiguous run in
 // the cache and in the output, streamed as a flat copy.  A workgroup copies
-// one power-of-two row range of a block (KVX_GATHER_TILE_BYTES).
+// one power-of-two share of the block's chunks (KVX_FLAT_TILE_BYTES).
 // Copy `total` chunks of K and of V: flat index f < 2 * total, K for
-// f < total, V above, so a one-row tile still gives every thread a chunk.
+// f < total, V above, so a tile of kFlatThreads chunks per tensor gives
+// every thread one K chunk and one V chunk.
 // Scale of chunk i (counted from a row start) of a flat run: the
 // per-tensor value, or the indexed entry of block `bid` and the chunk's head.
 __device__ __forceinline__ float run_scale(const GatherArgs &a, bool v, float ks, float vs,
@@ -1091,36 +1104,37 @@ __device__ __forceinline__ float run_scale(const GatherArgs &a, bool v, float ks
   return r.p[bid * r.s_block + (int64_t)h * r.s_head];
 }
 
+// c0: chunk index of ck / cv counted from a row start (indexed scales).
 template <class Op>
 __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, const char *cv,
                                           char *ok, char *ov, int64_t total, float ks, float vs,
-                                          int64_t bid) {
+                                          int64_t bid, int64_t c0) {
   constexpr int U = Op::kScaled ? kFlatUnrollDequant : kFlatUnroll;
   const int64_t both = 2 * total;
   int64_t f = threadIdx.x;
-  for (; f + (U - 1) * kBlockThreads < both; f += U * kBlockThreads) {
+  for (; f + (U - 1) * kFlatThreads < both; f += U * kFlatThreads) {
     Raw<Op::kSrc> x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t g = f + u * kBlockThreads;
+      const int64_t g = f + u * kFlatThreads;
       const bool v = g >= total;
       x[u] = ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + (g - (v ? total : 0)) * Op::kSrc);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t g = f + u * kBlockThreads;
+      const int64_t g = f + u * kFlatThreads;
       const bool v = g >= total;
       const int64_t i = g - (v ? total : 0);
       float sc = v ? vs : ks;
-      if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, i);
+      if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, c0 + i);
       st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst, Op::apply(x[u], sc));
     }
   }
-  for (; f < both; f += kBlockThreads) {
+  for (; f < both; f += kFlatThreads) {
     const bool v = f >= total;
     const int64_t i = f - (v ? total : 0);
     float sc = v ? vs : ks;
-    if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, i);
+    if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, c0 + i);
     st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst,
                                  Op::apply(ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + i * Op::kSrc),
                                            sc));
@@ -1128,7 +1142,7 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 }
 
 template <class Op, bool I64>
-__global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a) {
+__global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a) {
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
   const int64_t s = su;
@@ -1140,22 +1154,26 @@ __global__ __launch_bounds__(kBlockThreads) void gather_flat_kernel(GatherArgs a
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
   const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
-  const int32_t rows_per_part = a.block_size >> a.split_log2;
-  const int64_t t0 = (int64_t)lb * a.block_size + (int64_t)part * rows_per_part;
+  const int64_t t0 = (int64_t)lb * a.block_size;
   if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
+  // The block's valid rows are `valid` consecutive chunks of K (and of V);
+  // this workgroup copies chunks [c0, c0 + per_part) of them.
   const int64_t rem = n - t0;
-  const int32_t rows = rem < rows_per_part ? (int32_t)rem : rows_per_part;
+  const int64_t valid = (rem < a.block_size ? rem : (int64_t)a.block_size) * a.nchunks;
+  const int64_t per_part = ((int64_t)a.block_size * a.nchunks) >> a.split_log2;
+  const int64_t c0 = (int64_t)part * per_part;
+  if (c0 >= valid) return;
+  const int64_t cnt = valid - c0 < per_part ? valid - c0 : per_part;
   float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
-  const int64_t row0 = (int64_t)part * rows_per_part;
-  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
-  flat_copy<Op>(a, a.src_k + bid * a.gk.s_block + row0 * a.gk.s_off,
-                a.src_v + bid * a.gv.s_block + row0 * a.gv.s_off, a.dst_k + out0,
-                a.dst_v + out0, (int64_t)rows * a.nchunks, ks, vs, bid);
+  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes + c0 * Op::kDst;
+  flat_copy<Op>(a, a.src_k + bid * a.gk.s_block + c0 * Op::kSrc,
+                a.src_v + bid * a.gv.s_block + c0 * Op::kSrc, a.dst_k + out0, a.dst_v + out0,
+                cnt, ks, vs, bid, c0);
 }
 
 // Any other layout: rows go to (wave, lane group), each lane keeps the
@@ -1948,7 +1966,7 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
                            g, b, 0, s, a);
       }
     } else if (a.flat) {
-      hipLaunchKernelGGL((gather_flat_kernel<Op, I64>), g, b, 0, s, a);
+      hipLaunchKernelGGL((gather_flat_kernel<Op, I64>), g, dim3(kFlatThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((gather_rows_kernel<Op, I64>), g, b, 0, s, a);
     }
@@ -2411,12 +2429,17 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     a.rows_per_wg = (int32_t)rows;
     a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
   } else if (a.flat) {
-    // split a block into power-of-two row ranges of about TILE_BYTES per tensor
-    const int64_t row_bytes = row_elems * cs;
-    while ((int64_t)(p.block_size >> a.split_log2) * row_bytes > KVX_GATHER_TILE_BYTES &&
-           ((p.block_size >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == p.block_size)
+    // split a block's chunks into a power-of-two number of equal ranges of
+    // about KVX_FLAT_TILE_BYTES of cache per tensor
+    const int64_t chunks = (int64_t)p.block_size * a.nchunks;
+    const int64_t chunk_bytes = (int64_t)ge * cs;
+    while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
+           ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
+           a.split_log2 < 16)
       ++a.split_log2;
-    a.blocks_per_seq <<= a.split_log2;  // workgroups per sequence
+    const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
+    if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
+    a.blocks_per_seq = (int32_t)per_seq;
   }
   if (a.blocks_per_seq <= 0 || p.seq_count <= 0) return KVX_STATUS_OK;
   const int64_t grid = (int64_t)p.seq_count * a.blocks_per_seq;
