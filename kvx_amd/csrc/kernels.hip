@@ -67,9 +67,21 @@ constexpr int kTilePad = 16;
 #define KVX_FLAT_TILE_BYTES 2048
 #endif
 // Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about this
-// many cache bytes of each tensor.
+// many cache bytes of each tensor, in 256-thread workgroups.  The RAGGED
+// copy of row-dense caches (gather_indexed_flat_kernel without a dequant)
+// uses KVX_RAGGED_COPY_THREADS threads and KVX_RAGGED_COPY_TILE_BYTES
+// instead: on MI355X (c2, same box) 64 threads and 2 KiB measured 7% faster
+// than 256 threads and 4 KiB, 128 threads and 2 KiB 5%; the same change
+// made KV_OFFSETS copies 1-2% and the RAGGED dequantizing gather 2-8%
+// slower.
 #ifndef KVX_GATHER_TILE_BYTES
 #define KVX_GATHER_TILE_BYTES 4096
+#endif
+#ifndef KVX_RAGGED_COPY_THREADS
+#define KVX_RAGGED_COPY_THREADS 64
+#endif
+#ifndef KVX_RAGGED_COPY_TILE_BYTES
+#define KVX_RAGGED_COPY_TILE_BYTES 2048
 #endif
 // Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
 // together (the table load and the data load of each are dependent).
@@ -1744,8 +1756,18 @@ __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, 
 // workgroup's rows x chunks of K, then of V, are spread over all threads as
 // in gather_flat_kernel, and each thread resolves the source row of its own
 // chunk (threads of one row load the same table entry).
+// Threads per workgroup of gather_indexed_flat_kernel (see
+// KVX_RAGGED_COPY_THREADS).
+template <class Op, int FMT>
+constexpr int indexed_flat_threads() {
+  return FMT == KVX_BLOCK_TABLE_RAGGED && !Op::kScaled ? KVX_RAGGED_COPY_THREADS
+                                                       : kBlockThreads;
+}
+
 template <class Op, int FMT, bool I64, bool P64>
-__global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(GatherArgs a) {
+__global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
+    GatherArgs a) {
+  constexpr int kT = indexed_flat_threads<Op, FMT>();
   constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled;
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
@@ -1791,14 +1813,14 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_flat_kernel(Gath
   // Chunk f: K for f < total, V above; row r = index >> nchunks_log2.  Each
   // pass resolves kIndexedUnroll chunks' rows, then loads them all, then
   // stores them, so the table and data latencies overlap across chunks.
-  for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * kBlockThreads) {
+  for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * kT) {
     const char *src[kIndexedUnroll];
     char *dst[kIndexedUnroll];
     bool isv[kIndexedUnroll];
     float sc[kIndexedUnroll];
 #pragma unroll
     for (int u = 0; u < kIndexedUnroll; ++u) {
-      const uint32_t f = base + u * kBlockThreads;
+      const uint32_t f = base + u * kT;
       src[u] = nullptr;
       dst[u] = nullptr;
       isv[u] = f >= total;
@@ -1950,7 +1972,7 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
   if (a.format == KVX_BLOCK_TABLE_RAGGED) {
     if (a.flat) {
       hipLaunchKernelGGL((gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g,
-                         b, 0, s, a);
+                         dim3(indexed_flat_threads<Op, KVX_BLOCK_TABLE_RAGGED>()), 0, s, a);
     } else {
       hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g, b, 0,
                          s, a);
@@ -2416,7 +2438,9 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
     };
     a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
-    int64_t rows = KVX_GATHER_TILE_BYTES / (row_elems * cs);
+    const bool ragged_copy = a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy;
+    int64_t rows = (ragged_copy ? KVX_RAGGED_COPY_TILE_BYTES : KVX_GATHER_TILE_BYTES) /
+                   (row_elems * cs);
     const int64_t per_pass = a.flat ? 1 : (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
     rows = rows < per_pass ? per_pass : rows;
     if (a.flat && p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
