@@ -1125,6 +1125,16 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
   const int64_t both = 2 * total;
   int64_t f = threadIdx.x;
   for (; f + (U - 1) * kFlatThreads < both; f += U * kFlatThreads) {
+    // Indexed scales do not depend on the data: look them up first, so that
+    // their loads and the data loads are in flight together.
+    float sc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t g = f + u * kFlatThreads;
+      const bool v = g >= total;
+      sc[u] = v ? vs : ks;
+      if constexpr (Op::kScaled) sc[u] = run_scale(a, v, ks, vs, bid, c0 + g - (v ? total : 0));
+    }
     Raw<Op::kSrc> x[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1137,9 +1147,7 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
       const int64_t g = f + u * kFlatThreads;
       const bool v = g >= total;
       const int64_t i = g - (v ? total : 0);
-      float sc = v ? vs : ks;
-      if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, c0 + i);
-      st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst, Op::apply(x[u], sc));
+      st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst, Op::apply(x[u], sc[u]));
     }
   }
   for (; f < both; f += kFlatThreads) {
