@@ -175,3 +175,32 @@ def test_per_head_scale_kv_offsets_gather(fp8):
     check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=fp8, io_dtype=DType.F16,
                          k_scale=scale_arg(SG.PER_HEAD, gen, nb, H),
                          v_scale=scale_arg(SG.PER_HEAD, gen, nb, H))
+
+
+# Rows wider than the contiguous-block gather's per-workgroup share (2 KiB of
+# cache per tensor): shares end inside rows, the last block of a sequence is
+# partial, and an indexed scale is looked up from the share's first chunk.
+WIDE = [(DType.BF16, None, 16, 256), (DType.F32, None, 8, 128),
+        (DType.F8_E4M3, None, 16, 256), (DType.F8_E4M3, SG.PER_HEAD, 16, 256),
+        (DType.F8_E4M3, SG.PER_BLOCK_HEAD, 16, 256), (DType.F8_E5M2, SG.PER_BLOCK, 8, 512)]
+
+
+@pytest.mark.parametrize("case", WIDE, ids=[f"{c[0].name}-{c[1].name if c[1] else 'copy'}"
+                                            f"-H{c[2]}-D{c[3]}" for c in WIDE])
+def test_flat_gather_wide_rows(case):
+    dt, kind, H, D = case
+    gen = torch.Generator().manual_seed(60 + WIDE.index(case))
+    bs, nb, S, L = 16, 20, 5, 70
+    pc, kb, vb = make_cache(NHD, NHD, dt, nb, bs, H, D, gen=gen)
+    fp8 = dt in (DType.F8_E4M3, DType.F8_E5M2)
+    io = DType.BF16 if fp8 else dt
+    mbps = (L + bs - 1) // bs
+    table = torch.randint(-1, nb + 2, (S, mbps), generator=gen).to(torch.int32).to(DEV)
+    lens = torch.tensor([L, 0, 37, L + 9, 16], dtype=torch.int32, device=DEV)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    scales = {}
+    if fp8:
+        scales = (dict(k_scale=0.013, v_scale=0.021) if kind is None else
+                  dict(k_scale=scale_arg(kind, gen, nb, H), v_scale=scale_arg(kind, gen, nb, H)))
+    check_gather(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=io, **scales)
