@@ -2462,12 +2462,14 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
   } else if (a.flat) {
     // split a block's chunks into a power-of-two number of equal ranges of
-    // about KVX_FLAT_TILE_BYTES of cache per tensor
+    // about KVX_FLAT_TILE_BYTES of cache per tensor, while the grid stays
+    // within 2^31 - 1 workgroups (larger ranges loop inside a workgroup)
     const int64_t chunks = (int64_t)p.block_size * a.nchunks;
     const int64_t chunk_bytes = (int64_t)ge * cs;
+    const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
     while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
            ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
-           a.split_log2 < 16)
+           a.split_log2 < 16 && blocks <= (0x7FFFFFFF >> (a.split_log2 + 1)))
       ++a.split_log2;
     const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
     if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
