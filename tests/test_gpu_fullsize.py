@@ -259,3 +259,32 @@ def test_c5_full_long_context_200gb_pool():
     assert torch.equal(i16(ko[srow, idx]).reshape(-1, H, D), i16(key))
     assert torch.equal(i16(vo[srow, idx]).reshape(-1, H, D), i16(val))
     check_gather_against_indexing(pc, w, ko, vo, kb, vb, seqs_per_chunk=4)
+
+
+def test_token_write_grid_stride_loop():
+    """A write of more rows than the per-token kernel's grid holds (65536
+    workgroups of 4 waves, one 1 KiB row per wave): its waves loop over the
+    remaining rows.  NHD caches, random distinct slots with -1 and
+    out-of-range entries; every written row and every untouched block is
+    checked with torch indexing."""
+    H, D, bs = 4, 128, 16
+    T = 300_000
+    nb = (T + T // 4) // bs
+    gen = torch.Generator(device=DEV).manual_seed(77)
+    pc = paged.alloc_cache(nb, bs, H, D, torch.bfloat16, DEV)
+    pc.key_cache.view(torch.int16).random_(generator=gen)
+    pc.value_cache.view(torch.int16).random_(generator=gen)
+    k0, v0 = pc.key_cache.clone(), pc.value_cache.clone()
+    slots = torch.randperm(nb * bs, generator=gen, device=DEV)[:T]
+    slots[torch.rand(T, generator=gen, device=DEV) < 0.05] = -1
+    slots[torch.rand(T, generator=gen, device=DEV) < 0.01] = nb * bs + 7  # past the blocks
+    key = torch.empty((T, H, D), dtype=torch.bfloat16, device=DEV).normal_(generator=gen)
+    val = torch.empty_like(key).normal_(generator=gen)
+    assert paged.write_kv(pc, key, val, slots) == Status.OK
+    torch.cuda.synchronize()
+    ok = (slots >= 0) & (slots < nb * bs)
+    want_k, want_v = k0.view(-1, H, D), v0.view(-1, H, D)
+    want_k[slots[ok]] = key[ok]
+    want_v[slots[ok]] = val[ok]
+    assert torch.equal(i16(pc.key_cache).view(-1, H, D), i16(want_k))
+    assert torch.equal(i16(pc.value_cache).view(-1, H, D), i16(want_v))
