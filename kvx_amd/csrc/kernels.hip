@@ -642,6 +642,80 @@ __device__ __forceinline__ void group_runs(const WriteArgs &a, int64_t t0, int b
   }
 }
 
+// Run ownership for block sizes up to 32 (2 * bs slots fit one wave).  A
+// run here is a maximal stretch of tokens whose slots are valid, lie in one
+// block and follow each other (slot = previous slot + 1).  The workgroups
+// of group [t0, t0 + bs) own the runs that START in it; such a run ends
+// before t0 + 2 * bs - 1, since it holds at most bs tokens.  Every token
+// then has exactly one owner, and a prefill chunk that starts inside a
+// block has each of its blocks written whole by one workgroup instead of
+// split between two (whose shared 16-byte chunks would then be stored
+// piece by piece).  A whole block in order (write_tile_block's case) is one
+// run starting at t0 either way.
+//
+// Wave 0 loads the slots of tokens t0 - 1 .. t0 + 2 * bs - 2, one per lane,
+// and writes the owned runs to runs[] (LDS); *nruns = their count, or 0
+// when an owned token's slot is < 0 or past the blocks or there are more
+// than kMaxRuns runs (the owned tokens are then written token by token).
+// own[0], own[1]: the owned tokens, [t0 + own[0], t0 + own[1]).  Read after
+// the caller's __syncthreads().
+__device__ __forceinline__ void owned_runs(const WriteArgs &a, int64_t t0, int bs_log2,
+                                           GroupRun *runs, int32_t *nruns, int32_t *own) {
+  const int lane = (int)threadIdx.x;
+  if (lane >= kWave) return;
+  const int bs = 1 << bs_log2;
+  const int64_t t = t0 - 1 + lane;  // lane 0: the token before the group
+  const bool in = lane < 2 * bs && t >= 0 && t < a.num_tokens;
+  int64_t slot = -1;
+  if (in) slot = load_index(a.slots, t, a.slot_is64);
+  const int64_t blk = slot >> bs_log2;
+  const int32_t off = (int32_t)(slot & (bs - 1));
+  const bool ok = in && slot >= 0 && blk < a.num_blocks;
+  const int64_t prev = (int64_t)(((uint64_t)(uint32_t)__shfl_up((int)(slot >> 32), 1) << 32) |
+                                 (uint32_t)__shfl_up((int)slot, 1));
+  const uint64_t oks = __ballot(ok);
+  const uint64_t ins = __ballot(in);
+  const bool prev_ok = lane > 0 && ((oks >> (lane - 1)) & 1ull);
+  // Lanes without a token count as starts: they bound the last run.
+  const bool start = !in || !ok || !prev_ok || off == 0 || slot != prev + 1;
+  const uint64_t starts = __ballot(start);
+  const uint64_t group = ((1ull << bs) - 1ull) << 1;  // lanes of tokens t0 .. t0 + bs - 1
+  const uint64_t mine = starts & group & ins;
+  if (mine == 0) {
+    // The group's tokens all continue a run that starts before t0.
+    if (lane == 0) {
+      *nruns = 0;
+      own[0] = 0;
+      own[1] = 0;
+    }
+    return;
+  }
+  const int first = __ffsll((long long)mine) - 1;
+  const int last = 63 - __clzll((long long)mine);
+  const uint64_t after = last >= 63 ? 0ull : starts & (~0ull << (last + 1));
+  const int end = after ? __ffsll((long long)after) - 1 : kWave;  // exclusive lane
+  const uint64_t owned = (end >= kWave ? ~0ull : ((1ull << end) - 1ull)) & (~0ull << first);
+  const bool bad = (~oks & owned & ins) != 0;
+  const int count = __popcll(mine);
+  const bool take = !bad && count <= kMaxRuns;
+  if (lane == 0) {
+    *nruns = take ? count : 0;
+    own[0] = first - 1;
+    own[1] = end - 1;
+  }
+  if (take && ((mine >> lane) & 1ull)) {
+    const uint64_t later = lane >= 63 ? 0ull : starts & (~0ull << (lane + 1));
+    const int e = later ? __ffsll((long long)later) - 1 : kWave;
+    GroupRun r;
+    r.block = blk;
+    r.lo = off;
+    r.hi = off + (e - lane);
+    r.tok = lane - 1;
+    r.pad_ = 0;
+    runs[__popcll(mine & ((1ull << lane) - 1ull))] = r;
+  }
+}
+
 // Per-token write of the tokens [t0, t0 + bs) of a group that does not fill
 // a block, shared by `nwaves` waves: this workgroup's wave w is wave
 // wave0 + w of them and takes tokens wave0 + w, wave0 + w + nwaves, ...
@@ -993,13 +1067,24 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
     vs = a.vsc.p[0];
   }
   if (write_tile_block<Op, IDX>(a, wt, t0, tile, v, v ? vs : ks, lds)) return;
-  group_runs(a, t0, wt.bs_log2, s_runs, &s_nruns);
+  // Block sizes up to 32: the runs that start in the group (owned_runs);
+  // 64: the group's own tokens split into runs (group_runs).
+  __shared__ int32_t s_own[2];
+  if (wt.bs_log2 <= 5) {
+    owned_runs(a, t0, wt.bs_log2, s_runs, &s_nruns, s_own);
+  } else {
+    group_runs(a, t0, wt.bs_log2, s_runs, &s_nruns);
+    if (threadIdx.x == 0) {
+      s_own[0] = 0;
+      s_own[1] = 1 << wt.bs_log2;
+    }
+  }
   __syncthreads();
   const int32_t nruns = s_nruns;
   if (nruns == 0) {
-    write_group_tokens<TokOp, IDX>(a, t0, 1 << wt.bs_log2, ks, vs,
-                              ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
-                              2 * wt.tiles * kWavesPerBlock);
+    write_group_tokens<TokOp, IDX>(a, t0 + s_own[0], s_own[1] - s_own[0], ks, vs,
+                                   ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
+                                   2 * wt.tiles * kWavesPerBlock);
     return;
   }
   for (int32_t i = 0; i < nruns; ++i) {

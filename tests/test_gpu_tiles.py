@@ -227,6 +227,50 @@ def test_tiles_write_whole_block_edges(case, slot64):
     check_write(pc, kb, vb, key, val, slots, io_dtype=io, cache_dtype=dt, **scales)
 
 
+def _unaligned_chunk_slots(gen, nb, bs, seqs, spoil):
+    """Prefill chunks of `seqs` sequences, each starting at a random offset
+    inside a block and running a random length over distinct random blocks,
+    so that groups of bs tokens straddle blocks and sequences; `spoil`
+    random tokens get slot -1."""
+    perm = torch.randperm(nb, generator=gen)
+    out, used = [], 0
+    for _ in range(seqs):
+        off = int(torch.randint(0, bs, (1,), generator=gen))
+        n = int(torch.randint(1, 4 * bs + 3, (1,), generator=gen))
+        nblk = (off + n + bs - 1) // bs
+        blocks = perm[used:used + nblk]
+        used += nblk
+        p = torch.arange(off, off + n)
+        out.append(blocks[p // bs] * bs + p % bs)
+    slots = torch.cat(out)
+    idx = torch.randperm(slots.numel(), generator=gen)[:spoil]
+    slots[idx] = -1
+    return slots
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+@pytest.mark.parametrize("spoil", [0, 3])
+def test_tiles_write_unaligned_chunks(case, spoil):
+    """Chunks that start inside blocks: each block's run is owned by the
+    workgroups of the group where the run starts, and runs cross group and
+    sequence boundaries."""
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    gen = torch.Generator().manual_seed(340 + CASES.index(case) * 2 + int(spoil > 0))
+    nb = 96
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    slots = _unaligned_chunk_slots(gen, nb, bs, seqs=5, spoil=spoil)
+    T = slots.numel()
+    io = DType.BF16 if dt == DType.F8_E4M3 else dt
+    if dt == DType.F8_E4M3:
+        key = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+        val = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+    else:
+        key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+        val = random_fill(torch.empty_like(key), gen)
+    scales = dict(k_scale=0.013, v_scale=0.007) if dt == DType.F8_E4M3 else {}
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=dt, **scales)
+
+
 def _ragged_from_blocks(rng, S, L, bs, nb, spoil_frac, idx_dtype, ptr_dtype):
     """Per-token block ids of S sequences laid out block by block (so most
     tiles' rows name one block), a fraction of tokens given another id
