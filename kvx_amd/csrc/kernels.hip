@@ -948,17 +948,25 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
   }
 }
 
-// Whole-block fast path of write_tiles_kernel, for the usual prefill group:
-// its bs slots are block * bs + 0 .. bs - 1 in token order.  The group's
-// source rows do not depend on the slots, so every thread issues the loads
-// of its (at most kTileLoads) chunks of the tile first; each wave then
-// loads the bs slots itself (one per lane) and tests them with a ballot, so
-// the slot latency overlaps the data loads and no barrier is needed to
-// share the test.  Every wave reaches the same answer from the same slots.
-// Returns false, having stored nothing, when the group is not such a block
-// (or is the short last group, or its tile needs more than one pass): the
-// caller then runs the general run analysis.  The speculative loads stay
-// within the io rows of tokens [t0, t0 + bs) < num_tokens.
+// Whole-block fast path of write_tiles_kernel, for the usual prefill group.
+// Aligned: the group's bs slots are block * bs + 0 .. bs - 1 in token
+// order.  The group's source rows do not depend on the slots, so every
+// thread issues the loads of its (at most kTileLoads) chunks of the tile
+// first; each wave then loads the bs slots itself (one per lane) and tests
+// them with a ballot, so the slot latency overlaps the data loads and no
+// barrier is needed to share the test.  Every wave reaches the same answer
+// from the same slots.
+// Shifted (block sizes up to 32, where owned_runs decides ownership): a
+// prefill chunk that starts inside a block makes the group's first k
+// tokens continue the run of token t0 - 1 and its next bs tokens fill the
+// following block; the group then owns exactly that block (one run
+// starting at t0 + k).  k follows from the first test's slot of t0, so the
+// loads of rows t0 + k .. are issued together with the slots that confirm
+// it, instead of after the run analysis and a barrier.
+// Returns false, having stored nothing, when the group is neither (or is
+// the short last group, or its tile needs more than one pass): the caller
+// then runs the general run analysis.  The speculative loads stay within the
+// io rows of tokens < num_tokens.
 template <class Op, bool IDX>
 __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const WriteTileArgs &wt,
                                                  int64_t t0, int32_t tile, bool v,
@@ -970,16 +978,17 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   const int32_t total = region >> kDstLog2;                // chunks of the tile
   if (t0 + bs > a.num_tokens || total > kTileLoads * kBlockThreads) return false;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
-  const char *src = (v ? a.src_v : a.src_k) + t0 * a.row_bytes;
+  const char *io = v ? a.src_v : a.src_k;
   const int tid = (int)threadIdx.x;
   const int lane = tid & (kWave - 1);
   int64_t slot = -1;
   if (lane < bs) slot = load_index(a.slots, t0 + lane, a.slot_is64);
 
-  // Source of chunk u.  Row-major cache: the tile is bytes
-  // [tile * region, (tile + 1) * region) of the block, which hold io
-  // elements e = byte >> cache_es_log2 counted from row t0.  Otherwise:
-  // chunk u is chunk (u & cm) of the tile's columns of row u >> cpr_log2.
+  // Source of chunk u for a run starting at token tb.  Row-major cache: the
+  // tile is bytes [tile * region, (tile + 1) * region) of the block, which
+  // hold io elements e = byte >> cache_es_log2 counted from row tb.
+  // Otherwise: chunk u is chunk (u & cm) of the tile's columns of row
+  // tb + (u >> cpr_log2).
   const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
   const int32_t cm = (1 << cpr_log2) - 1;
   const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
@@ -988,26 +997,48 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
                ? (uint32_t)((tile * region + (u << kDstLog2)) >> wt.cache_es_log2)
                : e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
   };
-  auto src_of = [&](int32_t u) -> const char * {
-    return run_log2 < 0 ? src + ((int64_t)elem(u) << wt.io_es_log2)
-                        : src + (int64_t)(u >> cpr_log2) * a.row_bytes +
-                              ((int64_t)elem(u) << wt.io_es_log2);
-  };
   Raw<Op::kSrc> x[kTileLoads];
+  auto load_rows = [&](int64_t tb) {
+    const char *src = io + tb * a.row_bytes;
 #pragma unroll
-  for (int k = 0; k < kTileLoads; ++k) {
-    const int32_t u = tid + k * kBlockThreads;
-    if (u < total) x[k] = ld<Op::kSrc, kWriteNtLoad>(src_of(u));
-  }
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = tid + k * kBlockThreads;
+      if (u < total) {
+        x[k] = ld<Op::kSrc, kWriteNtLoad>(
+            run_log2 < 0 ? src + ((int64_t)elem(u) << wt.io_es_log2)
+                         : src + (int64_t)(u >> cpr_log2) * a.row_bytes +
+                               ((int64_t)elem(u) << wt.io_es_log2));
+      }
+    }
+  };
+  auto uniform64 = [](int64_t x) {
+    return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(x >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)x));
+  };
+  load_rows(t0);
 
-  const int64_t first =
-      (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32)) << 32) |
-                (uint32_t)__builtin_amdgcn_readfirstlane((int)slot));
+  const int64_t first = uniform64(slot);
+  int64_t block = first >> wt.bs_log2;
   const bool in_order = lane >= bs || slot == first + lane;
-  const int64_t block = first >> wt.bs_log2;
   if (__ballot(!in_order) != 0 || first < 0 || (first & (bs - 1)) != 0 ||
-      block >= a.num_blocks)
-    return false;
+      block >= a.num_blocks) {
+    // Shifted: tokens t0 .. t0 + k - 1 hold first, first + 1, ... up to the
+    // end of its block and continue token t0 - 1 (first - 1); tokens t0 + k
+    // .. t0 + k + bs - 1 fill one block in order.
+    if (wt.bs_log2 > 5 || t0 == 0 || first < 0 || block >= a.num_blocks) return false;
+    const int32_t k = bs - (int32_t)(first & (bs - 1));
+    if (k >= bs || t0 + k + bs > a.num_tokens) return false;
+    if (__ballot(lane < k && slot != first + lane) != 0) return false;
+    const int64_t prev = load_index(a.slots, t0 - 1, a.slot_is64);
+    int64_t next = -1;
+    if (lane < bs) next = load_index(a.slots, t0 + k + lane, a.slot_is64);
+    load_rows(t0 + k);
+    const int64_t f2 = uniform64(next);
+    block = f2 >> wt.bs_log2;
+    if (prev != first - 1 || __ballot(lane < bs && next != f2 + lane) != 0 || f2 < 0 ||
+        (f2 & (bs - 1)) != 0 || block >= a.num_blocks)
+      return false;
+  }
 
   const ScaleRef &sr = v ? a.vsc : a.ksc;
   const uint32_t hd = (uint32_t)a.head_dim;
