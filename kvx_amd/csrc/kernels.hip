@@ -115,6 +115,10 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #ifndef KVX_WRITE_NT_LOAD
 #define KVX_WRITE_NT_LOAD 0
 #endif
+// Row-dense writes take write_flat_kernel (1) or write_kernel (0).
+#ifndef KVX_WRITE_FLAT
+#define KVX_WRITE_FLAT 1
+#endif
 #ifndef KVX_TOKEN_WRITE_NT_LOAD
 #define KVX_TOKEN_WRITE_NT_LOAD 1
 #endif
@@ -123,6 +127,7 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #endif
 constexpr bool kWriteNtLoad = KVX_WRITE_NT_LOAD != 0;
 constexpr bool kTokenWriteNtLoad = KVX_TOKEN_WRITE_NT_LOAD != 0;
+constexpr bool kWriteFlat = KVX_WRITE_FLAT != 0;
 
 constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
@@ -482,6 +487,7 @@ struct WriteArgs {
   int32_t chunk_elems;  // G
   int32_t row_bytes;    // bytes of one io row
   int32_t lpt_log2;
+  int32_t nchunks_log2;  // write_flat_kernel: nchunks is a power of two
 };
 
 template <class Op>
@@ -576,6 +582,40 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
                                   Op::apply(yv, scale_of(a.vsc, vs, b, h)));
     }
   }
+}
+
+// Row-dense caches (a token's H * D elements are consecutive in its block
+// row, for K and V): the write is a flat list of (token, chunk) pairs, and
+// each lane of a kFlatThreads-thread workgroup copies one 16-byte chunk of
+// K and one of V.  The chunks are loaded before the token's slot arrives;
+// lanes of one token share the slot's address.  This is the contiguous
+// gather's shape (gather_flat_kernel) from the other side.
+template <class Op>
+__global__ __launch_bounds__(kFlatThreads) void write_flat_kernel(WriteArgs a) {
+  const int64_t f = (int64_t)blockIdx.x * kFlatThreads + threadIdx.x;
+  const int64_t t = f >> a.nchunks_log2;
+  if (t >= a.num_tokens) return;
+  const int32_t c = (int32_t)(f & ((1 << a.nchunks_log2) - 1));
+  const int64_t slot = load_index(a.slots, t, a.slot_is64);
+  const Raw<Op::kSrc> xk = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_k + t * a.row_bytes +
+                                                           (int64_t)c * Op::kSrc);
+  const Raw<Op::kSrc> xv = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_v + t * a.row_bytes +
+                                                           (int64_t)c * Op::kSrc);
+  float ks = 1.0f;
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
+  }
+  if (slot < 0) return;
+  int64_t b, o;
+  split_slot(slot, a.block_size, b, o);
+  if (b >= a.num_blocks) return;
+  const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
+  st<Op::kDst, kWriteNtStore>(a.dst_k + b * a.gk.s_block + o * a.gk.s_off + (int64_t)c * Op::kDst,
+                              Op::apply(xk, scale_at(a.ksc, ks, b, e, (uint32_t)a.head_dim)));
+  st<Op::kDst, kWriteNtStore>(a.dst_v + b * a.gv.s_block + o * a.gv.s_off + (int64_t)c * Op::kDst,
+                              Op::apply(xv, scale_at(a.vsc, vs, b, e, (uint32_t)a.head_dim)));
 }
 
 // ---------------------------------------------------------------------------
@@ -2049,6 +2089,7 @@ hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 // tile size.
 struct WriteLaunch {
   int grid;
+  int64_t flat_grid;  // write_flat_kernel's workgroups, 0 when it does not apply
   bool tiles;
   WriteTileArgs wt;
   int64_t tile_grid;
@@ -2082,6 +2123,9 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
     }
     hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false>), g, dim3(kBlockThreads), w.tile_lds,
                        s, a, w.wt);
+  } else if (w.flat_grid > 0) {
+    hipLaunchKernelGGL(write_flat_kernel<Op>, dim3((uint32_t)w.flat_grid), dim3(kFlatThreads), 0,
+                       s, a);
   } else {
     hipLaunchKernelGGL(write_kernel<Op>, dim3(w.grid), dim3(kBlockThreads), 0, s, a);
   }
@@ -2446,6 +2490,18 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   // 2-4% slower (8% with blocks in ascending order).
   wl.grid = (int)(want < 65536 ? want : 65536);
   wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
+  // write_flat_kernel: K and V rows hold H * D consecutive elements and the
+  // chunk count is a power of two.
+  auto row_dense = [&](const Geom &g) {
+    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
+  };
+  a.nchunks_log2 = log2_exact(a.nchunks);
+  wl.flat_grid = 0;
+  if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
+    const int64_t fg = (((int64_t)p.num_tokens << a.nchunks_log2) + kFlatThreads - 1) /
+                       kFlatThreads;
+    if (fg <= 0x7FFFFFFF) wl.flat_grid = fg;
+  }
   hipStream_t s = as_stream(stream);
 
   if (p.conv == kConvCopy) {

@@ -263,11 +263,12 @@ def test_c5_full_long_context_200gb_pool():
 
 def test_token_write_grid_stride_loop():
     """A write of more rows than the per-token kernel's grid holds (65536
-    workgroups of 4 waves, one 1 KiB row per wave): its waves loop over the
-    remaining rows.  NHD caches, random distinct slots with -1 and
-    out-of-range entries; every written row and every untouched block is
-    checked with torch indexing."""
-    H, D, bs = 4, 128, 16
+    workgroups of 4 waves, one row per wave): its waves loop over the
+    remaining rows.  Three heads make 48 chunks per row, not a power of two,
+    so the write takes write_kernel rather than write_flat_kernel.  NHD
+    caches, random distinct slots with -1 and out-of-range entries; every
+    written row and every untouched block is checked with torch indexing."""
+    H, D, bs = 3, 128, 16
     T = 300_000
     nb = (T + T // 4) // bs
     gen = torch.Generator(device=DEV).manual_seed(77)
