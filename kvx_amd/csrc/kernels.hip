@@ -53,8 +53,9 @@ constexpr int kTilePad = 16;
 #ifndef KVX_GATHER_NT_STORE
 #define KVX_GATHER_NT_STORE 1
 #endif
-// Contiguous-block gather (gather_flat_kernel): threads per workgroup and
-// cache bytes per tensor per workgroup.  A block's valid chunks are split
+// Contiguous-block gather (gather_flat_kernel): threads per workgroup (also
+// those of the row-dense write, write_flat_kernel) and cache bytes per
+// tensor per workgroup.  A block's valid chunks are split
 // into power-of-two ranges of about this size, so that each lane copies one
 // 16-byte chunk of K and one of V.  On MI355X (c2, same box) 128 threads and
 // 2 KiB measured 3.7% faster than 256 threads and 4 KiB, 64 threads and
