@@ -289,3 +289,51 @@ def test_token_write_grid_stride_loop():
     want_v[slots[ok]] = val[ok]
     assert torch.equal(i16(pc.key_cache).view(-1, H, D), i16(want_k))
     assert torch.equal(i16(pc.value_cache).view(-1, H, D), i16(want_v))
+
+
+@pytest.mark.parametrize("layout", ["x_packed_nhd", "vllm"])
+def test_c3_size_chunks_starting_inside_blocks(layout):
+    """c3's size (16 sequences x 2048 tokens) with every chunk starting at a
+    different offset inside its first block, into x-packed K with NHD V or
+    vLLM's pair (x-packed K, token-innermost V): each block is owned by the
+    group where its run starts (whole-block and shifted fast paths, the
+    two-run groups at chunk starts).  Every row must land at its slot, every
+    other byte of the caches keep its value."""
+    H, D, bs, S, C, nb = 8, 128, 16, 16, 2048, 8192
+    gen = torch.Generator().manual_seed(81)
+    perm = torch.randperm(nb, generator=gen)
+    slots, used = [], 0
+    for s in range(S):
+        off = (5 + 3 * s) % bs
+        nblk = (off + C + bs - 1) // bs
+        blocks = perm[used:used + nblk]
+        used += nblk
+        p = torch.arange(off, off + C)
+        slots.append(blocks[p // bs] * bs + p % bs)
+    slots = torch.cat(slots).to(DEV)
+    kc = torch.empty(paged.cache_shape(Layout.BLOCK_HND_PACKED, nb, bs, H, D, 8),
+                     dtype=torch.bfloat16, device=DEV)
+    if layout == "vllm":
+        vstore = torch.empty((nb, H, D, bs), dtype=torch.bfloat16, device=DEV)
+        vc = paged.custom_view(vstore, "bhdo")
+        pc = paged.PagedCache(kc, vc, Layout.BLOCK_HND_PACKED, Layout.BLOCK_CUSTOM, nb, bs, H, D)
+    else:
+        vstore = torch.empty((nb, bs, H, D), dtype=torch.bfloat16, device=DEV)
+        pc = paged.PagedCache(kc, vstore, Layout.BLOCK_HND_PACKED, Layout.BLOCK_NHD, nb, bs, H, D)
+    i16(kc).fill_(-7)
+    i16(vstore).fill_(-7)
+    T = slots.numel()
+    key = torch.randn((T, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((T, H, D), device=DEV).to(torch.bfloat16)
+    assert paged.write_kv(pc, key, val, slots, tokens_per_seq=C) == Status.OK
+    torch.cuda.synchronize()
+    kview = block_view(pc.key_cache, pc.k_layout, 8)
+    vview = block_view(pc.value_cache, pc.v_layout, 8)
+    blk, off = slots // bs, slots % bs
+    assert torch.equal(i16(kview[blk, off]), i16(key))
+    assert torch.equal(i16(vview[blk, off]), i16(val))
+    # no other byte changed: rows not addressed by a slot keep the sentinel
+    hit = torch.zeros(nb * bs, dtype=torch.bool, device=DEV)
+    hit[slots] = True
+    hit = hit.view(nb, bs)
+    assert bool((i16(kview)[~hit] == -7).all()) and bool((i16(vview)[~hit] == -7).all())
