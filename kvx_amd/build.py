@@ -19,6 +19,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -28,7 +29,10 @@ INCLUDE = REPO / "include"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libkvx_amd.so"
 
-SOURCES = ["abi.cpp", "launch.cpp", "kernels.hip"]
+# The kernel families live in kernels_*.hip (one translation unit each, all
+# including kernels.h) so that they compile in parallel.
+SOURCES = ["abi.cpp", "launch.cpp", "dispatch.hip"] + sorted(
+    p.name for p in CSRC.glob("kernels_*.hip"))
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -68,16 +72,28 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(stderr, file=sys.stderr, flush=True)
 
 
+def build_jobs() -> int:
+    """Parallel compiler processes: MAX_JOBS when set, else one per CPU (at
+    most 16)."""
+    env = os.environ.get("MAX_JOBS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, min(16, os.cpu_count() or 1))
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source and link LIB_PATH.  Always rebuilds."""
     OBJ_DIR.mkdir(exist_ok=True)
     cc = hipcc()
-    objs = []
-    for src in SOURCES:
-        obj = OBJ_DIR / (src + ".o")
-        _run([cc, *COMMON_FLAGS, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)],
-             verbose)
-        objs.append(str(obj))
+    objs = [str(OBJ_DIR / (src + ".o")) for src in SOURCES]
+    for stale in OBJ_DIR.glob("*.o"):
+        if str(stale) not in objs:
+            stale.unlink()
+    jobs = [[cc, *COMMON_FLAGS, "-x", "hip", "-c", str(CSRC / src), "-o", obj]
+            for src, obj in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=build_jobs()) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd in jobs]:
+            f.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs,
           "-Wl,-Bsymbolic", "-Wl,--no-undefined",

@@ -1,0 +1,479 @@
+// Host-side launch planning: picks a kernel family, its chunk width, tile
+// shape and grid for a validated write or gather plan, and enqueues it on
+// the caller's stream through the run_* entry points of kernels.h.
+#include <hip/hip_runtime.h>
+
+#include "kernels.h"
+#include "kvx_internal.h"
+
+namespace kvx {
+namespace dev {
+namespace {
+
+GeomBytes to_bytes(const Geom &g, int esize) {
+  GeomBytes r;
+  r.s_block = g.s_block * esize;
+  r.s_off = g.s_off * esize;
+  r.s_head = g.s_head * esize;
+  r.s_piece = g.s_piece * esize;
+  r.s_inner = g.s_inner * esize;
+  r.pack = g.pack;
+  r.pad_ = 0;
+  return r;
+}
+
+bool aligned(const void *p, int64_t b) {
+  return ((uintptr_t)p % (uintptr_t)b) == 0;
+}
+
+// True when chunks of g elements (g*esize bytes each) stay inside one
+// contiguous cache piece and every cache address they use is aligned.
+bool cache_chunk_ok(const Geom &g, const void *base, int esize, int head_dim,
+                    int ge) {
+  const int64_t bytes = (int64_t)ge * esize;
+  if (ge > 1 && g.s_inner != 1) return false;
+  if (g.pack % ge != 0 || head_dim % ge != 0) return false;
+  if (!aligned(base, bytes)) return false;
+  const int64_t strides[4] = {g.s_block, g.s_off, g.s_head, g.s_piece};
+  for (int64_t st : strides) {
+    if ((st * esize) % bytes != 0) return false;
+  }
+  return true;
+}
+
+// Widest chunk (elements) that works for K, V and the io buffers.  The io
+// side is contiguous with rows of H*D elements of io_size bytes.
+int pick_chunk(const Geom &gk, const Geom &gv, const void *ck, const void *cv,
+               int cache_size, const void *ik, const void *iv, int io_size,
+               int head_dim, int max_chunk_bytes_cache) {
+  for (int ge = max_chunk_bytes_cache / cache_size; ge >= 1; ge /= 2) {
+    if (!cache_chunk_ok(gk, ck, cache_size, head_dim, ge)) continue;
+    if (!cache_chunk_ok(gv, cv, cache_size, head_dim, ge)) continue;
+    const int64_t io_bytes = (int64_t)ge * io_size;
+    if (!aligned(ik, io_bytes) || !aligned(iv, io_bytes)) continue;
+    return ge;
+  }
+  return 1;
+}
+
+int lpt_log2_for(int nchunks) {
+  int lg = 0;
+  while ((1 << lg) < nchunks && lg < 6) ++lg;
+  return lg;
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int lg = 0;
+  while ((int64_t(1) << lg) < v) ++lg;
+  return lg;
+}
+
+// Elements of one per-token contiguous run when `g` is a dense block in
+// (run, offset, within-run) order, element e of row o at
+// (e / W) * bs * W + o * W + e % W, else -1: W = H * D (row-major), D (HND),
+// x (x-packed) or 1 (token axis innermost).  Any block stride.
+int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
+  const int64_t p = g.pack;
+  const bool split = p < D;  // d = (d / p) * p + d % p with its own strides
+  if (g.s_inner == 1 && (!split || g.s_piece == p)) {
+    if (g.s_off == H * D && g.s_head == D) return H * D;
+    if (g.s_off == D && g.s_head == bs * D) return D;
+  }
+  if (split && g.s_inner == 1 && g.s_off == p && g.s_piece == bs * p && g.s_head == bs * D)
+    return p;
+  if (g.s_off == 1 && g.s_inner == bs && (!split || g.s_piece == bs * p) && g.s_head == bs * D)
+    return 1;
+  return -1;
+}
+
+// Transposing-gather plan (gather_tiles_kernel) for a PACKED-table gather of
+// dense blocks of which at least one is not row-major, or false.  On MI355X
+// (c2 shapes, bf16) it beats the row kernel for every run length measured:
+// token-innermost 2.45 -> 5.90 TB/s, x-packed 4.66 -> 5.88, HND (256-byte
+// runs) 5.14 -> 5.87.  KVX_TILE_BYTES is the cache bytes per tensor of one
+// tile (8 KiB measured best against 4 and 16 KiB).
+#ifndef KVX_TILE_BYTES
+#define KVX_TILE_BYTES 8192
+#endif
+bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
+                int64_t *grid, uint32_t *lds_bytes) {
+  const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
+  const bool ragged = p.format == KVX_BLOCK_TABLE_RAGGED;
+  if (ragged && p.block_size > kWave) return false;  // one wave compares a tile's ids
+  const int64_t bs = p.block_size;
+  const int64_t H = p.heads;
+  const int64_t D = p.head_dim;
+  const int64_t row_cache = H * D * cs;
+  const int bs_log2 = log2_exact(bs);
+  const int row_log2 = log2_exact(row_cache);
+  if (bs_log2 < 0 || row_log2 < 0 || row_cache < 16) return false;
+  const Geom *g[2] = {&p.gk, &p.gv};
+  const void *src[2] = {p.src_k, p.src_v};
+  void *dst[2] = {p.dst_k, p.dst_v};
+  int run_log2[2];
+  bool transposed = false;
+  int64_t min_tw = 16;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t w = dense_run_elems(*g[i], bs, H, D);
+    if (w < 0) return false;
+    run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
+    if (w != H * D) {
+      if (run_log2[i] < 0) return false;
+      transposed = true;
+      if (w * cs > min_tw) min_tw = w * cs;
+    }
+    // block addresses: base + index * pitch, all 16-byte aligned
+    const uintptr_t base =
+        offsets ? reinterpret_cast<uintptr_t>(p.pool[0]) | reinterpret_cast<uintptr_t>(p.pool[1]) |
+                      (uintptr_t)p.bytes_per_block
+                : reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(g[i]->s_block * cs);
+    if (base % 16 != 0) return false;
+    const int dst_align = src_chunk / cs * is;  // output bytes per chunk
+    if (reinterpret_cast<uintptr_t>(dst[i]) % dst_align != 0) return false;
+  }
+  if (!transposed) return false;  // row-major pairs: the flat kernels
+  if ((D * cs) % src_chunk != 0) return false;  // chunks never straddle heads
+  int64_t tw = row_cache;
+  while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  const int64_t pitch = tw + kTilePad;
+  if (bs * pitch > 64 * 1024) return false;
+  t->table = p.block_table;
+  t->seq_lens = p.seq_lens;
+  t->indptr = p.indptr;
+  t->table_count = p.table_count;
+  t->pool[0] = p.pool[0];
+  t->pool[1] = p.pool[1];
+  t->bytes_per_block = p.bytes_per_block;
+  t->out_row_bytes = H * D * is;
+  t->max_blocks_per_seq = p.max_blocks_per_seq;
+  const int64_t by_len = ((int64_t)p.max_seq_len + bs - 1) / bs;
+  // RAGGED rows do not use max_blocks_per_seq
+  t->blocks_per_seq = (int32_t)(ragged || by_len < p.max_blocks_per_seq ? by_len
+                                                                       : p.max_blocks_per_seq);
+  t->tiles = (int32_t)(row_cache / tw);
+  t->tw_log2 = log2_exact(tw);
+  t->pitch = (int32_t)pitch;
+  t->max_seq_len = p.max_seq_len;
+  t->num_blocks = p.num_blocks;
+  t->head_dim = p.head_dim;
+  t->row_elems = (int32_t)(H * D);
+  t->bs_log2 = bs_log2;
+  t->cache_es_log2 = log2_exact(cs);
+  t->io_es_log2 = log2_exact(is);
+  const ScaleRef sc[2] = {p.k_scale, p.v_scale};
+  for (int i = 0; i < 2; ++i) {
+    t->t[i].src = static_cast<const char *>(src[i]);
+    t->t[i].dst = static_cast<char *>(dst[i]);
+    t->t[i].s_block = g[i]->s_block * cs;
+    t->t[i].sc = sc[i];
+    t->t[i].run_log2 = run_log2[i];
+    t->t[i].pad_ = 0;
+  }
+  *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
+  *lds_bytes = (uint32_t)(bs * pitch);
+  return *grid <= 0x7FFFFFFF;
+}
+
+// Tiled block write plan (write_tiles_kernel): at least bs tokens,
+// power-of-two bs (<= one wave) and cache row bytes, dense blocks of which
+// at least one is not row-major, 16-byte aligned block addresses, io rows
+// aligned to the tile op's source chunk, and (quantizing) heads a whole
+// number of 8-element chunks, so that every chunk has one scale.
+// KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile of a copying
+// write; KVX_QUANT_TILE_BYTES the same for the FP8 quantizing write (whose
+// io rows are 2-4x its cache bytes).  On MI355X (c3 shapes, inputs not
+// cache-resident) 8 KiB measured 1.5-3% faster than 16 KiB for copies, and
+// 4-5% faster than 32 or 64 KiB; the quantizing write is 4-8% faster with
+// 16 KiB; 4 KiB is 25-30% slower for both.  Tiles are 0-5% faster than
+// staging whole blocks of K and V in one workgroup (x-packed / HND), 5x for
+// the token-innermost value cache.
+#ifndef KVX_WRITE_TILE_BYTES
+#define KVX_WRITE_TILE_BYTES 8192
+#endif
+#ifndef KVX_QUANT_TILE_BYTES
+#define KVX_QUANT_TILE_BYTES 16384
+#endif
+bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int64_t *grid,
+                      uint32_t *lds_bytes) {
+  const int64_t bs = p.block_size;
+  const int64_t H = p.heads;
+  const int64_t D = p.head_dim;
+  const int64_t row_cache = H * D * cs;
+  const int bs_log2 = log2_exact(bs);
+  if (bs_log2 < 0 || bs > kWave || p.num_tokens < bs) return false;
+  if (log2_exact(row_cache) < 0 || row_cache < 16) return false;
+  const int src_chunk = p.conv == kConvQuant ? 8 * is : 16;
+  if (p.conv == kConvQuant && D % 8 != 0) return false;
+  const Geom *g[2] = {&p.gk, &p.gv};
+  const void *src[2] = {p.src_k, p.src_v};
+  const void *dst[2] = {p.dst_k, p.dst_v};
+  bool transposed = false;
+  int64_t min_tw = 16;
+  for (int i = 0; i < 2; ++i) {
+    const int64_t w = dense_run_elems(*g[i], bs, H, D);
+    if (w < 0) return false;
+    wt->run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
+    if (w != H * D) {
+      if (wt->run_log2[i] < 0) return false;
+      transposed = true;
+      if (w * cs > min_tw) min_tw = w * cs;
+    }
+    if ((reinterpret_cast<uintptr_t>(dst[i]) | (uintptr_t)(g[i]->s_block * cs)) % 16 != 0)
+      return false;
+    if ((reinterpret_cast<uintptr_t>(src[i]) | (uintptr_t)(H * D * is)) % src_chunk != 0)
+      return false;
+  }
+  if (!transposed) return false;
+  const int64_t tile_bytes =
+      p.conv == kConvQuant ? KVX_QUANT_TILE_BYTES : KVX_WRITE_TILE_BYTES;
+  int64_t tw = row_cache;
+  while (tw * bs > tile_bytes && tw / 2 >= min_tw) tw /= 2;
+  const int64_t pitch = tw + kTilePad;
+  if (bs * pitch > 64 * 1024) return false;
+  wt->tiles = (int32_t)(row_cache / tw);
+  wt->tw_log2 = log2_exact(tw);
+  wt->pitch = (int32_t)pitch;
+  wt->bs_log2 = bs_log2;
+  wt->cache_es_log2 = log2_exact(cs);
+  wt->io_es_log2 = log2_exact(is);
+  *grid = (p.num_tokens + bs - 1) / bs * wt->tiles;
+  *lds_bytes = (uint32_t)(bs * pitch);
+  return *grid <= 0x7FFFFFFF;
+}
+
+}  // namespace
+}  // namespace dev
+
+using namespace dev;
+
+int dtype_size(kvx_dtype_t dt) {
+  switch (dt) {
+    case KVX_DTYPE_F32: return 4;
+    case KVX_DTYPE_F16:
+    case KVX_DTYPE_BF16: return 2;
+    case KVX_DTYPE_F8_E4M3:
+    case KVX_DTYPE_F8_E5M2: return 1;
+    default: return 0;
+  }
+}
+
+kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
+  const int cs = dtype_size((kvx_dtype_t)p.cache_dtype);
+  const int is = dtype_size((kvx_dtype_t)p.io_dtype);
+  const int max_bytes = (p.conv == kConvQuant) ? 8 : 16;
+  const int ge = pick_chunk(p.gk, p.gv, p.dst_k, p.dst_v, cs, p.src_k,
+                            p.src_v, is, p.head_dim, max_bytes);
+  const int64_t row_elems = (int64_t)p.heads * p.head_dim;
+
+  WriteArgs a;
+  a.src_k = static_cast<const char *>(p.src_k);
+  a.src_v = static_cast<const char *>(p.src_v);
+  a.dst_k = static_cast<char *>(p.dst_k);
+  a.dst_v = static_cast<char *>(p.dst_v);
+  a.slots = p.slots;
+  a.ksc = p.k_scale;
+  a.vsc = p.v_scale;
+  a.gk = to_bytes(p.gk, cs);
+  a.gv = to_bytes(p.gv, cs);
+  a.num_tokens = p.num_tokens;
+  a.slot_is64 = p.slot_is64;
+  a.block_size = p.block_size;
+  a.num_blocks = p.num_blocks;
+  a.head_dim = p.head_dim;
+  a.nchunks = (int32_t)(row_elems / ge);
+  a.chunk_elems = ge;
+  a.row_bytes = (int32_t)(row_elems * is);
+  a.lpt_log2 = lpt_log2_for(a.nchunks);
+  const int tpw = kWave >> a.lpt_log2;
+  a.num_groups = (p.num_tokens + tpw - 1) / tpw;
+  const int64_t want = (a.num_groups + kWavesPerBlock - 1) / kWavesPerBlock;
+  WriteLaunch wl;
+  // One wave per token group up to 65536 workgroups, then a grid-stride
+  // loop: on MI355X a 2048-workgroup cap made c3-sized NHD prefill writes
+  // 2-4% slower (8% with blocks in ascending order).
+  wl.grid = (int)(want < 65536 ? want : 65536);
+  wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
+  // write_flat_kernel: K and V rows hold H * D consecutive elements and the
+  // chunk count is a power of two.
+  auto row_dense = [&](const Geom &g) {
+    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
+  };
+  a.nchunks_log2 = log2_exact(a.nchunks);
+  wl.flat_grid = 0;
+  if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
+    const int64_t fg = (((int64_t)p.num_tokens << a.nchunks_log2) + kFlatThreads - 1) /
+                       kFlatThreads;
+    if (fg <= 0x7FFFFFFF) wl.flat_grid = fg;
+  }
+  hipStream_t s = as_stream(stream);
+
+  if (p.conv == kConvCopy) {
+    run_write_copy(ge * cs, a, wl, s);
+  } else {
+    const bool e5 = p.cache_dtype == KVX_DTYPE_F8_E5M2;
+    switch (p.io_dtype) {
+      case KVX_DTYPE_F32:
+        (e5 ? run_write_quant_e5m2_f32 : run_write_quant_e4m3_f32)(ge, a, wl, s);
+        break;
+      case KVX_DTYPE_F16:
+        (e5 ? run_write_quant_e5m2_f16 : run_write_quant_e4m3_f16)(ge, a, wl, s);
+        break;
+      default:
+        (e5 ? run_write_quant_e5m2_bf16 : run_write_quant_e4m3_bf16)(ge, a, wl, s);
+        break;
+    }
+  }
+  return hipGetLastError() == hipSuccess ? KVX_STATUS_OK
+                                         : KVX_STATUS_INTERNAL_ERROR;
+}
+
+kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
+  const int cs = dtype_size((kvx_dtype_t)p.cache_dtype);
+  const int is = dtype_size((kvx_dtype_t)p.io_dtype);
+  const int max_bytes =
+      p.conv != kConvDequant ? 16
+      : p.format == KVX_BLOCK_TABLE_RAGGED ? KVX_RAGGED_DEQUANT_CHUNK : KVX_DEQUANT_CHUNK;
+  const void *base_k = p.src_k;
+  const void *base_v = p.src_v;
+  if (p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+    // Blocks start at pool + index * bytes_per_block: every such address is
+    // as aligned as the OR of both pool pointers and the block pitch.
+    base_k = base_v = reinterpret_cast<const void *>(
+        reinterpret_cast<uintptr_t>(p.pool[0]) | reinterpret_cast<uintptr_t>(p.pool[1]) |
+        (uintptr_t)p.bytes_per_block);
+  }
+  hipStream_t s = as_stream(stream);
+  {
+    // Dense blocks that are not all row-major: the transposing gather.
+    TileArgs t;
+    int64_t tgrid = 0;
+    uint32_t tlds = 0;
+    const bool dq = p.conv == kConvDequant;
+    if (p.seq_count > 0 && plan_tiles(p, cs, is, dq ? KVX_DEQUANT_CHUNK : 16, &t, &tgrid, &tlds)) {
+      if (tgrid == 0) return KVX_STATUS_OK;
+      const bool i64 = p.lens_is64 != 0;
+      const bool p64 = p.indptr_is64 != 0;
+      if (!dq) {
+        run_tiles_copy(t, p.format, i64, p64, tgrid, tlds, s);
+      } else if (p.cache_dtype == KVX_DTYPE_F8_E5M2) {
+        run_tiles_dequant_e5m2(p.io_dtype, t, p.format, i64, p64, tgrid, tlds, s);
+      } else {
+        run_tiles_dequant_e4m3(p.io_dtype, t, p.format, i64, p64, tgrid, tlds, s);
+      }
+      return hipGetLastError() == hipSuccess ? KVX_STATUS_OK : KVX_STATUS_INTERNAL_ERROR;
+    }
+  }
+  const int ge = pick_chunk(p.gk, p.gv, base_k, base_v, cs, p.dst_k,
+                            p.dst_v, is, p.head_dim, max_bytes);
+  const int64_t row_elems = (int64_t)p.heads * p.head_dim;
+
+  GatherArgs a;
+  a.src_k = static_cast<const char *>(p.src_k);
+  a.src_v = static_cast<const char *>(p.src_v);
+  a.dst_k = static_cast<char *>(p.dst_k);
+  a.dst_v = static_cast<char *>(p.dst_v);
+  a.table = p.block_table;
+  a.seq_lens = p.seq_lens;
+  a.ksc = p.k_scale;
+  a.vsc = p.v_scale;
+  a.gk = to_bytes(p.gk, cs);
+  a.gv = to_bytes(p.gv, cs);
+  a.out_row_bytes = row_elems * is;
+  a.index_is64 = p.index_is64;
+  a.lens_is64 = p.lens_is64;
+  a.indptr = p.indptr;
+  a.indptr_is64 = p.indptr_is64;
+  a.table_count = p.table_count;
+  a.pool[0] = p.pool[0];
+  a.pool[1] = p.pool[1];
+  a.bytes_per_block = p.bytes_per_block;
+  a.format = p.format;
+  a.rows_per_wg = 0;
+  a.max_blocks_per_seq = p.max_blocks_per_seq;
+  const int64_t by_len =
+      ((int64_t)p.max_seq_len + p.block_size - 1) / p.block_size;
+  a.blocks_per_seq =
+      (int32_t)(by_len < p.max_blocks_per_seq ? by_len : p.max_blocks_per_seq);
+  a.max_seq_len = p.max_seq_len;
+  a.block_size = p.block_size;
+  a.num_blocks = p.num_blocks;
+  a.head_dim = p.head_dim;
+  a.nchunks = (int32_t)(row_elems / ge);
+  a.chunk_elems = ge;
+  a.lpt_log2 = lpt_log2_for(a.nchunks);
+  // Rows of a block form one contiguous run when each row is H*D
+  // consecutive elements and consecutive offsets are one row apart.
+  auto rows_contiguous = [&](const Geom &g) {
+    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim &&
+           g.s_off == row_elems;
+  };
+  a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
+  a.split_log2 = 0;
+  a.nchunks_log2 = log2_exact(a.nchunks);
+  a.bs_log2 = log2_exact(p.block_size);
+  if (p.format != KVX_BLOCK_TABLE_PACKED) {
+    // indexed formats: tiles of rows, about TILE_BYTES of each tensor's cache
+    // rows.  Rows that are H*D contiguous elements (any row stride) and a
+    // power-of-two chunk count take the flat kernel; otherwise the row
+    // kernel, with at least one full pass of its row groups.
+    auto row_dense = [&](const Geom &g) {
+      return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
+    };
+    a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
+    const bool ragged_copy = a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy;
+    int64_t rows = (ragged_copy ? KVX_RAGGED_COPY_TILE_BYTES : KVX_GATHER_TILE_BYTES) /
+                   (row_elems * cs);
+    const int64_t per_pass = a.flat ? 1 : (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
+    rows = rows < per_pass ? per_pass : rows;
+    if (a.flat && p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
+      // a power of two no larger than the (power-of-two) block: tiles never
+      // straddle blocks
+      int64_t r2 = 1;
+      while (r2 * 2 <= rows && r2 * 2 <= p.block_size) r2 *= 2;
+      rows = r2;
+    }
+    a.rows_per_wg = (int32_t)rows;
+    a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
+  } else if (a.flat) {
+    // split a block's chunks into a power-of-two number of equal ranges of
+    // about KVX_FLAT_TILE_BYTES of cache per tensor, while the grid stays
+    // within 2^31 - 1 workgroups (larger ranges loop inside a workgroup)
+    const int64_t chunks = (int64_t)p.block_size * a.nchunks;
+    const int64_t chunk_bytes = (int64_t)ge * cs;
+    const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
+    while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
+           ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
+           a.split_log2 < 16 && blocks <= (0x7FFFFFFF >> (a.split_log2 + 1)))
+      ++a.split_log2;
+    const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
+    if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
+    a.blocks_per_seq = (int32_t)per_seq;
+  }
+  if (a.blocks_per_seq <= 0 || p.seq_count <= 0) return KVX_STATUS_OK;
+  const int64_t grid = (int64_t)p.seq_count * a.blocks_per_seq;
+  if (grid > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;  // one workgroup per block
+
+  if (p.conv == kConvCopy) {
+    run_gather_copy(ge * cs, a, grid, s);
+  } else {
+    const bool e5 = p.cache_dtype == KVX_DTYPE_F8_E5M2;
+    switch (p.io_dtype) {
+      case KVX_DTYPE_F32:
+        (e5 ? run_gather_dequant_e5m2_f32 : run_gather_dequant_e4m3_f32)(ge, a, grid, s);
+        break;
+      case KVX_DTYPE_F16:
+        (e5 ? run_gather_dequant_e5m2_f16 : run_gather_dequant_e4m3_f16)(ge, a, grid, s);
+        break;
+      default:
+        (e5 ? run_gather_dequant_e5m2_bf16 : run_gather_dequant_e4m3_bf16)(ge, a, grid, s);
+        break;
+    }
+  }
+  return hipGetLastError() == hipSuccess ? KVX_STATUS_OK
+                                         : KVX_STATUS_INTERNAL_ERROR;
+}
+
+}  // namespace kvx

@@ -1,0 +1,12 @@
+// Quantizing writes of f32 rows into an FP8 E5M2 cache.
+#include "kernels.h"
+
+namespace kvx {
+namespace dev {
+
+void run_write_quant_e5m2_f32(int ge, const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
+  dispatch_quant<KVX_DTYPE_F32, KVX_DTYPE_F8_E5M2>(ge, a, w, s);
+}
+
+}  // namespace dev
+}  // namespace kvx

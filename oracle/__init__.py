@@ -78,6 +78,16 @@ def lib() -> C.CDLL:
         L.oracle_gather_kv_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i, i32,
                                                           i32, i32, i32, i32, i32, i32, i]
         L.oracle_gather_kv_fast.restype = i
+        L.oracle_write_kv_quant_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64,
+                                                               i32, i32, i32, i32, i, i, f32,
+                                                               f32]
+        L.oracle_write_kv_quant_fast.restype = i
+        L.oracle_gather_kv_dequant_fast.argtypes = geom + geom + [vp, vp, vp, vp, vp, vp, i,
+                                                                  i32, i32, i32, i32, i32, i32,
+                                                                  i32, i, i, f32, f32]
+        L.oracle_gather_kv_dequant_fast.restype = i
+        L.oracle_quantize_fp8_fast.argtypes = [vp, i, i64, f32, i, vp]
+        L.oracle_dequantize_fp8_fast.argtypes = [vp, i64, f32, i, i, vp]
         L.oracle_set_threads.argtypes = [i]
         L.oracle_set_threads.restype = i
         L.oracle_gather_kv_ragged.argtypes = geom + geom + [vp, vp, vp, vp, vp, i, i64, vp, i,
@@ -231,6 +241,52 @@ def gather_kv_fast(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out,
                                        int(block_table.dtype == np.int64), seq_count,
                                        max_blocks_per_seq, max_seq_len, heads, head_dim,
                                        block_size, num_blocks, elem_size)
+
+
+def write_kv_quant_fast(gk: Geometry, gv: Geometry, key, value, key_cache, value_cache,
+                        slots, *, heads, head_dim, block_size, num_blocks, io_dtype,
+                        cache_dtype, k_scale: float, v_scale: float) -> int:
+    """Quantizing write of write_kv with per-tensor scales, OpenMP and
+    table-driven casts (the timed CPU baseline of FP8 caches)."""
+    slots = np.ascontiguousarray(slots)
+    return lib().oracle_write_kv_quant_fast(*gk.args(), *gv.args(), _ptr(key), _ptr(value),
+                                            _ptr(key_cache), _ptr(value_cache), _ptr(slots),
+                                            int(slots.dtype == np.int64), int(slots.size),
+                                            heads, head_dim, block_size, num_blocks,
+                                            int(io_dtype), int(cache_dtype), float(k_scale),
+                                            float(v_scale))
+
+
+def gather_kv_dequant_fast(gk: Geometry, gv: Geometry, key_cache, value_cache, key_out,
+                           value_out, block_table, seq_lens, *, seq_count,
+                           max_blocks_per_seq, max_seq_len, heads, head_dim, block_size,
+                           num_blocks, cache_dtype, io_dtype, k_scale: float,
+                           v_scale: float) -> int:
+    """Dequantizing gather of gather_kv with per-tensor scales, OpenMP and
+    table-driven casts (the timed CPU baseline of FP8 caches)."""
+    return lib().oracle_gather_kv_dequant_fast(
+        *gk.args(), *gv.args(), _ptr(key_cache), _ptr(value_cache), _ptr(key_out),
+        _ptr(value_out), _ptr(block_table), _ptr(seq_lens), int(block_table.dtype == np.int64),
+        seq_count, max_blocks_per_seq, max_seq_len, heads, head_dim, block_size, num_blocks,
+        int(cache_dtype), int(io_dtype), float(k_scale), float(v_scale))
+
+
+def quantize_fp8_fast(x: np.ndarray, io_dtype: int, scale: float, fp8: int = 4) -> np.ndarray:
+    """quantize_fp8 through the fast paths' table-driven cast."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(x.size, np.uint8)
+    lib().oracle_quantize_fp8_fast(_ptr(x), int(io_dtype), x.size, float(scale), int(fp8),
+                                   _ptr(out))
+    return out
+
+
+def dequantize_fp8_fast(q: np.ndarray, scale: float, io_dtype: int, fp8: int = 4) -> np.ndarray:
+    """dequantize_fp8 through the fast paths' table-driven cast."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    out = np.empty(q.size, np.uint32 if int(io_dtype) == 3 else np.uint16)
+    lib().oracle_dequantize_fp8_fast(_ptr(q), q.size, float(scale), int(fp8), int(io_dtype),
+                                     _ptr(out))
+    return out
 
 
 def set_threads(n: int) -> int:

@@ -568,3 +568,166 @@ int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
   }
   return threads_used();
 }
+
+/* ------------------------------------------------------------------------ */
+/* Fast FP8 variants (the timed CPU baseline of FP8 caches).                  */
+/*                                                                            */
+/* Quantize: every rounding boundary of E4M3 and E5M2 (the midpoint of two    */
+/* adjacent codes, and the saturation threshold) has at most 4 significant   */
+/* bits, so it is a bf16 value.  An f32 whose upper 16 bits are u therefore   */
+/* lies in [bf16(u), next bf16) with no boundary strictly inside: its code is */
+/* that of bf16(u) itself when its lower 16 bits are 0 (ties included), and   */
+/* that of any value just above bf16(u) otherwise.  Two 65536-entry tables    */
+/* per format, filled with the element-wise casts, give every f32's code.     */
+/* Dequantize: a 256-entry table of code values, one f32 product, and the     */
+/* round-to-nearest-even narrowing to bf16 (f16 and f32 outputs use the       */
+/* element-wise store).                                                       */
+
+static uint8_t fq_lo[2][65536], fq_hi[2][65536];
+static float fdq[2][256];
+static int ftables_ready;
+
+static void fast_tables(void) {
+  if (ftables_ready) return;
+  for (int f = 0; f < 2; ++f) {
+    for (uint32_t u = 0; u < 65536; ++u) {
+      const float lo = float_of(u << 16), hi = float_of((u << 16) | 1u);
+      fq_lo[f][u] = f ? oracle_f32_to_e5m2(lo) : oracle_f32_to_e4m3(lo);
+      fq_hi[f][u] = f ? oracle_f32_to_e5m2(hi) : oracle_f32_to_e4m3(hi);
+    }
+    for (int q = 0; q < 256; ++q)
+      fdq[f][q] = f ? oracle_e5m2_to_f32((uint8_t)q) : oracle_e4m3_to_f32((uint8_t)q);
+  }
+  ftables_ready = 1;
+}
+
+static inline uint8_t fast_to_fp8(float q, int e5) {
+  const uint32_t u = bits_of(q);
+  return (u & 0xFFFFu) ? fq_hi[e5][u >> 16] : fq_lo[e5][u >> 16];
+}
+
+static inline uint16_t fast_f32_to_bf16(float v) {
+  const uint32_t u = bits_of(v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+static inline float fast_load_io(const uint8_t *p, int dt) {
+  if (dt == D_BF16) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return float_of((uint32_t)h << 16);
+  }
+  return load_io_f32(p, dt);
+}
+
+static inline void fast_store_io(uint8_t *p, int dt, float v) {
+  if (dt == D_BF16) {
+    const uint16_t h = fast_f32_to_bf16(v);
+    memcpy(p, &h, 2);
+  } else {
+    store_io_f32(p, dt, v);
+  }
+}
+
+void oracle_quantize_fp8_fast(const void *in, int io_dtype, int64_t n, float scale,
+                              int fp8_dtype, uint8_t *out) {
+  fast_tables();
+  const int es = dtype_size(io_dtype), e5 = fp8_dtype == D_E5M2;
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = fast_to_fp8(fast_load_io((const uint8_t *)in + i * es, io_dtype) / scale, e5);
+}
+
+void oracle_dequantize_fp8_fast(const uint8_t *in, int64_t n, float scale, int fp8_dtype,
+                                int io_dtype, void *out) {
+  fast_tables();
+  const int es = dtype_size(io_dtype), e5 = fp8_dtype == D_E5M2;
+  for (int64_t i = 0; i < n; ++i)
+    fast_store_io((uint8_t *)out + i * es, io_dtype, fdq[e5][in[i]] * scale);
+}
+
+int oracle_write_kv_quant_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                               int v_layout, const int64_t *v_stride, int64_t v_pack,
+                               const void *key, const void *value, void *key_cache,
+                               void *value_cache, const void *slots, int slot_is64,
+                               int64_t num_tokens, int32_t heads, int32_t head_dim,
+                               int32_t block_size, int32_t num_blocks, int io_dtype,
+                               int cache_dtype, float k_scale, float v_scale) {
+  fast_tables();
+  const int64_t kr = run_elems(k_layout, k_stride, k_pack, head_dim);
+  const int64_t vr = run_elems(v_layout, v_stride, v_pack, head_dim);
+  const int is = dtype_size(io_dtype), e5 = cache_dtype == D_E5M2;
+  const uint8_t *k_in = key, *v_in = value;
+  uint8_t *kc = key_cache, *vc = value_cache;
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    const int64_t slot = load_index(slots, t, slot_is64);
+    if (slot < 0) continue;
+    const int64_t b = slot / block_size;
+    const int64_t o = slot - b * block_size;
+    if (b >= num_blocks) continue;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t row = (t * heads + h) * head_dim;
+      for (int64_t d = 0; d < head_dim; d += kr) {
+        uint8_t *dst = kc + oracle_cache_offset(k_layout, k_stride, k_pack, b, o, h, d);
+        for (int64_t j = 0; j < kr; ++j)
+          dst[j] = fast_to_fp8(fast_load_io(k_in + (row + d + j) * is, io_dtype) / k_scale, e5);
+      }
+      for (int64_t d = 0; d < head_dim; d += vr) {
+        uint8_t *dst = vc + oracle_cache_offset(v_layout, v_stride, v_pack, b, o, h, d);
+        for (int64_t j = 0; j < vr; ++j)
+          dst[j] = fast_to_fp8(fast_load_io(v_in + (row + d + j) * is, io_dtype) / v_scale, e5);
+      }
+    }
+  }
+  return threads_used();
+}
+
+int oracle_gather_kv_dequant_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                                  int v_layout, const int64_t *v_stride, int64_t v_pack,
+                                  const void *key_cache, const void *value_cache,
+                                  void *key_out, void *value_out,
+                                  const void *block_table, const void *seq_lens,
+                                  int index_is64, int32_t seq_count,
+                                  int32_t max_blocks_per_seq, int32_t max_seq_len,
+                                  int32_t heads, int32_t head_dim, int32_t block_size,
+                                  int32_t num_blocks, int cache_dtype, int io_dtype,
+                                  float k_scale, float v_scale) {
+  fast_tables();
+  const int64_t kr = run_elems(k_layout, k_stride, k_pack, head_dim);
+  const int64_t vr = run_elems(v_layout, v_stride, v_pack, head_dim);
+  const int64_t nlb = ((int64_t)max_seq_len + block_size - 1) / block_size;
+  const int is = dtype_size(io_dtype), e5 = cache_dtype == D_E5M2;
+  const float *tab = fdq[e5];
+  const uint8_t *kc = key_cache, *vc = value_cache;
+  uint8_t *ko_ = key_out, *vo_ = value_out;
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t w = 0; w < (int64_t)seq_count * nlb; ++w) {
+    const int64_t s = w / nlb, lb = w - s * nlb;
+    if (lb >= max_blocks_per_seq) continue;
+    const int64_t seq_len = load_index(seq_lens, s, index_is64);
+    const int64_t n = seq_len < max_seq_len ? seq_len : max_seq_len;
+    const int64_t t0 = lb * block_size;
+    if (t0 >= n) continue;
+    const int64_t bid = load_index(block_table, s * max_blocks_per_seq + lb, index_is64);
+    if (bid < 0 || bid >= num_blocks) continue;
+    const int64_t t1 = t0 + block_size < n ? t0 + block_size : n;
+    for (int64_t t = t0; t < t1; ++t) {
+      const int64_t o = t - t0;
+      for (int64_t h = 0; h < heads; ++h) {
+        const int64_t row = ((s * max_seq_len + t) * heads + h) * head_dim;
+        for (int64_t d = 0; d < head_dim; d += kr) {
+          const uint8_t *src = kc + oracle_cache_offset(k_layout, k_stride, k_pack, bid, o, h, d);
+          for (int64_t j = 0; j < kr; ++j)
+            fast_store_io(ko_ + (row + d + j) * is, io_dtype, tab[src[j]] * k_scale);
+        }
+        for (int64_t d = 0; d < head_dim; d += vr) {
+          const uint8_t *src = vc + oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d);
+          for (int64_t j = 0; j < vr; ++j)
+            fast_store_io(vo_ + (row + d + j) * is, io_dtype, tab[src[j]] * v_scale);
+        }
+      }
+    }
+  }
+  return threads_used();
+}

@@ -116,6 +116,35 @@ int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
                           int32_t heads, int32_t head_dim, int32_t block_size,
                           int32_t num_blocks, int elem_size);
 
+/* FP8 variants of the fast paths (the timed CPU baseline of FP8 caches):
+ * per-tensor scales, same results as oracle_write_kv / oracle_gather_kv.
+ * The casts are table lookups built once from the element-wise casts below
+ * (oracle_quantize_fp8_fast / oracle_dequantize_fp8_fast expose them for the
+ * tests).  Return the number of OpenMP threads used. */
+int oracle_write_kv_quant_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                               int v_layout, const int64_t *v_stride, int64_t v_pack,
+                               const void *key, const void *value, void *key_cache,
+                               void *value_cache, const void *slots, int slot_is64,
+                               int64_t num_tokens, int32_t heads, int32_t head_dim,
+                               int32_t block_size, int32_t num_blocks, int io_dtype,
+                               int cache_dtype, float k_scale, float v_scale);
+
+int oracle_gather_kv_dequant_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
+                                  int v_layout, const int64_t *v_stride, int64_t v_pack,
+                                  const void *key_cache, const void *value_cache,
+                                  void *key_out, void *value_out,
+                                  const void *block_table, const void *seq_lens,
+                                  int index_is64, int32_t seq_count,
+                                  int32_t max_blocks_per_seq, int32_t max_seq_len,
+                                  int32_t heads, int32_t head_dim, int32_t block_size,
+                                  int32_t num_blocks, int cache_dtype, int io_dtype,
+                                  float k_scale, float v_scale);
+
+void oracle_quantize_fp8_fast(const void *in, int io_dtype, int64_t n, float scale,
+                              int fp8_dtype, uint8_t *out);
+void oracle_dequantize_fp8_fast(const uint8_t *in, int64_t n, float scale, int fp8_dtype,
+                                int io_dtype, void *out);
+
 /* Threads of the *_fast functions from now on (n > 0); returns the previous
  * count (always 1 without OpenMP). */
 int oracle_set_threads(int n);
