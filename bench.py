@@ -1,45 +1,68 @@
 #!/usr/bin/env python3
 """Benchmark of the KVX paged KV write + gather hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config c2] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W]            headline + every config
+    python bench.py --config cN [options]              one configuration only
+    python bench.py --sweep c3 [--sweep-scales 1,2,4,8]  size sweep of c3
+    python bench.py --copy-probe                       rocprofv3 calibration
 
-Default workload: Llama-3-8B-shaped decode, bf16, 32
-layers, 8 KV heads x 128, block_size 16, batch 256, contexts U[512, 8192],
-5% of slots -1.  One step = for each of the 32 layers (each with its own
-~4.6 GB paged K+V pool): the decode write of 256 new tokens, then the gather
-of every sequence's full context into contiguous [256, 8192, 8, 128] K and V
+Headline: Llama-3-8B-shaped decode, bf16, 32 layers,
+8 KV heads x 128, block_size 16, batch 256, contexts U[512, 8192], 5% of
+slots -1.  One step = for each of the 32 layers (each with its own ~4.6 GB
+paged K+V pool): the decode write of 256 new tokens, then the gather of
+every sequence's full context into contiguous [256, 8192, 8, 128] K and V
 buffers (shared across layers, as an attention workspace would be).  All
-inputs are resident in HBM before timing; every launch goes through the
-C ABI (kvx_launch_write_kv / kvx_launch_gather_kv) on one HIP stream.
+inputs are resident in HBM before timing; every launch goes through the C
+ABI (kvx_launch_write_kv* / kvx_launch_gather_kv*) on one HIP stream.
 
 value = algorithmic bytes of the whole step / step time (GB/s, 1e9), where
 algorithmic bytes are the bytes a perfect implementation must move: every
 valid K/V row read once and written once, plus the index arrays used
 (kvx_amd.workloads.write_bytes / gather_bytes).
 
-The roofline entry is for the dominant kernel (the gather): its algorithmic
-bytes per launch / its mean launch duration, the duration measured with HIP
-events recorded on the launch stream around every gather launch inside the
-timed region.  `traffic` is read from the committed rocprofv3 counter
-summary (profiles/) when present.
+roofline: the dominant kernel (the gather): its algorithmic bytes per
+launch / its mean launch duration, measured with HIP events recorded on the
+launch stream around every launch inside the timed region.  `traffic` is
+the HBM bytes per launch of the committed rocprofv3 counter summary
+(profiles/traffic_<kind>_<workload>.json), used only when that summary was
+taken of the same algorithmic bytes and of the kernel sources now in the
+tree (sha256 of kvx_amd/csrc's kernel files); otherwise null.
 
-cpu_baseline: the CPU oracle's row-memcpy write + gather (oracle/, OpenMP)
-timed on this host's cores over a bounded sample of the same workload.
+configs: the other BASELINE configurations, each timed the same way in the
+same run (c1 TinyLlama, c3 chunked prefill write, c4 FP8 E4M3 decode with a
+dequantizing gather, c5 Llama-3-70B bs32 on a ~200 GB pool), each with its
+kernels' mean / median, GB/s, fraction of peak and its own CPU baseline.
 
-Outside the timed region: copy_reference (torch's device copy of 1 GiB on
-the same stream) and write_graph (the workload's writes captured in one HIP
-graph and replayed: device time per write without per-call launch cost).
+stream_ceiling: plain streaming copy / read / write kernels
+(libkvx_amd_probe.so, several launch shapes, the fastest reported) over the
+same byte count as the dominant kernel, on buffers beyond the 256 MB
+Infinity Cache: the best the box sustains with no index work.
+
+cpu_baseline: the CPU oracle's OpenMP fast path (row memcpy; table-driven
+casts for FP8) timed on this host's cores, threads pinned, over a bounded
+sample of the same workload.
+
+write_graph: the headline's 32 decode writes captured in one HIP graph and
+replayed with every cache level flushed before each replay (a 1 GiB read),
+so the device time per write is an HBM figure without per-call launch cost.
 """
 from __future__ import annotations
 
-import argparse
-import ctypes as C
-import json
 import os
-import statistics
-import sys
-import time
-from pathlib import Path
+
+# Pin the CPU baseline's OpenMP threads (one per core, in order) unless the
+# caller chose otherwise; libgomp reads these when it initialises.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
+import argparse  # noqa: E402
+import ctypes as C  # noqa: E402
+import hashlib  # noqa: E402
+import json  # noqa: E402
+import statistics  # noqa: E402
+import sys  # noqa: E402
+import time  # noqa: E402
+from pathlib import Path  # noqa: E402
 
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
@@ -47,6 +70,9 @@ sys.path.insert(0, str(REPO))
 METRIC = ("achieved HBM GB/s (% of peak) and tokens/s for KV write+gather, "
           "1 MI355X")
 PEAK_HBM_GBS = 8000.0
+# Timed launches of the dominant kernel per sub-configuration, at least.
+MIN_LAUNCHES = {"c1": 64, "c3": 64, "c4": 64, "c5": 20}
+CPU_SAMPLE_SEQS = {"c1": 8, "c2": 64, "c3": 16, "c4": 32, "c5": 8}
 
 
 def parse_args():
@@ -54,7 +80,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c4", "c5"],
+                   help="run one configuration as the headline, without the others "
+                        "(default: c2 as the headline, then c1, c3, c4, c5)")
     p.add_argument("--table", default="packed", choices=["packed", "ragged", "kv_offsets"],
                    help="block-table format of the gather (c1, c2, c4, c5); kv_offsets "
                         "puts K and V blocks in one TensorRT-LLM-style pool")
@@ -78,11 +106,23 @@ def parse_args():
                         "block, per block and head)")
     p.add_argument("--layers", type=int, default=None,
                    help="override the layer count of c1/c2/c4")
+    p.add_argument("--c3-order", default="random", choices=["random", "ascending"],
+                   help="c3: block assignment (random draw from the pool, or ascending "
+                        "as a fresh allocator hands blocks out)")
+    p.add_argument("--c3-seqs", type=int, default=16,
+                   help="c3: 2048-token chunks per write (pool 512 blocks per chunk)")
+    p.add_argument("--sweep", default=None, choices=["c3"],
+                   help="time c3's write, the PACKED gather of the same table and a plain "
+                        "copy of the same bytes at several sizes; fit time = intercept + "
+                        "bytes / slope")
+    p.add_argument("--sweep-scales", default="1,2,4,8",
+                   help="--sweep: multiples of c3's 16 sequences")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0,
-                   help="CPU baseline sampling budget")
+    p.add_argument("--cpu-seconds", type=float, default=5.0,
+                   help="CPU baseline sampling budget per configuration")
     p.add_argument("--profile-only", action="store_true",
-                   help="skip the CPU baseline (profiler runs)")
+                   help="time only the KV kernels (no CPU baseline, stream ceiling or "
+                        "graph): the command profiler runs use")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run three plain 1 GiB device copies: the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -117,8 +157,18 @@ class Launch:
             raise RuntimeError(f"{self.kind} launch returned status {st}")
 
 
-def build_config(name: str, layers_override, dev, table_fmt="packed", write_entry="launch",
-                 fp8="e4m3", scales="tensor", layout=None, heads=None):
+class Built:
+    """A configuration on the device: the workload, the per-step launch
+    lists (rotated by step index), the config record and every buffer."""
+
+    def __init__(self, w, steps, cfg, keep, extra=None):
+        self.w, self.steps, self.cfg, self.keep = w, steps, cfg, keep
+        self.extra = extra or {}
+
+
+def build_config(name: str, dev, layers_override=None, table_fmt="packed",
+                 write_entry="launch", fp8="e4m3", scales="tensor", layout=None,
+                 heads=None, c3_seqs=16, c3_order="random", c3_gathers=False) -> Built:
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -127,7 +177,10 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
     lib = abi.load()
     tdt = {DType.BF16: torch.bfloat16, DType.F16: torch.float16,
            DType.F8_E4M3: torch.float8_e4m3fn, DType.F8_E5M2: torch.float8_e5m2}
-    w = W.CONFIGS[name]()
+    if name == "c3":
+        w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order)
+    else:
+        w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
     if (fp8 != "e4m3" or scales != "tensor") and name != "c4":
         raise SystemExit("--fp8 / --scales apply to c4")
@@ -206,6 +259,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
 
     slots = torch.tensor(w.slots, device=dev)
     lens = torch.tensor(w.seq_lens, device=dev)
+    offsets = None
     if table_fmt == "ragged":
         indices, indptr = W.ragged_table(w)
         table = paged.RaggedTable(torch.tensor(indices, device=dev),
@@ -266,6 +320,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         return Launch("gather", lib.kvx_launch_gather_kv, (C.byref(cd), C.byref(gd)),
                       gbytes, gtok)
 
+    extra = {}
     if name in ("c1", "c2", "c4"):
         layers = layers_override or w.layers
         out_dt = tdt[w.io_dtype]
@@ -283,6 +338,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
             top = 57344.0 if fp8 == "e5m2" else 448.0
             ks = (cal_k.abs().max() / top).reshape(1).float()
             vs = (cal_v.abs().max() / top).reshape(1).float()
+            extra["scales"] = (float(ks.item()), float(vs.item()))
             if scales != "tensor":
                 # per-head amax / top, and (block kinds) a seeded per-block factor
                 gs = torch.Generator(device=dev).manual_seed(w.notes["calibration_seed"] + 1)
@@ -310,10 +366,18 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         cfg = {"layers": layers}
     elif name == "c3":
         # four rotating buffer sets (> the 256 MB Infinity Cache)
+        gathers = []
         for _ in range(4):
             pc, _ = cache_for(w)
-            steps.append([write_launch(pc, rows(w), rows(w))])
-        cfg = {"buffer_sets": 4}
+            key, val = rows(w), rows(w)
+            steps.append([write_launch(pc, key, val)])
+            if c3_gathers:
+                # the PACKED gather of the same table back into this set's
+                # io buffers, [S, 2048, H, D]: it returns the rows just written
+                shape = (w.seq_count, w.max_seq_len, w.heads, w.head_dim)
+                gathers.append(gather_launch(pc, key.view(shape), val.view(shape)))
+        extra["gathers"] = gathers
+        cfg = {"buffer_sets": 4, "block_order": c3_order}
     else:  # c5
         pc, gc = cache_for(w)
         ko = torch.empty((w.seq_count, w.max_seq_len, w.heads, w.head_dim),
@@ -321,7 +385,7 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
         vo = torch.empty_like(ko)
         keep += [ko, vo]
         steps.append([write_launch(pc, rows(w), rows(w)), gather_launch(gc, ko, vo)])
-        cfg = {"layers": 1}
+        cfg = {"layers": 1, "pool_bytes": 2 * pc.key_cache.numel() * pc.key_cache.element_size()}
     torch.cuda.synchronize()
     if table_fmt != "packed":
         w.name = f"{w.name}_{table_fmt}"
@@ -334,28 +398,213 @@ def build_config(name: str, layers_override, dev, table_fmt="packed", write_entr
                 "max_seq_len": w.max_seq_len, "pool_blocks": w.num_blocks,
                 "cache_dtype": w.cache_dtype.name, "io_dtype": w.io_dtype.name,
                 "k_layout": w.k_layout.name, "v_layout": w.v_layout.name})
-    return w, steps, cfg, keep
+    return Built(w, steps, cfg, keep, extra)
+
+
+# ---------------------------------------------------------------------------
+# Timing.
+
+def time_launches(steps, K, W, stream):
+    """W untimed warmup steps, then K steps with HIP events around every
+    launch and around the whole region.  Returns (total ms, [(ms, launch)],
+    wall seconds)."""
+    import torch
+
+    sh = stream.cuda_stream
+    for i in range(W):
+        for launch in steps[i % len(steps)]:
+            launch(sh)
+    torch.cuda.synchronize()
+    per_step = [steps[i % len(steps)] for i in range(K)]
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(sum(len(s) for s in per_step))]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    k = 0
+    order = []
+    for s in per_step:
+        for launch in s:
+            e0, e1 = evs[k]
+            e0.record(stream)
+            launch(sh)
+            e1.record(stream)
+            order.append(launch)
+            k += 1
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    return (t_start.elapsed_time(t_end),
+            [(e0.elapsed_time(e1), l) for (e0, e1), l in zip(evs, order)], wall)
+
+
+def summarize(ms_total, timed, K):
+    """Whole-step and per-kernel figures of one timed region."""
+    ms_per_step = ms_total / K
+    by_kind = {}
+    for ms, launch in timed:
+        by_kind.setdefault(launch.kind, []).append((ms, launch))
+    step_bytes = sum(l.nbytes for _, l in timed) / K
+    step_tokens = {}
+    for _, l in timed:
+        step_tokens[l.kind] = step_tokens.get(l.kind, 0) + l.tokens / K
+    value = step_bytes / (ms_per_step / 1e3) / 1e9
+    kernels = {}
+    for kind, lst in by_kind.items():
+        ms = [x for x, _ in lst]
+        mean_ms = statistics.fmean(ms)
+        med_ms = statistics.median(ms)
+        nbytes = lst[0][1].nbytes
+        gbps = nbytes / (mean_ms / 1e3) / 1e9
+        kernels[kind] = {
+            "launches": len(ms), "mean_ms": round(mean_ms, 5),
+            "median_ms": round(med_ms, 5),
+            "bytes_per_launch": nbytes,
+            "GBps": round(gbps, 1),
+            "GBps_median": round(nbytes / (med_ms / 1e3) / 1e9, 1),
+            "frac": round(gbps / PEAK_HBM_GBS, 4),
+            "tokens_per_s": round(lst[0][1].tokens / (mean_ms / 1e3), 1),
+        }
+    dom = max(kernels, key=lambda k_: kernels[k_]["mean_ms"] * kernels[k_]["launches"])
+    return {"ms_per_step": round(ms_per_step, 4), "value": round(value, 1),
+            "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
+            "tokens_per_s": {k_: round(v / (ms_per_step / 1e3), 1)
+                             for k_, v in step_tokens.items()},
+            "kernels": kernels, "dominant": dom}
+
+
+# ---------------------------------------------------------------------------
+# Streaming ceilings (libkvx_amd_probe.so).
+
+class Probe:
+    """Plain copy / read / write kernels over byte counts beyond the
+    Infinity Cache: the best stream of this box, beside the KV kernels."""
+
+    OPS = ("copy", "read", "write")
+
+    def __init__(self):
+        from kvx_amd import build as kbuild
+
+        if not kbuild.PROBE_LIB.exists():
+            raise RuntimeError(f"{kbuild.PROBE_LIB} is not built (python -m kvx_amd.build)")
+        L = C.CDLL(str(kbuild.PROBE_LIB))
+        vp, i64, i = C.c_void_p, C.c_int64, C.c_int
+        L.kvx_probe_copy.argtypes = [vp, vp, i64, i, vp]
+        L.kvx_probe_read.argtypes = [vp, i64, vp, i, vp]
+        L.kvx_probe_write.argtypes = [vp, i64, C.c_uint32, i, vp]
+        L.kvx_probe_shape.argtypes = [i, C.POINTER(i), C.POINTER(i)]
+        self.L = L
+        self.shapes = []
+        for k in range(L.kvx_probe_shapes()):
+            t, u = C.c_int(), C.c_int()
+            L.kvx_probe_shape(k, C.byref(t), C.byref(u))
+            self.shapes.append((t.value, u.value))
+
+    def ceiling(self, nbytes, stream, reps=4, rotate_bytes=1 << 30):
+        """Per op: {bytes moved per launch, GB/s of the fastest shape, that
+        shape (threads, chunks per lane), mean us}.  Copy moves 2 * nbytes
+        (read + write); read and write move nbytes.  Launches rotate over
+        buffer pairs covering at least `rotate_bytes` per side, so that each
+        one's data has left L2 and the Infinity Cache before it is reused;
+        every pair runs at least `reps` times per (op, shape)."""
+        import torch
+
+        nbytes = max(16, nbytes // 16 * 16)
+        pairs = max(1, min(1024, -(-rotate_bytes // nbytes)))
+        cycles = max(1, -(-reps // pairs))
+        src_all = torch.empty(pairs * nbytes, dtype=torch.uint8, device="cuda").fill_(3)
+        dst_all = torch.empty(pairs * nbytes, dtype=torch.uint8, device="cuda")
+        bufs = [(dst_all[i * nbytes:(i + 1) * nbytes], src_all[i * nbytes:(i + 1) * nbytes])
+                for i in range(pairs)]
+        sink = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+        sh = stream.cuda_stream
+        out = {}
+        for op in self.OPS:
+            best = None
+            for k, shape in enumerate(self.shapes):
+                def one(d, s):
+                    if op == "copy":
+                        return self.L.kvx_probe_copy(d.data_ptr(), s.data_ptr(), nbytes, k, sh)
+                    if op == "read":
+                        return self.L.kvx_probe_read(s.data_ptr(), nbytes, sink.data_ptr(), k,
+                                                     sh)
+                    return self.L.kvx_probe_write(d.data_ptr(), nbytes, 7, k, sh)
+
+                for d, s in bufs:
+                    if one(d, s) != 0:
+                        raise RuntimeError(f"probe {op} shape {shape} failed")
+                evs = []
+                for _ in range(cycles):
+                    for d, s in bufs:
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record(stream)
+                        one(d, s)
+                        e1.record(stream)
+                        evs.append((e0, e1))
+                torch.cuda.synchronize()
+                ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
+                moved = 2 * nbytes if op == "copy" else nbytes
+                gbps = moved / (ms / 1e3) / 1e9
+                if best is None or gbps > best["GBps"]:
+                    best = {"bytes_per_launch": moved, "GBps": round(gbps, 1),
+                            "frac": round(gbps / PEAK_HBM_GBS, 4),
+                            "shape": list(shape), "mean_us": round(ms * 1e3, 2)}
+            out[op] = best
+        out["buffers"] = pairs
+        out["footprint_bytes"] = 2 * pairs * nbytes
+        del bufs, sink, src_all, dst_all
+        torch.cuda.empty_cache()
+        return out
 
 
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle's fast path on a bounded sample.
 
-def cpu_baseline(w, seconds: float):
+def cpu_model() -> str:
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
+    except OSError:
+        return "unknown"
+    name = info.get("model name", "unknown")
+    extra = [f"family {info.get('cpu family', '?')} model {info.get('model', '?')} "
+             f"stepping {info.get('stepping', '?')}"]
+    if "hypervisor" in info.get("flags", "").split():
+        extra.append("virtual machine")
+    return f"{name} ({', '.join(extra)})"
+
+
+def cpu_baseline(w, seconds: float, sample_seqs: int, gather: bool = True,
+                 scales=(0.01, 0.01), table_fmt="packed"):
+    """The oracle's fast write (+ gather) over the first `sample_seqs`
+    sequences of `w` on a compacted pool (the blocks they use, renumbered),
+    timed for about `seconds`; GB/s of the same algorithmic bytes as the GPU
+    figures.  FP8 caches use the quantizing / dequantizing fast paths with
+    per-tensor scales."""
     import numpy as np
 
     import oracle
     from kvx_amd import workloads as W
-    from kvx_amd.abi import Layout
+    from kvx_amd.abi import DType, Layout, contiguous_strides
+    from kvx_amd.paged import cache_shape
 
-    n_s = min(w.seq_count, 64)
+    if Layout.BLOCK_CUSTOM in (w.k_layout, w.v_layout):
+        return None  # the sample below builds the canonical layouts only
+    n_s = min(w.seq_count, sample_seqs)
     table = w.block_table[:n_s].astype(np.int64)
-    used = np.unique(table[table >= 0])
+    ok = (table >= 0) & (table < w.num_blocks)
+    used = np.unique(table[ok])
     remap = np.full(int(w.num_blocks), -1, np.int64)
     remap[used] = np.arange(used.size)
-    sub_table = np.where(table >= 0, remap[np.maximum(table, 0)], -1)
+    sub_table = np.where(ok, remap[np.where(ok, table, 0)], -1)
     slots = w.slots.astype(np.int64)
     bs = w.block_size
-    # tokens whose slot lands in a sampled sequence's blocks
     blk = np.where(slots >= 0, slots // bs, -1)
     keep_tok = (blk >= 0) & np.isin(blk, used)
     sub_slots = np.where(keep_tok, remap[np.maximum(blk, 0)] * bs + slots % bs, -1)
@@ -364,22 +613,31 @@ def cpu_baseline(w, seconds: float):
                      w.cache_dtype, w.io_dtype, w.k_layout, w.v_layout, w.pack,
                      sub_slots, w.tokens_per_seq, sub_table.astype(w.block_table.dtype),
                      w.seq_lens[:n_s].copy(), w.max_seq_len)
-    es = W.dtype_bytes(w.cache_dtype)
-    if W.dtype_bytes(w.io_dtype) != es:
-        return None  # the CPU fast path is a byte copy; no dequant baseline
-    if Layout.BLOCK_CUSTOM in (w.k_layout, w.v_layout):
-        return None  # the sample below builds canonical layouts only
+    cs, is_ = W.dtype_bytes(w.cache_dtype), W.dtype_bytes(w.io_dtype)
+    fp8 = w.cache_dtype in (DType.F8_E4M3, DType.F8_E5M2)
+    if not fp8 and cs != is_:
+        return None
     rng = np.random.default_rng(0)
     E = w.heads * w.head_dim
     blk_elems = bs * E
-    kc = rng.integers(0, 255, size=used.size * blk_elems * es, dtype=np.uint8)
-    vc = rng.integers(0, 255, size=used.size * blk_elems * es, dtype=np.uint8)
-    key = rng.integers(0, 255, size=sub_slots.size * E * es, dtype=np.uint8)
-    val = rng.integers(0, 255, size=sub_slots.size * E * es, dtype=np.uint8)
-    ko = np.zeros(n_s * w.max_seq_len * E * es, np.uint8)
+    kc = rng.integers(0, 255, size=used.size * blk_elems * cs, dtype=np.uint8)
+    vc = rng.integers(0, 255, size=used.size * blk_elems * cs, dtype=np.uint8)
+    if fp8:
+        # N(0, 1) rows in the io dtype (the quantizing write reads numbers)
+        def normal_rows():
+            x = rng.standard_normal(sub_slots.size * E).astype(np.float32)
+            if w.io_dtype == DType.BF16:
+                x = (x.view(np.uint32) >> 16).astype(np.uint16)
+            elif w.io_dtype == DType.F16:
+                x = x.astype(np.float16)
+            return x.view(np.uint8)
+
+        key, val = normal_rows(), normal_rows()
+    else:
+        key = rng.integers(0, 255, size=sub_slots.size * E * is_, dtype=np.uint8)
+        val = rng.integers(0, 255, size=sub_slots.size * E * is_, dtype=np.uint8)
+    ko = np.zeros(n_s * w.max_seq_len * E * is_ if gather else 0, np.uint8)
     vo = np.zeros_like(ko)
-    from kvx_amd.paged import cache_shape
-    from kvx_amd.abi import contiguous_strides
 
     def geom(layout):
         st = contiguous_strides(cache_shape(layout, used.size, bs, w.heads, w.head_dim,
@@ -389,17 +647,27 @@ def cpu_baseline(w, seconds: float):
     gk, gv = geom(w.k_layout), geom(w.v_layout)
     lens = sub.seq_lens
     tbl = sub.block_table
+    common = dict(heads=w.heads, head_dim=w.head_dim, block_size=bs,
+                  num_blocks=int(used.size))
+    gcommon = dict(common, seq_count=n_s, max_blocks_per_seq=w.max_blocks_per_seq,
+                   max_seq_len=w.max_seq_len)
 
     def once():
         t0 = time.perf_counter()
-        th = oracle.write_kv_fast(gk, gv, key, val, kc, vc, sub_slots, heads=w.heads,
-                                  head_dim=w.head_dim, block_size=bs,
-                                  num_blocks=int(used.size), elem_size=es)
-        oracle.gather_kv_fast(gk, gv, kc, vc, ko, vo, tbl, lens, seq_count=n_s,
-                              max_blocks_per_seq=w.max_blocks_per_seq,
-                              max_seq_len=w.max_seq_len, heads=w.heads,
-                              head_dim=w.head_dim, block_size=bs,
-                              num_blocks=int(used.size), elem_size=es)
+        if fp8:
+            th = oracle.write_kv_quant_fast(gk, gv, key, val, kc, vc, sub_slots,
+                                            io_dtype=w.io_dtype, cache_dtype=w.cache_dtype,
+                                            k_scale=scales[0], v_scale=scales[1], **common)
+            if gather:
+                oracle.gather_kv_dequant_fast(gk, gv, kc, vc, ko, vo, tbl, lens,
+                                              cache_dtype=w.cache_dtype, io_dtype=w.io_dtype,
+                                              k_scale=scales[0], v_scale=scales[1], **gcommon)
+        else:
+            th = oracle.write_kv_fast(gk, gv, key, val, kc, vc, sub_slots, elem_size=cs,
+                                      **common)
+            if gather:
+                oracle.gather_kv_fast(gk, gv, kc, vc, ko, vo, tbl, lens, elem_size=cs,
+                                      **gcommon)
         return time.perf_counter() - t0, th
 
     once()  # touch every page first
@@ -411,107 +679,190 @@ def cpu_baseline(w, seconds: float):
         if len(times) >= 200:
             break
     med = statistics.median(times)
-    nbytes = W.write_bytes(sub) + W.gather_bytes(sub)
-    # the same sample on one thread, three runs
+    nbytes = W.write_bytes(sub) + (W.gather_bytes(sub) if gather else 0)
+    tokens = sub.valid_write_tokens() + (sub.gathered_tokens() if gather else 0)
     prev = oracle.set_threads(1)
     try:
         one = statistics.median(once()[0] for _ in range(3))
     finally:
         oracle.set_threads(prev)
+    what = "write+gather" if gather else "write"
+    cast = "; FP8 casts by table lookup" if fp8 else ""
+    sample = (f"{w.name} one layer: {'all' if n_s == w.seq_count else f'first {n_s} of'} "
+              f"{w.seq_count} sequences (write {sub.valid_write_tokens()} tokens"
+              + (f", gather {sub.gathered_tokens()} tokens" if gather else "")
+              + f") on a compacted pool of {used.size} blocks; oracle row-memcpy {what}"
+              f"{cast}, OpenMP; median of {len(times)} runs")
+    if table_fmt != "packed":
+        sample += ("; the oracle's fast path reads the PACKED form of this workload's table "
+                   "(same rows and bytes)")
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": int(threads),
             "single_thread": {"value": round(nbytes / one / 1e9, 3), "unit": "GB/s",
                               "cores": 1, "seconds_per_run": round(one, 4)},
             "cpu_model": cpu_model(), "nproc": os.cpu_count(),
-            "kind": "port",
-            "sample": (f"{w.name} one layer: first {n_s} of {w.seq_count} sequences "
-                       f"(gather {sub.gathered_tokens()} tokens, write "
-                       f"{sub.valid_write_tokens()} tokens) on a compacted pool of "
-                       f"{used.size} blocks; oracle row-memcpy write+gather, OpenMP; "
-                       f"median of {len(times)} runs"),
-            "tokens_per_s": round((sub.gathered_tokens() + sub.valid_write_tokens()) / med, 1),
+            "binding": {k: os.environ.get(k) for k in ("OMP_PROC_BIND", "OMP_PLACES")},
+            "kind": "port", "sample": sample,
+            "tokens_per_s": round(tokens / med, 1),
             "seconds_per_run": round(med, 4)}
 
 
-def cpu_model() -> str:
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+# ---------------------------------------------------------------------------
+# Extras of the headline.
 
-
-def copy_reference(stream, nbytes: int = 1 << 30, reps: int = 5):
-    """torch's device-to-device copy_ of `nbytes` on `stream` (read plus
-    write bytes per second): a plain copy beside the roofline, for the same
-    box and run."""
-    import torch
-
-    a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(7)
-    b = torch.empty_like(a)
-    with torch.cuda.stream(stream):
-        for _ in range(2):
-            b.copy_(a)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(reps)]
-        for e0, e1 in ev:
-            e0.record(stream)
-            b.copy_(a)
-            e1.record(stream)
-    torch.cuda.synchronize()
-    ms = statistics.fmean(e0.elapsed_time(e1) for e0, e1 in ev)
-    del a, b
-    torch.cuda.empty_cache()
-    return {"kernel": "torch copy_ device to device", "bytes_per_copy": 2 * nbytes,
-            "GBps": round(2 * nbytes / (ms / 1e3) / 1e9, 1), "reps": reps}
-
-
-def write_graph(steps, stream, reps: int = 10, min_launches: int = 32):
-    """The workload's cache writes replayed from a HIP graph: every write
-    launch of every step, repeated to at least `min_launches` launches, is
-    captured once on the bench stream, so the per-call host cost of the
-    launch path (descriptor checks, planning, the launch itself) is paid at
-    capture only, as under vLLM's graph-mode decode.  `reps` replays are
-    queued back to back between two events, so the device never waits for
-    the host; reports the mean device time per write."""
+def write_graph(steps, stream, flush_bytes: int = 1 << 30, reps: int = 10):
+    """The workload's cache writes replayed from one HIP graph: every write
+    launch of the steps, captured once on the bench stream, so the per-call
+    host cost of the launch path is paid at capture only (as under vLLM's
+    graph-mode decode).  Before each replay a read of `flush_bytes` (outside
+    the timed events) evicts the inputs and the cache rows from L2 and the
+    Infinity Cache, so the time per write is that of HBM-resident data."""
     import torch
 
     writes = [l for s in steps for l in s if l.kind == "write"]
     if not writes:
         return None
-    rounds = -(-min_launches // len(writes))
+    probe = Probe()
+    flush = torch.empty(flush_bytes, dtype=torch.uint8, device="cuda").fill_(1)
+    sink = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+    sh = stream.cuda_stream
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
-        for _ in range(rounds):
-            for l in writes:
-                l(stream.cuda_stream)
+        for l in writes:
+            l(sh)
     for _ in range(2):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+    evs = []
     for _ in range(reps):
+        if probe.L.kvx_probe_read(flush.data_ptr(), flush_bytes, sink.data_ptr(), 2, sh) != 0:
+            raise RuntimeError("flush read failed")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
         g.replay()
-    e1.record(stream)
+        e1.record(stream)
+        evs.append((e0, e1))
     torch.cuda.synchronize()
-    n = reps * rounds * len(writes)
-    ms = e0.elapsed_time(e1) / n
-    del g
-    return {"launches_per_graph": rounds * len(writes), "replays": reps,
+    ms = statistics.fmean(a.elapsed_time(b) for a, b in evs) / len(writes)
+    del g, flush, sink
+    torch.cuda.empty_cache()
+    return {"launches_per_graph": len(writes), "replays": reps,
+            "caches": f"flushed before each replay ({flush_bytes >> 20} MiB read)",
             "us_per_write": round(ms * 1e3, 3),
             "GBps": round(writes[0].nbytes / (ms / 1e3) / 1e9, 1)}
 
 
-def load_traffic(kernel: str, workload: str):
-    """HBM bytes per launch from the committed rocprofv3 counter summary."""
-    p = REPO / "profiles" / f"traffic_{kernel}_{workload}.json"
+def kernel_sources_digest() -> str:
+    """sha256 over the kernel sources (the device code and the launch
+    planning): a counter summary taken of other sources is stale."""
+    from kvx_amd import build as kbuild
+
+    h = hashlib.sha256()
+    for name in sorted(["kernels.h", "fp_convert.h", "kvx_internal.h"] +
+                       [s for s in kbuild.SOURCES if s.endswith(".hip")]):
+        h.update(name.encode())
+        h.update((kbuild.CSRC / name).read_bytes())
+    return h.hexdigest()
+
+
+def load_traffic(kind: str, workload: str, algo_bytes: int):
+    """HBM bytes per launch from the committed rocprofv3 counter summary of
+    this kernel kind and workload, with its file name, or (None, reason)
+    when there is none or it was taken of other bytes or other sources."""
+    rel = f"profiles/traffic_{kind}_{workload}.json"
+    p = REPO / rel
     if not p.exists():
-        return None
+        return None, f"{rel}: none"
     try:
-        return json.loads(p.read_text()).get("bytes_per_launch")
+        d = json.loads(p.read_text())
     except (OSError, ValueError):
-        return None
+        return None, f"{rel}: unreadable"
+    if d.get("algorithmic_bytes") != algo_bytes:
+        return None, f"{rel}: taken of {d.get('algorithmic_bytes')} algorithmic bytes"
+    if d.get("kernel_sources_sha256") != kernel_sources_digest():
+        return None, f"{rel}: taken of other kernel sources"
+    return d.get("bytes_per_launch"), rel
+
+
+def roofline_of(summary, workload):
+    k = summary["kernels"][summary["dominant"]]
+    traffic, src = load_traffic(summary["dominant"], workload, k["bytes_per_launch"])
+    return {"bound": "hbm", "achieved": k["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": k["frac"], "traffic": traffic, "traffic_source": src,
+            "kernel": summary["dominant"],
+            "algorithmic_bytes_per_launch": k["bytes_per_launch"],
+            "frac_median": round(k["GBps_median"] / PEAK_HBM_GBS, 4)}
+
+
+def run_config(name, dev, stream, K, W, args, cpu: bool, **kw):
+    """Build, time and summarise one configuration, then free it."""
+    import torch
+
+    b = build_config(name, dev, **kw)
+    ms_total, timed, wall = time_launches(b.steps, K, W, stream)
+    res = summarize(ms_total, timed, K)
+    res["roofline"] = roofline_of(res, b.w.name)
+    res["config"] = b.cfg
+    res["steps"], res["warmup"] = K, W
+    res["dtype"] = {"F8_E4M3": "fp8_e4m3", "F8_E5M2": "fp8_e5m2"}.get(
+        b.w.cache_dtype.name, b.w.io_dtype.name.lower())
+    res["wall_s_timed"] = round(wall, 3)
+    extras = {}
+    if not args.profile_only:
+        dom = res["kernels"][res["dominant"]]
+        extras["stream_ceiling"] = Probe().ceiling(dom["bytes_per_launch"] // 2, stream)
+    w, steps = b.w, b.steps
+    scales = b.extra.get("scales", (0.01, 0.01))
+    del b
+    torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, CPU_SAMPLE_SEQS[name],
+                                           gather=name != "c3", scales=scales,
+                                           table_fmt=kw.get("table_fmt", "packed"))
+    res.update(extras)
+    return res
+
+
+def sweep_c3(args, dev, stream):
+    """c3's write, the PACKED gather of the same table, and a plain copy of
+    the same bytes, at several multiples of c3's size; least-squares fit of
+    mean time = intercept + bytes / slope for each."""
+    import numpy as np
+    import torch
+
+    probe = Probe()
+    rows = []
+    for n in (int(x) for x in args.sweep_scales.split(",")):
+        b = build_config("c3", dev, c3_seqs=16 * n, c3_order=args.c3_order, c3_gathers=True)
+        reps = max(8, 64 // n)
+        _, tw, _ = time_launches(b.steps, 4 * reps, 4, stream)
+        gsteps = [[g] for g in b.extra["gathers"]]
+        _, tg, _ = time_launches(gsteps, 4 * reps, 4, stream)
+        wbytes, gbytes = b.steps[0][0].nbytes, gsteps[0][0].nbytes
+        del b, gsteps
+        torch.cuda.empty_cache()
+        cp = probe.ceiling(wbytes // 2, stream, reps=max(2, reps // 2))
+        wms = [x for x, _ in tw]
+        gms = [x for x, _ in tg]
+        rows.append({"scale": n, "tokens": 32768 * n,
+                     "write": {"bytes": wbytes, "mean_us": round(statistics.fmean(wms) * 1e3, 2),
+                               "median_us": round(statistics.median(wms) * 1e3, 2)},
+                     "gather": {"bytes": gbytes,
+                                "mean_us": round(statistics.fmean(gms) * 1e3, 2),
+                                "median_us": round(statistics.median(gms) * 1e3, 2)},
+                     "copy": {"bytes": cp["copy"]["bytes_per_launch"],
+                              "mean_us": cp["copy"]["mean_us"], "shape": cp["copy"]["shape"]}})
+        print(json.dumps(rows[-1]), flush=True)
+    fits = {}
+    for kind in ("write", "gather", "copy"):
+        x = np.array([r[kind]["bytes"] for r in rows], float)
+        y = np.array([r[kind]["mean_us"] for r in rows], float)
+        if len(rows) >= 2:
+            slope_us_per_byte, icpt = np.polyfit(x, y, 1)
+            fits[kind] = {"slope_GBps": round(1e-3 / slope_us_per_byte, 1),
+                          "slope_frac": round(1e-3 / slope_us_per_byte / PEAK_HBM_GBS, 4),
+                          "intercept_us": round(float(icpt), 2)}
+    print(json.dumps({"sweep": "c3", "block_order": args.c3_order, "rows": rows,
+                      "fit": fits}), flush=True)
 
 
 def main():
@@ -530,97 +881,63 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
-    w, steps, cfg, keep = build_config(args.config, args.layers, dev, args.table,
-                                       args.write_entry, args.fp8, args.scales, args.layout,
-                                       args.heads)
     stream = torch.cuda.Stream(device=dev)
-    sh = stream.cuda_stream
     torch.cuda.set_stream(stream)  # launches that use torch's current stream
 
-    for i in range(args.warmup):
-        for launch in steps[i % len(steps)]:
-            launch(sh)
-    torch.cuda.synchronize()
+    if args.sweep:
+        sweep_c3(args, dev, stream)
+        return
 
-    K = args.steps
-    per_step = [steps[i % len(steps)] for i in range(K)]
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(sum(len(s) for s in per_step))]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_start.record(stream)
-    k = 0
-    kinds = []
-    for s in per_step:
-        for launch in s:
-            e0, e1 = evs[k]
-            e0.record(stream)
-            launch(sh)
-            e1.record(stream)
-            kinds.append(launch)
-            k += 1
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_total = t_start.elapsed_time(t_end)
-    ms_per_step = ms_total / K
+    head = args.config or "c2"
+    kw = dict(layers_override=args.layers, table_fmt=args.table,
+              write_entry=args.write_entry, fp8=args.fp8, scales=args.scales,
+              layout=args.layout, heads=args.heads, c3_seqs=args.c3_seqs,
+              c3_order=args.c3_order)
+    K, W = args.steps, args.warmup
+    cpu = not args.no_cpu_baseline and not args.profile_only
 
-    by_kind = {}
-    for (e0, e1), launch in zip(evs, kinds):
-        by_kind.setdefault(launch.kind, []).append((e0.elapsed_time(e1), launch))
-    step_bytes = sum(l.nbytes for s in per_step for l in s) / K
-    step_tokens = {}
-    for s in per_step:
-        for l in s:
-            step_tokens[l.kind] = step_tokens.get(l.kind, 0) + l.tokens / K
-    value = step_bytes / (ms_per_step / 1e3) / 1e9
+    b = build_config(head, dev, **kw)
+    ms_total, timed, wall = time_launches(b.steps, K, W, stream)
+    res = summarize(ms_total, timed, K)
+    roofline = roofline_of(res, b.w.name)
+    ceiling = graph = None
+    if not args.profile_only:
+        dom = res["kernels"][res["dominant"]]
+        ceiling = Probe().ceiling(dom["bytes_per_launch"] // 2, stream)
+        graph = write_graph(b.steps, stream)
+    w, cfg = b.w, b.cfg
+    scales = b.extra.get("scales", (0.01, 0.01))
+    del b
+    torch.cuda.empty_cache()
 
-    kernels = {}
-    for kind, lst in by_kind.items():
-        ms = [x for x, _ in lst]
-        mean_ms = statistics.fmean(ms)
-        nbytes = lst[0][1].nbytes
-        kernels[kind] = {
-            "launches": len(ms), "mean_ms": round(mean_ms, 5),
-            "median_ms": round(statistics.median(ms), 5),
-            "bytes_per_launch": nbytes,
-            "GBps": round(nbytes / (mean_ms / 1e3) / 1e9, 1),
-            "tokens_per_s": round(lst[0][1].tokens / (mean_ms / 1e3), 1),
-        }
-    dom = max(kernels, key=lambda k_: kernels[k_]["mean_ms"] * kernels[k_]["launches"])
-    achieved = kernels[dom]["GBps"]
-    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": load_traffic(dom, w.name), "kernel": dom,
-                "algorithmic_bytes_per_launch": kernels[dom]["bytes_per_launch"]}
+    configs = {}
+    if args.config is None:
+        for name in ("c1", "c3", "c4", "c5"):
+            ks = max(K, -(-MIN_LAUNCHES[name] // {"c1": 22, "c4": 32}.get(name, 1)))
+            configs[name] = run_config(name, dev, stream, ks, W, args, cpu)
+            print(f"config {name}: {configs[name]['kernels']}", file=sys.stderr, flush=True)
 
-    copy_ref = None if args.profile_only else copy_reference(stream)
-    graph = None if args.profile_only else write_graph(steps, stream)
-    cpu = None
-    if not args.no_cpu_baseline and not args.profile_only:
-        cpu = cpu_baseline(w, args.cpu_seconds)
-        if cpu is not None and args.table != "packed":
-            cpu["sample"] += ("; the oracle's fast path reads the PACKED form of this "
-                              "workload's table (same rows and bytes)")
+    cpu_res = None
+    if cpu:
+        cpu_res = cpu_baseline(w, args.cpu_seconds, CPU_SAMPLE_SEQS[head],
+                               gather=head != "c3", scales=scales, table_fmt=args.table)
 
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "metric": METRIC, "value": res["value"], "unit": "GB/s", "n_gpus": 1,
+        "steps": K, "warmup": W, "ms_per_step": res["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"F8_E4M3": "fp8_e4m3", "F8_E5M2": "fp8_e5m2"}.get(
             w.cache_dtype.name, w.io_dtype.name.lower()),
         "data": "synthetic",
         "config": cfg,
-        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
-        "tokens_per_s": {k_: round(v / (ms_per_step / 1e3), 1)
-                         for k_, v in step_tokens.items()},
-        "kernels": kernels,
+        "pct_of_peak": res["pct_of_peak"],
+        "tokens_per_s": res["tokens_per_s"],
+        "kernels": res["kernels"],
         "roofline": roofline,
-        "copy_reference": copy_ref,
+        "stream_ceiling": ceiling,
         "write_graph": graph,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_res,
+        "configs": configs,
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(out), flush=True)

@@ -102,6 +102,20 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+PROBE_SRC = CSRC / "stream_probe.hip"
+PROBE_LIB = PKG_DIR / "libkvx_amd_probe.so"
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """Compile the streaming-probe library (plain copy / read / write
+    kernels that bench.py times beside the KV kernels)."""
+    cc = hipcc()
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([cc, *COMMON_FLAGS, "-shared", "-x", "hip", str(PROBE_SRC), "-o", str(tmp)], verbose)
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 BENCH_SRC = CSRC / "kvx_bench.cpp"
 BENCH_BIN = PKG_DIR / "kvx_bench"
 
@@ -149,4 +163,5 @@ def build_torch_ops(verbose: bool = False) -> Path:
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
     print(build_bench(verbose="-v" in sys.argv))
+    print(build_probe(verbose="-v" in sys.argv))
     print(build_torch_ops(verbose="-v" in sys.argv))

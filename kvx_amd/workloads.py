@@ -203,14 +203,32 @@ def c2_llama8b_decode(seed: int = 2, batch: int = 256) -> Workload:
                     notes={"padded_slots": int(pad.size)})
 
 
-def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD) -> Workload:
+def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs: int = 16,
+                       order: str = "random") -> Workload:
+    """c3; `seqs` chunks of 2048 tokens over a pool of 512 blocks per
+    sequence (16 and 8192 as configured).  order "random": each sequence's
+    blocks are a seeded random draw from the pool; "ascending": sequence s
+    takes blocks s * 128 .. s * 128 + 127 in order, as a fresh allocator
+    would hand them out."""
     rng = np.random.Generator(np.random.PCG64(seed))
-    S, chunk, bs, pool = 16, 2048, 16, 8192
+    S, chunk, bs = seqs, 2048, 16
+    pool = 512 * S
     mbps = chunk // bs
-    table = rng.permutation(pool)[: S * mbps].reshape(S, mbps).astype(np.int32)
+    if order == "random":
+        ids = rng.permutation(pool)[: S * mbps]
+    elif order == "ascending":
+        ids = np.arange(S * mbps)
+    else:
+        raise ValueError(order)
+    table = ids.reshape(S, mbps).astype(np.int32)
     pos = np.arange(chunk)
     slots = np.concatenate([_slots_for(pos, table[s], bs) for s in range(S)])
-    return Workload("c3_llama3_8b_prefill_packedK_bf16", seed, 8, 128, bs, pool,
+    name = "c3_llama3_8b_prefill_packedK_bf16"
+    if S != 16:
+        name += f"_s{S}"
+    if order != "random":
+        name += f"_{order}"
+    return Workload(name, seed, 8, 128, bs, pool,
                     DType.BF16, DType.BF16, Layout.BLOCK_HND_PACKED, Layout(v_layout), 8,
                     slots.astype(np.int64), chunk, table, np.full(S, chunk, np.int32),
                     chunk)

@@ -46,7 +46,7 @@ def _run(cmd: list[str]) -> None:
 def build_oracle() -> Path:
     BUILD.mkdir(exist_ok=True)
     tmp = ORACLE_LIB.with_suffix(".so.tmp")
-    _run(["gcc", "-std=c11", "-O2", "-fopenmp", "-fPIC", "-shared", "-Wall",
+    _run(["gcc", "-std=c11", "-O3", "-fopenmp", "-fPIC", "-shared", "-Wall",
           "-o", str(tmp), str(HERE / "kvx_oracle.c"), "-lm"])
     os.replace(tmp, ORACLE_LIB)
     return ORACLE_LIB

@@ -578,13 +578,13 @@ int oracle_gather_kv_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
 /* lies in [bf16(u), next bf16) with no boundary strictly inside: its code is */
 /* that of bf16(u) itself when its lower 16 bits are 0 (ties included), and   */
 /* that of any value just above bf16(u) otherwise.  Two 65536-entry tables    */
-/* per format, filled with the element-wise casts, give every f32's code.     */
-/* Dequantize: a 256-entry table of code values, one f32 product, and the     */
-/* round-to-nearest-even narrowing to bf16 (f16 and f32 outputs use the       */
-/* element-wise store).                                                       */
+/* per format, filled once with the element-wise casts, give every f32's      */
+/* code; the quotient x / scale is one IEEE f32 division as in quant_one.     */
+/* Dequantize: with a per-tensor scale the output depends on the code alone,  */
+/* so each call fills a 256-entry table of io values with dequant_one and     */
+/* maps every code through it.                                                */
 
 static uint8_t fq_lo[2][65536], fq_hi[2][65536];
-static float fdq[2][256];
 static int ftables_ready;
 
 static void fast_tables(void) {
@@ -595,8 +595,6 @@ static void fast_tables(void) {
       fq_lo[f][u] = f ? oracle_f32_to_e5m2(lo) : oracle_f32_to_e4m3(lo);
       fq_hi[f][u] = f ? oracle_f32_to_e5m2(hi) : oracle_f32_to_e4m3(hi);
     }
-    for (int q = 0; q < 256; ++q)
-      fdq[f][q] = f ? oracle_e5m2_to_f32((uint8_t)q) : oracle_e4m3_to_f32((uint8_t)q);
   }
   ftables_ready = 1;
 }
@@ -604,12 +602,6 @@ static void fast_tables(void) {
 static inline uint8_t fast_to_fp8(float q, int e5) {
   const uint32_t u = bits_of(q);
   return (u & 0xFFFFu) ? fq_hi[e5][u >> 16] : fq_lo[e5][u >> 16];
-}
-
-static inline uint16_t fast_f32_to_bf16(float v) {
-  const uint32_t u = bits_of(v);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
 static inline float fast_load_io(const uint8_t *p, int dt) {
@@ -621,12 +613,22 @@ static inline float fast_load_io(const uint8_t *p, int dt) {
   return load_io_f32(p, dt);
 }
 
-static inline void fast_store_io(uint8_t *p, int dt, float v) {
-  if (dt == D_BF16) {
-    const uint16_t h = fast_f32_to_bf16(v);
-    memcpy(p, &h, 2);
+/* The io value of every code for one per-tensor scale. */
+typedef struct {
+  uint8_t v[256][4];
+} dq_table_t;
+
+static void dq_table(dq_table_t *t, int fp8_dtype, float scale, int io_dtype) {
+  for (int q = 0; q < 256; ++q) dequant_one((uint8_t)q, fp8_dtype, scale, io_dtype, t->v[q]);
+}
+
+/* n codes -> n io elements of `is` bytes. */
+static void dequant_run(const uint8_t *src, uint8_t *dst, int64_t n, const dq_table_t *t,
+                        int is) {
+  if (is == 2) {
+    for (int64_t j = 0; j < n; ++j) memcpy(dst + 2 * j, t->v[src[j]], 2);
   } else {
-    store_io_f32(p, dt, v);
+    for (int64_t j = 0; j < n; ++j) memcpy(dst + 4 * j, t->v[src[j]], 4);
   }
 }
 
@@ -640,10 +642,9 @@ void oracle_quantize_fp8_fast(const void *in, int io_dtype, int64_t n, float sca
 
 void oracle_dequantize_fp8_fast(const uint8_t *in, int64_t n, float scale, int fp8_dtype,
                                 int io_dtype, void *out) {
-  fast_tables();
-  const int es = dtype_size(io_dtype), e5 = fp8_dtype == D_E5M2;
-  for (int64_t i = 0; i < n; ++i)
-    fast_store_io((uint8_t *)out + i * es, io_dtype, fdq[e5][in[i]] * scale);
+  dq_table_t t;
+  dq_table(&t, fp8_dtype, scale, io_dtype);
+  dequant_run(in, out, n, &t, dtype_size(io_dtype));
 }
 
 int oracle_write_kv_quant_fast(int k_layout, const int64_t *k_stride, int64_t k_pack,
@@ -693,12 +694,13 @@ int oracle_gather_kv_dequant_fast(int k_layout, const int64_t *k_stride, int64_t
                                   int32_t heads, int32_t head_dim, int32_t block_size,
                                   int32_t num_blocks, int cache_dtype, int io_dtype,
                                   float k_scale, float v_scale) {
-  fast_tables();
   const int64_t kr = run_elems(k_layout, k_stride, k_pack, head_dim);
   const int64_t vr = run_elems(v_layout, v_stride, v_pack, head_dim);
   const int64_t nlb = ((int64_t)max_seq_len + block_size - 1) / block_size;
-  const int is = dtype_size(io_dtype), e5 = cache_dtype == D_E5M2;
-  const float *tab = fdq[e5];
+  const int is = dtype_size(io_dtype);
+  dq_table_t kt, vt;
+  dq_table(&kt, cache_dtype, k_scale, io_dtype);
+  dq_table(&vt, cache_dtype, v_scale, io_dtype);
   const uint8_t *kc = key_cache, *vc = value_cache;
   uint8_t *ko_ = key_out, *vo_ = value_out;
 #pragma omp parallel for schedule(dynamic, 16)
@@ -716,16 +718,12 @@ int oracle_gather_kv_dequant_fast(int k_layout, const int64_t *k_stride, int64_t
       const int64_t o = t - t0;
       for (int64_t h = 0; h < heads; ++h) {
         const int64_t row = ((s * max_seq_len + t) * heads + h) * head_dim;
-        for (int64_t d = 0; d < head_dim; d += kr) {
-          const uint8_t *src = kc + oracle_cache_offset(k_layout, k_stride, k_pack, bid, o, h, d);
-          for (int64_t j = 0; j < kr; ++j)
-            fast_store_io(ko_ + (row + d + j) * is, io_dtype, tab[src[j]] * k_scale);
-        }
-        for (int64_t d = 0; d < head_dim; d += vr) {
-          const uint8_t *src = vc + oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d);
-          for (int64_t j = 0; j < vr; ++j)
-            fast_store_io(vo_ + (row + d + j) * is, io_dtype, tab[src[j]] * v_scale);
-        }
+        for (int64_t d = 0; d < head_dim; d += kr)
+          dequant_run(kc + oracle_cache_offset(k_layout, k_stride, k_pack, bid, o, h, d),
+                      ko_ + (row + d) * is, kr, &kt, is);
+        for (int64_t d = 0; d < head_dim; d += vr)
+          dequant_run(vc + oracle_cache_offset(v_layout, v_stride, v_pack, bid, o, h, d),
+                      vo_ + (row + d) * is, vr, &vt, is);
       }
     }
   }

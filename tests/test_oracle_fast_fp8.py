@@ -1,13 +1,15 @@
 """Pins of the oracle's fast FP8 paths (the timed CPU baseline of FP8 caches)
 against the element-wise oracle — CPU only.
 
-The fast paths cast through tables built from the element-wise casts: a
+The fast paths cast through tables built from the element-wise casts.  A
 quantized code is looked up by the upper 16 bits of the f32 quotient and
 whether its lower 16 bits are zero, which is exact because every rounding
-boundary of E4M3 / E5M2 is a bf16 value.  These tests check that claim over
+boundary of E4M3 / E5M2 is a bf16 value; these tests check that claim over
 every bf16 and f16 input and over f32 inputs just above, at and below every
-bf16 value, for several scales, and check the fast write / gather against
-oracle.write_kv / oracle.gather_kv on random layouts, lengths and tables.
+bf16 value, for several scales.  A dequantized value is looked up in a
+per-call table of all 256 codes.  The fast write / gather are checked
+against oracle.write_kv / oracle.gather_kv on random layouts, lengths and
+tables.
 """
 import numpy as np
 import pytest
