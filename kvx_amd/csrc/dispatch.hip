@@ -64,6 +64,12 @@ int lpt_log2_for(int nchunks) {
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// HIP's limits on one grid dimension: at most 2^31 - 1 workgroups and
+// 2^32 - 1 work-items (gridDim.x * blockDim.x).
+bool grid_fits(int64_t workgroups, int threads) {
+  return workgroups <= 0x7FFFFFFF && workgroups * threads <= 0xFFFFFFFFll;
+}
+
 int log2_exact(int64_t v) {
   if (v <= 0 || (v & (v - 1)) != 0) return -1;
   int lg = 0;
@@ -174,7 +180,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   }
   *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
   *lds_bytes = (uint32_t)(bs * pitch);
-  return *grid <= 0x7FFFFFFF;
+  return grid_fits(*grid, kBlockThreads);
 }
 
 // Tiled block write plan (write_tiles_kernel): at least bs tokens,
@@ -241,7 +247,7 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   wt->io_es_log2 = log2_exact(is);
   *grid = (p.num_tokens + bs - 1) / bs * wt->tiles;
   *lds_bytes = (uint32_t)(bs * pitch);
-  return *grid <= 0x7FFFFFFF;
+  return grid_fits(*grid, kBlockThreads);
 }
 
 }  // namespace
@@ -306,7 +312,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
     const int64_t fg = (((int64_t)p.num_tokens << a.nchunks_log2) + kFlatThreads - 1) /
                        kFlatThreads;
-    if (fg <= 0x7FFFFFFF) wl.flat_grid = fg;
+    if (grid_fits(fg, kFlatThreads)) wl.flat_grid = fg;  // else write_kernel's grid-stride loop
   }
   hipStream_t s = as_stream(stream);
 
@@ -333,9 +339,21 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
 kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   const int cs = dtype_size((kvx_dtype_t)p.cache_dtype);
   const int is = dtype_size((kvx_dtype_t)p.io_dtype);
+  // RAGGED gathers of caches whose block rows are contiguous, with a
+  // power-of-two row length, take gather_ragged_tile_kernel.
+  const int64_t row_elems_all = (int64_t)p.heads * p.head_dim;
+  auto rows_contig = [&](const Geom &g) {
+    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim &&
+           g.s_off == row_elems_all;
+  };
+  const bool ragged_tile =
+      p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv) &&
+      log2_exact(row_elems_all) >= 0 &&
+      (p.conv == kConvDequant ? KVX_RAGGED_TILE_DEQUANT != 0 : KVX_RAGGED_TILE_COPY != 0);
   const int max_bytes =
       p.conv != kConvDequant ? 16
-      : p.format == KVX_BLOCK_TABLE_RAGGED ? KVX_RAGGED_DEQUANT_CHUNK : KVX_DEQUANT_CHUNK;
+      : p.format == KVX_BLOCK_TABLE_RAGGED && !ragged_tile ? KVX_RAGGED_DEQUANT_CHUNK
+                                                           : KVX_DEQUANT_CHUNK;
   const void *base_k = p.src_k;
   const void *base_v = p.src_v;
   if (p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
@@ -392,6 +410,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.bytes_per_block = p.bytes_per_block;
   a.format = p.format;
   a.rows_per_wg = 0;
+  a.ragged_tile = 0;
   a.max_blocks_per_seq = p.max_blocks_per_seq;
   const int64_t by_len =
       ((int64_t)p.max_seq_len + p.block_size - 1) / p.block_size;
@@ -423,6 +442,16 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
     };
     a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
+    if (ragged_tile && a.nchunks_log2 >= 0) {
+      // R rows of about KVX_FLAT_TILE_BYTES of cache per tensor: a power of
+      // two <= 64 (one block id per lane) that divides block_size
+      int64_t want = KVX_FLAT_TILE_BYTES / (row_elems * cs);
+      int64_t r = 1;
+      while (r * 2 <= want && r * 2 <= kWave && p.block_size % (r * 2) == 0) r *= 2;
+      a.ragged_tile = 1;
+      a.rows_per_wg = (int32_t)r;
+      a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + r - 1) / r);
+    }
     const bool ragged_copy = a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy;
     int64_t rows = (ragged_copy ? KVX_RAGGED_COPY_TILE_BYTES : KVX_GATHER_TILE_BYTES) /
                    (row_elems * cs);
@@ -435,18 +464,20 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       while (r2 * 2 <= rows && r2 * 2 <= p.block_size) r2 *= 2;
       rows = r2;
     }
-    a.rows_per_wg = (int32_t)rows;
-    a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
+    if (!a.ragged_tile) {
+      a.rows_per_wg = (int32_t)rows;
+      a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
+    }
   } else if (a.flat) {
     // split a block's chunks into a power-of-two number of equal ranges of
     // about KVX_FLAT_TILE_BYTES of cache per tensor, while the grid stays
-    // within 2^31 - 1 workgroups (larger ranges loop inside a workgroup)
+    // within HIP's limits (larger ranges loop inside a workgroup)
     const int64_t chunks = (int64_t)p.block_size * a.nchunks;
     const int64_t chunk_bytes = (int64_t)ge * cs;
     const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
     while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
            ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
-           a.split_log2 < 16 && blocks <= (0x7FFFFFFF >> (a.split_log2 + 1)))
+           a.split_log2 < 16 && grid_fits(blocks << (a.split_log2 + 1), kFlatThreads))
       ++a.split_log2;
     const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
     if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
@@ -454,7 +485,18 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   }
   if (a.blocks_per_seq <= 0 || p.seq_count <= 0) return KVX_STATUS_OK;
   const int64_t grid = (int64_t)p.seq_count * a.blocks_per_seq;
-  if (grid > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;  // one workgroup per block
+  // threads per workgroup of the kernel launch_gather_typed picks
+  int threads = kBlockThreads;
+  if (p.format == KVX_BLOCK_TABLE_PACKED) {
+    if (a.flat) threads = kFlatThreads;
+  } else if (a.ragged_tile) {
+    threads = kFlatThreads;
+  } else if (a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy) {
+    threads = KVX_RAGGED_COPY_THREADS;
+  }
+  // one workgroup per (sequence, tile): a batch whose grid exceeds HIP's
+  // limits (some 4 x 10^9 work-items) is not launched
+  if (!grid_fits(grid, threads)) return KVX_STATUS_UNSUPPORTED;
 
   if (p.conv == kConvCopy) {
     run_gather_copy(ge * cs, a, grid, s);

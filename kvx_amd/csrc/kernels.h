@@ -93,6 +93,15 @@ constexpr int kTilePad = 16;
 #endif
 // Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
 // together (the table load and the data load of each are dependent).
+// RAGGED gathers of row-contiguous caches (canonical NHD blocks) take
+// gather_ragged_tile_kernel (1) or gather_indexed_flat_kernel (0), for
+// copies and for dequantizing gathers.
+#ifndef KVX_RAGGED_TILE_COPY
+#define KVX_RAGGED_TILE_COPY 1
+#endif
+#ifndef KVX_RAGGED_TILE_DEQUANT
+#define KVX_RAGGED_TILE_DEQUANT 1
+#endif
 #ifndef KVX_INDEXED_UNROLL
 #define KVX_INDEXED_UNROLL 4
 #endif
@@ -123,6 +132,17 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #ifndef KVX_WRITE_NT_LOAD
 #define KVX_WRITE_NT_LOAD 0
 #endif
+// write_flat_kernel: when a row has at least 64 chunks, every lane of a
+// wave belongs to one token; the slot is then one scalar load per wave (1)
+// instead of one vector load per lane (0).
+#ifndef KVX_WRITE_FLAT_UNIFORM_SLOT
+#define KVX_WRITE_FLAT_UNIFORM_SLOT 1
+#endif
+// The row loads of write_flat_kernel and write_kernel are forced ahead of
+// the slot test (1), or left to the compiler (0), which sinks them below it.
+#ifndef KVX_WRITE_KEEP_LOADS
+#define KVX_WRITE_KEEP_LOADS 0
+#endif
 // Row-dense writes take write_flat_kernel (1) or write_kernel (0).
 #ifndef KVX_WRITE_FLAT
 #define KVX_WRITE_FLAT 1
@@ -136,6 +156,8 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 constexpr bool kWriteNtLoad = KVX_WRITE_NT_LOAD != 0;
 constexpr bool kTokenWriteNtLoad = KVX_TOKEN_WRITE_NT_LOAD != 0;
 constexpr bool kWriteFlat = KVX_WRITE_FLAT != 0;
+constexpr bool kWriteFlatUniformSlot = KVX_WRITE_FLAT_UNIFORM_SLOT != 0;
+constexpr bool kWriteKeepLoads = KVX_WRITE_KEEP_LOADS != 0;
 
 constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
 constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
@@ -243,6 +265,17 @@ __device__ __forceinline__ void st(char *p, const Raw<B> &r) {
 }
 
 // Element i of a chunk (i is a compile-time constant after unrolling).
+// Keep a chunk's load ahead of a branch: the empty asm consumes its
+// registers, so the compiler cannot sink the load into the branch's
+// successor (where it would issue only after the branch condition's own
+// load has returned).  The load and that condition's load are then in
+// flight together.
+template <int B>
+__device__ __forceinline__ void keep_loaded(const Raw<B> &r) {
+#pragma unroll
+  for (int i = 0; i < Raw<B>::kWords; ++i) asm volatile("" ::"v"(r.w[i]));
+}
+
 template <int B>
 __device__ __forceinline__ uint32_t get8(const Raw<B> &r, int i) {
   return (r.w[i >> 2] >> ((i & 3) * 8)) & 0xFFu;
@@ -551,6 +584,10 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
         if (c < a.nchunks) {
           xk[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sk + (int64_t)c * Op::kSrc);
           xv[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sv + (int64_t)c * Op::kSrc);
+          if constexpr (kWriteKeepLoads) {
+            keep_loaded(xk[k]);
+            keep_loaded(xv[k]);
+          }
         }
       }
     }
@@ -595,25 +632,40 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 // Row-dense caches (a token's H * D elements are consecutive in its block
 // row, for K and V): the write is a flat list of (token, chunk) pairs, and
 // each lane of a kFlatThreads-thread workgroup copies one 16-byte chunk of
-// K and one of V.  The chunks are loaded before the token's slot arrives;
-// lanes of one token share the slot's address.  This is the contiguous
-// gather's shape (gather_flat_kernel) from the other side.
-template <class Op>
+// K and one of V.  The chunks' loads are issued first and kept ahead of the
+// slot test, so the slot and the row data are in flight together.  S64:
+// int64 slots (else int32).  UNIFORM: rows of 64 or more chunks, so that a
+// wave holds chunks of one token only; the slot is then one scalar load per
+// wave (the token index made wave-uniform with readfirstlane) instead of one
+// vector load per lane.  This is the contiguous gather's shape
+// (gather_flat_kernel) from the other side.
+template <class Op, bool S64, bool UNIFORM>
 __global__ __launch_bounds__(kFlatThreads) void write_flat_kernel(WriteArgs a) {
   const int64_t f = (int64_t)blockIdx.x * kFlatThreads + threadIdx.x;
   const int64_t t = f >> a.nchunks_log2;
   if (t >= a.num_tokens) return;
   const int32_t c = (int32_t)(f & ((1 << a.nchunks_log2) - 1));
-  const int64_t slot = load_index(a.slots, t, a.slot_is64);
   const Raw<Op::kSrc> xk = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_k + t * a.row_bytes +
                                                            (int64_t)c * Op::kSrc);
   const Raw<Op::kSrc> xv = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_v + t * a.row_bytes +
                                                            (int64_t)c * Op::kSrc);
+  int64_t slot;
+  if constexpr (UNIFORM) {
+    // f < 2^32 (the grid is bounded by HIP's limits), so t < 2^26
+    const int64_t tw = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)t);
+    slot = load_idx<S64>(a.slots, tw);
+  } else {
+    slot = load_idx<S64>(a.slots, t);
+  }
   float ks = 1.0f;
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
+  }
+  if constexpr (kWriteKeepLoads) {
+    keep_loaded(xk);
+    keep_loaded(xv);
   }
   if (slot < 0) return;
   int64_t b, o;
@@ -1216,6 +1268,7 @@ struct GatherArgs {
   int32_t format;      // kvx_block_table_format_t
   int32_t nchunks_log2;  // indexed flat: nchunks is a power of two
   int32_t bs_log2;       // log2(block_size), or -1 when not a power of two
+  int32_t ragged_tile;   // RAGGED: gather_ragged_tile_kernel
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -2035,6 +2088,97 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
   }
 }
 
+// RAGGED gather of caches whose block rows are contiguous (canonical NHD
+// blocks): a workgroup of kFlatThreads threads covers rows_per_wg = R
+// consecutive output rows t0 .. t0 + R - 1 of one sequence, with R a
+// divisor of block_size and t0 a multiple of R, so the rows sit at offsets
+// t0 % bs .. t0 % bs + R - 1 of their blocks (KVX_SPEC.md:107-114: row t
+// is token indptr[s] + t at offset t % bs).  After seq_len and the indptr
+// pair, each wave loads the R block ids itself, one lane per row; a ballot
+// tells whether they name one valid block, which is the usual case (a
+// RAGGED table lists each block's tokens in order).  The tile is then one
+// contiguous run of that block, copied as in gather_flat_kernel; otherwise
+// every chunk takes its row's id from the lane that loaded it, and rows
+// whose id is < 0 or >= num_blocks are skipped.  No chunk loads an index of
+// its own.
+template <class Op, bool I64, bool P64>
+__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
+  constexpr int U = Op::kScaled ? kFlatUnrollDequant : kFlatUnroll;
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
+  int64_t n;
+  int64_t start;
+  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return;
+  const int64_t rem = n - t0;
+  const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;  // <= 64
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  int32_t id = -1;  // block ids are < num_blocks < 2^31
+  if (lane < rows) {
+    const int64_t b = load_idx<I64>(a.table, start + t0 + lane);
+    id = (b < 0 || b >= a.num_blocks) ? -1 : (int32_t)b;
+  }
+  const int32_t first = __builtin_amdgcn_readfirstlane(id);
+  const bool one = __ballot(lane < rows && id != first) == 0 && first >= 0;
+  const uint32_t tu = (uint32_t)t0;  // t0 < max_seq_len < 2^31
+  const uint32_t o0 = a.bs_log2 >= 0 ? tu & ((1u << a.bs_log2) - 1u) : tu % (uint32_t)a.block_size;
+  float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
+  float vs = 1.0f;
+  if constexpr (Op::kScaled) {
+    ks = a.ksc.p[0];
+    vs = a.vsc.p[0];
+  }
+  const uint32_t total = (uint32_t)rows << a.nchunks_log2;
+  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
+  if (one) {
+    flat_copy<Op>(a, a.src_k + first * a.gk.s_block + o0 * a.gk.s_off,
+                  a.src_v + first * a.gv.s_block + o0 * a.gv.s_off, a.dst_k + out0,
+                  a.dst_v + out0, total, ks, vs, first, 0);
+    return;
+  }
+  // Rows in several blocks (or skipped): chunk f is K for f < total, V
+  // above; row r = index >> nchunks_log2 takes its id from lane r.  The
+  // loop trip count is the same for every thread, so every lane joins each
+  // shuffle.
+  const uint32_t both = 2 * total;
+  const uint32_t cmask = (1u << a.nchunks_log2) - 1u;
+  for (uint32_t base = 0; base < both; base += U * kFlatThreads) {
+    const char *src[U];
+    char *dst[U];
+    float sc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t f = base + u * kFlatThreads + threadIdx.x;
+      const bool v = f >= total;
+      const uint32_t gi = f - (v ? total : 0u);
+      const uint32_t r = f < both ? gi >> a.nchunks_log2 : 0u;
+      const int32_t rid = __shfl(id, (int)r);
+      src[u] = nullptr;
+      dst[u] = nullptr;
+      sc[u] = v ? vs : ks;
+      if (f < both && rid >= 0) {
+        const GeomBytes &g = v ? a.gv : a.gk;
+        const uint32_t c = gi & cmask;
+        src[u] = (v ? a.src_v : a.src_k) + rid * g.s_block + (int64_t)(o0 + r) * g.s_off +
+                 (int64_t)c * Op::kSrc;
+        dst[u] = (v ? a.dst_v : a.dst_k) + out0 + (int64_t)r * a.out_row_bytes +
+                 (int64_t)c * Op::kDst;
+        if constexpr (Op::kScaled) sc[u] = run_scale(a, v, ks, vs, rid, c);
+      }
+    }
+    Raw<Op::kSrc> x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (src[u] != nullptr) x[u] = ld<Op::kSrc, kGatherNtLoad>(src[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (src[u] != nullptr) st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Launch templates.
 
@@ -2078,8 +2222,18 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
     hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false>), g, dim3(kBlockThreads), w.tile_lds,
                        s, a, w.wt);
   } else if (w.flat_grid > 0) {
-    hipLaunchKernelGGL(write_flat_kernel<Op>, dim3((uint32_t)w.flat_grid), dim3(kFlatThreads), 0,
-                       s, a);
+    const dim3 g((uint32_t)w.flat_grid), b(kFlatThreads);
+    if (kWriteFlatUniformSlot && a.nchunks_log2 >= 6) {
+      if (a.slot_is64) {
+        hipLaunchKernelGGL((write_flat_kernel<Op, true, true>), g, b, 0, s, a);
+      } else {
+        hipLaunchKernelGGL((write_flat_kernel<Op, false, true>), g, b, 0, s, a);
+      }
+    } else if (a.slot_is64) {
+      hipLaunchKernelGGL((write_flat_kernel<Op, true, false>), g, b, 0, s, a);
+    } else {
+      hipLaunchKernelGGL((write_flat_kernel<Op, false, false>), g, b, 0, s, a);
+    }
   } else {
     hipLaunchKernelGGL(write_kernel<Op>, dim3(w.grid), dim3(kBlockThreads), 0, s, a);
   }
@@ -2092,7 +2246,10 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
   const dim3 g((uint32_t)grid);
   const dim3 b(kBlockThreads);
   if (a.format == KVX_BLOCK_TABLE_RAGGED) {
-    if (a.flat) {
+    if (a.ragged_tile) {
+      hipLaunchKernelGGL((gather_ragged_tile_kernel<Op, I64, P64>), g, dim3(kFlatThreads), 0, s,
+                         a);
+    } else if (a.flat) {
       hipLaunchKernelGGL((gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g,
                          dim3(indexed_flat_threads<Op, KVX_BLOCK_TABLE_RAGGED>()), 0, s, a);
     } else {

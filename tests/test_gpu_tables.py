@@ -19,8 +19,8 @@ import torch
 from kvx_amd import paged
 from kvx_amd.abi import DType, Layout
 
-from gpu_helpers import (TORCH_DT, OffsetsPool, check_gather_offsets, check_gather_ragged,
-                         make_cache, random_fill)
+from gpu_helpers import (TORCH_DT, OffsetsPool, ScaleArg, check_gather_offsets,
+                         check_gather_ragged, make_cache, random_fill)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -143,6 +143,69 @@ def test_ragged_decode_shape():
     ko, vo = out_pair(S, L, H, D, DType.BF16, gen)
     check_gather_ragged(pc, kb, vb, ko, vo, table, torch.from_numpy(lens_np).to(DEV), L,
                         cache_dtype=DType.BF16, io_dtype=DType.BF16)
+
+
+def block_run_table(rng, S, L, nb, bs, idt, pdt, spoil=0):
+    """RAGGED table of block-structured sequences (each lists the tokens of
+    its blocks in order, as a paged-attention RAGGED table does): lengths up
+    to L + 3, random distinct blocks, and `spoil` ids replaced by -1, an
+    out-of-range id or another block, so that some row tiles name several
+    blocks or skipped rows."""
+    counts = rng.integers(0, L + 4, size=S)
+    counts[0] = L  # one full-length sequence
+    nblk = (counts + bs - 1) // bs
+    perm = rng.permutation(nb)
+    ids, at = [], 0
+    for s in range(S):
+        blocks = perm[(at + np.arange(nblk[s])) % nb]
+        at += nblk[s]
+        ids.append(np.repeat(blocks, bs)[: counts[s]])
+    indices = np.concatenate(ids) if ids else np.zeros(0)
+    if indices.size == 0:
+        indices = np.zeros(1)
+    for i in rng.choice(indices.size, size=min(spoil, indices.size), replace=False):
+        indices[i] = [-1, nb + 3, (indices[i] + 1) % nb][int(rng.integers(0, 3))]
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(pdt)
+    return paged.RaggedTable(torch.from_numpy(indices.astype(idt)).to(DEV),
+                             torch.from_numpy(indptr).to(DEV))
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_ragged_block_runs(case):
+    """RAGGED tables that list whole blocks in order, on canonical NHD caches
+    (the row-tile kernel's one-block path), with a few spoiled ids (its
+    per-row path): copies and FP8 dequantizing gathers with per-tensor,
+    per-head, per-block and per-block-head scales, block sizes 1, 6, 16 and
+    32, int32 / int64 indices and indptr."""
+    rng = np.random.default_rng(7000 + case)
+    gen = torch.Generator().manual_seed(case)
+    from kvx_amd.abi import ScaleGranularity as SG
+
+    bs = [16, 32, 1, 6][case % 4]
+    dt = [DType.BF16, DType.F8_E4M3, DType.F8_E5M2, DType.F16][(case // 4) % 4]
+    io = {DType.F8_E4M3: [DType.BF16, DType.F16, DType.F32][case % 3],
+          DType.F8_E5M2: [DType.BF16, DType.F32, DType.F16][case % 3]}.get(dt, dt)
+    H, D = [(8, 128), (2, 64), (4, 32), (1, 128)][case % 4]
+    nb = int(rng.integers(20, 60))
+    S, L = int(rng.integers(2, 7)), int(rng.integers(bs, 200))
+    idt = [np.int32, np.int64][case % 2]
+    pdt = [np.int64, np.int32][(case // 2) % 2]
+    pc, kb, vb = make_cache(NHD, NHD, dt, nb, bs, H, D, gen=gen)
+    table = block_run_table(rng, S, L, nb, bs, idt, pdt, spoil=[0, 3][case % 2])
+    lens = lens_tensor(rng, S, L, idt)
+    ko, vo = out_pair(S, L, H, D, io, gen)
+    ks = vs = None
+    if dt in (DType.F8_E4M3, DType.F8_E5M2):
+        kind = ["tensor", "head", "block", "block_head"][(case // 2) % 4]
+        if kind == "tensor":
+            ks, vs = 0.021, 1.75
+        else:
+            shape = {"head": (H,), "block": (nb,), "block_head": (nb, H)}[kind]
+            g = {"head": SG.PER_HEAD, "block": SG.PER_BLOCK, "block_head": SG.PER_BLOCK_HEAD}[kind]
+            ks = ScaleArg(g, rng.uniform(0.01, 2.0, size=shape))
+            vs = ScaleArg(g, rng.uniform(0.01, 2.0, size=shape))
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=io,
+                        k_scale=ks, v_scale=vs)
 
 
 # ---------------------------------------------------------------------------

@@ -424,3 +424,30 @@ def test_kv_offsets_validation(kvx_lib):
     c, g = offsets_gather(L=0, lens=DType.S64)
     c.k.data = c.v.data = None
     assert G(kvx_lib, c, g) == OK
+
+
+# ---------------------------------------------------------------------------
+# Grid limits: HIP allows at most 2^32 - 1 work-items per grid dimension.
+# Each case below is just past that limit for the kernel its shape selects,
+# so it returns UNSUPPORTED before any launch (no GPU is touched).
+
+def big_gather(layout, S, L, H, D, bs, fmt="packed"):
+    cache = abi.make_cache(layout, DType.F16, D_, 64, bs, H, D, FAKE, FAKE)
+    sl = abi.make_seq_lens(S, DType.S32, FAKE)
+    tb = abi.make_block_table_packed(S, (L + bs - 1) // bs, DType.S32, FAKE)
+    if fmt == "ragged":
+        tb.format = TableFormat.RAGGED
+        tb.indptr, tb.indptr_dtype, tb.indptr_count = FAKE, DType.S32, S + 1
+    return cache, abi.make_gather(S, L, H, D, DType.F16, D_, FAKE, FAKE, tb, sl)
+
+
+def test_gather_grid_past_hip_limits(kvx_lib):
+    # gather_rows_kernel (HND rows of 12 bytes: no LDS tile), 256 threads:
+    # 4096 x 4096 workgroups = 2^32 work-items
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_HND, 4096, 65536, 1, 6, 16)) == UNS
+    # gather_flat_kernel (canonical NHD), 128 threads, blocks no longer
+    # split: 8192 x 4096 workgroups = 2^32 work-items
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16)) == UNS
+    # gather_ragged_tile_kernel, 128 threads, 16 rows per workgroup
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16,
+                                  fmt="ragged")) == UNS
