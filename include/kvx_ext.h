@@ -33,6 +33,22 @@
  *
  * The reference has no FP8 kernels (KVX_CONFORMANCE.md:24, :35); this is new
  * functionality.
+ *
+ * Block-table formats beyond PACKED (KVX_SPEC.md:99-122), gathered by
+ * kvx_launch_gather_kv, kvx_launch_gather_kv_dequant and kvx_gather_kv (the
+ * reference returns UNSUPPORTED for them, kernels/kvx_paged_kv.cu:788-790):
+ *   RAGGED      row t of sequence s is token indptr[s] + t, valid for
+ *               t < indptr[s+1] - indptr[s]; its block id is indices[token]
+ *               (skipped when < 0 or >= num_blocks), its offset t % block_size.
+ *   KV_OFFSETS  int32 KVCacheIndex entries [seq_count, 1, 2, max_blocks_per_seq]
+ *               (K then V): bit 31 selects the secondary pool, bits 0-30 the
+ *               block; the block's address is pool + index * bytes_per_block.
+ *               An entry is skipped when its index is >= num_blocks or its
+ *               pool is NULL.  kvx_pool_desc_t carries no pool sizes, so
+ *               BOTH pools must hold at least num_blocks blocks of
+ *               bytes_per_block bytes: a smaller secondary pool (an offload
+ *               pool, say) is read out of bounds by indices between its size
+ *               and num_blocks.
  */
 #ifndef KVX_EXT_H
 #define KVX_EXT_H

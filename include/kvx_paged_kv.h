@@ -19,7 +19,9 @@ extern "C" {
 
 /* Scatter K/V rows [num_tokens, H, D] into the paged cache at slot_mapping
  * positions; slot < 0 and block >= num_blocks are skipped.  Dispatches on
- * the cache dtype (F16/BF16/F32; F8_E4M3 quantizes with a per-tensor scale).
+ * the cache dtype: F16/BF16/F32 copy; an F8_E4M3 or F8_E5M2 cache with
+ * F16/BF16/F32 io quantizes with per-tensor, per-head, per-block or
+ * per-block-head scales (kvx_ext.h).
  * Replaces reference kvx_paged_kv.cu:472-491. */
 KVX_API kvx_status_t kvx_launch_write_kv(const kvx_cache_desc_t *cache,
                                          const kvx_write_desc_t *write,
@@ -31,9 +33,13 @@ KVX_API kvx_status_t kvx_launch_write_kv_prefill(
     const kvx_cache_desc_t *cache, const kvx_write_desc_t *write,
     int32_t tokens_per_seq, void *stream);
 
-/* Gather a PACKED block table's sequences into contiguous
- * [seq_count, max_seq_len, H, D]; rows at or past seq_len, logical blocks
- * past max_blocks_per_seq and negative block ids are left untouched.
+/* Gather the sequences of a PACKED, RAGGED or KV_OFFSETS block table
+ * (kvx_ext.h) into contiguous [seq_count, max_seq_len, H, D]; rows at or
+ * past seq_len, logical blocks past max_blocks_per_seq, and rows whose block
+ * id is < 0 or >= num_blocks are left untouched (the reference skips only
+ * negative ids and reads larger ones out of bounds).  A batch whose launch
+ * grid would exceed HIP's limits (2^32 - 1 work-items per dimension) returns
+ * KVX_STATUS_UNSUPPORTED without launching.
  * Replaces reference kvx_paged_kv.cu:891-910. */
 KVX_API kvx_status_t kvx_launch_gather_kv(const kvx_cache_desc_t *cache,
                                           const kvx_gather_desc_t *gather,
