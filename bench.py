@@ -106,9 +106,12 @@ def parse_args():
                         "block, per block and head)")
     p.add_argument("--layers", type=int, default=None,
                    help="override the layer count of c1/c2/c4")
-    p.add_argument("--c3-order", default="random", choices=["random", "ascending"],
-                   help="c3: block assignment (random draw from the pool, or ascending "
-                        "as a fresh allocator hands blocks out)")
+    p.add_argument("--c3-order", default="random",
+                   choices=["random", "ascending", "sorted", "compact"],
+                   help="c3: block assignment: a random draw from the pool (the config), "
+                        "ascending as a fresh allocator hands blocks out, the random draw "
+                        "sorted (random's footprint in ascending order), or ascending's "
+                        "blocks permuted (ascending's footprint in random order)")
     p.add_argument("--c3-seqs", type=int, default=16,
                    help="c3: 2048-token chunks per write (pool 512 blocks per chunk)")
     p.add_argument("--sweep", default=None, choices=["c3"],
@@ -482,7 +485,7 @@ class Probe:
     """Plain copy / read / write kernels over byte counts beyond the
     Infinity Cache: the best stream of this box, beside the KV kernels."""
 
-    OPS = ("copy", "read", "write")
+    OPS = ("copy", "read", "write", "expand")
 
     def __init__(self):
         from kvx_amd import build as kbuild
@@ -494,6 +497,7 @@ class Probe:
         L.kvx_probe_copy.argtypes = [vp, vp, i64, i, vp]
         L.kvx_probe_read.argtypes = [vp, i64, vp, i, vp]
         L.kvx_probe_write.argtypes = [vp, i64, C.c_uint32, i, vp]
+        L.kvx_probe_expand.argtypes = [vp, vp, i64, i, vp]
         L.kvx_probe_shape.argtypes = [i, C.POINTER(i), C.POINTER(i)]
         self.L = L
         self.shapes = []
@@ -505,19 +509,20 @@ class Probe:
     def ceiling(self, nbytes, stream, reps=4, rotate_bytes=1 << 30):
         """Per op: {bytes moved per launch, GB/s of the fastest shape, that
         shape (threads, chunks per lane), mean us}.  Copy moves 2 * nbytes
-        (read + write); read and write move nbytes.  Launches rotate over
-        buffer pairs covering at least `rotate_bytes` per side, so that each
-        one's data has left L2 and the Infinity Cache before it is reused;
-        every pair runs at least `reps` times per (op, shape)."""
+        (read + write); read and write move nbytes; expand 3 * nbytes (read
+        nbytes, write 2 * nbytes).  Launches rotate over buffer pairs
+        covering at least `rotate_bytes` per side, so that each one's data
+        has left L2 and the Infinity Cache before it is reused; every pair
+        runs at least `reps` times per (op, shape)."""
         import torch
 
         nbytes = max(16, nbytes // 16 * 16)
         pairs = max(1, min(1024, -(-rotate_bytes // nbytes)))
         cycles = max(1, -(-reps // pairs))
         src_all = torch.empty(pairs * nbytes, dtype=torch.uint8, device="cuda").fill_(3)
-        dst_all = torch.empty(pairs * nbytes, dtype=torch.uint8, device="cuda")
-        bufs = [(dst_all[i * nbytes:(i + 1) * nbytes], src_all[i * nbytes:(i + 1) * nbytes])
-                for i in range(pairs)]
+        dst_all = torch.empty(2 * pairs * nbytes, dtype=torch.uint8, device="cuda")
+        bufs = [(dst_all[2 * i * nbytes:2 * (i + 1) * nbytes],
+                 src_all[i * nbytes:(i + 1) * nbytes]) for i in range(pairs)]
         sink = torch.zeros(1024, dtype=torch.uint8, device="cuda")
         sh = stream.cuda_stream
         out = {}
@@ -530,6 +535,8 @@ class Probe:
                     if op == "read":
                         return self.L.kvx_probe_read(s.data_ptr(), nbytes, sink.data_ptr(), k,
                                                      sh)
+                    if op == "expand":
+                        return self.L.kvx_probe_expand(d.data_ptr(), s.data_ptr(), nbytes, k, sh)
                     return self.L.kvx_probe_write(d.data_ptr(), nbytes, 7, k, sh)
 
                 for d, s in bufs:
@@ -546,7 +553,7 @@ class Probe:
                         evs.append((e0, e1))
                 torch.cuda.synchronize()
                 ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
-                moved = 2 * nbytes if op == "copy" else nbytes
+                moved = {"copy": 2, "expand": 3}.get(op, 1) * nbytes
                 gbps = moved / (ms / 1e3) / 1e9
                 if best is None or gbps > best["GBps"]:
                     best = {"bytes_per_launch": moved, "GBps": round(gbps, 1),

@@ -76,12 +76,12 @@ constexpr int kTilePad = 16;
 #endif
 // Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about this
 // many cache bytes of each tensor, in 256-thread workgroups.  The RAGGED
-// copy of row-dense caches (gather_indexed_flat_kernel without a dequant)
-// uses KVX_RAGGED_COPY_THREADS threads and KVX_RAGGED_COPY_TILE_BYTES
-// instead: on MI355X (c2, same box) 64 threads and 2 KiB measured 7% faster
-// than 256 threads and 4 KiB, 128 threads and 2 KiB 5%; the same change
-// made KV_OFFSETS copies 1-2% and the RAGGED dequantizing gather 2-8%
-// slower.
+// copy of row-dense caches whose rows are not contiguous in the block
+// (gather_indexed_flat_kernel without a dequant) uses
+// KVX_RAGGED_COPY_THREADS threads and KVX_RAGGED_COPY_TILE_BYTES instead: on
+// MI355X (c2, same box) 64 threads and 2 KiB measured 7% faster than 256
+// threads and 4 KiB, 128 threads and 2 KiB 5%; the same change made
+// KV_OFFSETS copies 1-2% and that kernel's dequantizing gather 2-8% slower.
 #ifndef KVX_GATHER_TILE_BYTES
 #define KVX_GATHER_TILE_BYTES 4096
 #endif
@@ -91,17 +91,20 @@ constexpr int kTilePad = 16;
 #ifndef KVX_RAGGED_COPY_TILE_BYTES
 #define KVX_RAGGED_COPY_TILE_BYTES 2048
 #endif
-// Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
-// together (the table load and the data load of each are dependent).
 // RAGGED gathers of row-contiguous caches (canonical NHD blocks) take
 // gather_ragged_tile_kernel (1) or gather_indexed_flat_kernel (0), for
-// copies and for dequantizing gathers.
+// copies and for dequantizing gathers.  On MI355X (same-box A/B, medians of
+// 6 alternating rounds) the tile kernel took c4's FP8 dequantizing gather
+// from 690 to 629 us and c5's copy from 2336 to 2241 us; c2's copy measured
+// 1587 against 1571 us.
 #ifndef KVX_RAGGED_TILE_COPY
 #define KVX_RAGGED_TILE_COPY 1
 #endif
 #ifndef KVX_RAGGED_TILE_DEQUANT
 #define KVX_RAGGED_TILE_DEQUANT 1
 #endif
+// Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
+// together (the table load and the data load of each are dependent).
 #ifndef KVX_INDEXED_UNROLL
 #define KVX_INDEXED_UNROLL 4
 #endif
@@ -115,8 +118,9 @@ constexpr int kTilePad = 16;
 #endif
 constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 // FP8 cache bytes per chunk of the dequantizing gathers (8 or 16): 16-byte
-// chunks measured 3% faster for the RAGGED row kernels on MI355X (half the
-// per-chunk block-id loads) and 20-40% slower for every other gather.
+// chunks measured 3% faster for the RAGGED kernels that load a block id per
+// chunk (gather_indexed_flat_kernel; half the id loads) and 20-40% slower
+// for every other gather, gather_ragged_tile_kernel included (8).
 #ifndef KVX_DEQUANT_CHUNK
 #define KVX_DEQUANT_CHUNK 8
 #endif
@@ -134,12 +138,17 @@ constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 #endif
 // write_flat_kernel: when a row has at least 64 chunks, every lane of a
 // wave belongs to one token; the slot is then one scalar load per wave (1)
-// instead of one vector load per lane (0).
+// instead of one vector load per lane (0).  Kernel traces on MI355X: c4's
+// quantizing write 5.11 against 5.45 us, c2's and c5's writes unchanged
+// (3.90 / 3.87 and 4.75 / 4.77 us).
 #ifndef KVX_WRITE_FLAT_UNIFORM_SLOT
 #define KVX_WRITE_FLAT_UNIFORM_SLOT 1
 #endif
 // The row loads of write_flat_kernel and write_kernel are forced ahead of
-// the slot test (1), or left to the compiler (0), which sinks them below it.
+// the slot test (1), or left to the compiler (0), which may sink them below
+// it.  On MI355X (kernel traces, same box) forcing them measured no gain:
+// c2's decode write 3.90 against 3.88 us, c4's quantizing write 5.11
+// against 4.86 us, c5's 2048-token write 4.75 against 4.82 us.
 #ifndef KVX_WRITE_KEEP_LOADS
 #define KVX_WRITE_KEEP_LOADS 0
 #endif

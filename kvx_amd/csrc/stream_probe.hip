@@ -4,7 +4,9 @@
 //          KV write or gather, with no index work);
 //   read   reads n bytes (folded into one word per workgroup that is stored
 //          only if it equals a value the data never produce);
-//   write  writes n bytes of a constant.
+//   write  writes n bytes of a constant;
+//   expand reads n bytes and writes each 16-byte chunk twice, to 2n bytes
+//          (the 1:2 read/write mix of an FP8 -> bf16 dequantizing gather).
 //
 // Each kernel is instantiated in a few launch shapes (threads per
 // workgroup x 16-byte chunks per lane, every chunk of a workgroup in flight
@@ -66,6 +68,25 @@ __global__ __launch_bounds__(T) void write_kernel(u32x4 *dst, int64_t n, uint32_
   }
 }
 
+template <int T, int U>
+__global__ __launch_bounds__(T) void expand_kernel(const u32x4 *src, u32x4 *dst, int64_t n) {
+  const int64_t base = (int64_t)blockIdx.x * (T * U) + threadIdx.x;
+  u32x4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    if (i < n) v[u] = __builtin_nontemporal_load(src + i);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    if (i < n) {
+      __builtin_nontemporal_store(v[u], dst + i);
+      __builtin_nontemporal_store(v[u], dst + n + i);
+    }
+  }
+}
+
 struct Shape {
   int threads;
   int unroll;
@@ -92,9 +113,12 @@ void launch(int op, void *dst, const void *src, int64_t n, uint32_t value, int64
   } else if (op == 1) {
     hipLaunchKernelGGL((read_kernel<T, U>), grid, block, 0, s, static_cast<const u32x4 *>(src),
                        n, static_cast<uint32_t *>(dst), value);
-  } else {
+  } else if (op == 2) {
     hipLaunchKernelGGL((write_kernel<T, U>), grid, block, 0, s, static_cast<u32x4 *>(dst), n,
                        value);
+  } else {
+    hipLaunchKernelGGL((expand_kernel<T, U>), grid, block, 0, s,
+                       static_cast<const u32x4 *>(src), static_cast<u32x4 *>(dst), n);
   }
 }
 
@@ -146,6 +170,11 @@ int kvx_probe_read(const void *src, int64_t bytes, void *sink, int shape, void *
 
 int kvx_probe_write(void *dst, int64_t bytes, uint32_t value, int shape, void *stream) {
   return run(2, shape, dst, nullptr, bytes, value, stream);
+}
+
+// dst: 2 * bytes of device memory.
+int kvx_probe_expand(void *dst, const void *src, int64_t bytes, int shape, void *stream) {
+  return run(3, shape, dst, src, bytes, 0, stream);
 }
 
 }  // extern "C"

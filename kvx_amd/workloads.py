@@ -206,18 +206,26 @@ def c2_llama8b_decode(seed: int = 2, batch: int = 256) -> Workload:
 def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs: int = 16,
                        order: str = "random") -> Workload:
     """c3; `seqs` chunks of 2048 tokens over a pool of 512 blocks per
-    sequence (16 and 8192 as configured).  order "random": each sequence's
+    sequence (16 and 8192 as configured).  order "random": the sequences'
     blocks are a seeded random draw from the pool; "ascending": sequence s
     takes blocks s * 128 .. s * 128 + 127 in order, as a fresh allocator
-    would hand them out."""
+    would hand them out.  Two orders separate what random blocks change:
+    "sorted" is the random draw in ascending order (random's footprint,
+    ascending's order), "compact" a random permutation of ascending's
+    blocks (ascending's footprint, random order)."""
     rng = np.random.Generator(np.random.PCG64(seed))
     S, chunk, bs = seqs, 2048, 16
     pool = 512 * S
     mbps = chunk // bs
+    draw = rng.permutation(pool)[: S * mbps]
     if order == "random":
-        ids = rng.permutation(pool)[: S * mbps]
+        ids = draw
     elif order == "ascending":
         ids = np.arange(S * mbps)
+    elif order == "sorted":
+        ids = np.sort(draw)
+    elif order == "compact":
+        ids = rng.permutation(S * mbps)
     else:
         raise ValueError(order)
     table = ids.reshape(S, mbps).astype(np.int32)
