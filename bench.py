@@ -528,6 +528,7 @@ class Probe:
         out = {}
         for op in self.OPS:
             best = None
+            every = {}  # "threads x chunks per lane" -> GB/s
             for k, shape in enumerate(self.shapes):
                 def one(d, s):
                     if op == "copy":
@@ -555,10 +556,12 @@ class Probe:
                 ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
                 moved = {"copy": 2, "expand": 3}.get(op, 1) * nbytes
                 gbps = moved / (ms / 1e3) / 1e9
+                every[f"{shape[0]}x{shape[1]}"] = round(gbps, 1)
                 if best is None or gbps > best["GBps"]:
                     best = {"bytes_per_launch": moved, "GBps": round(gbps, 1),
                             "frac": round(gbps / PEAK_HBM_GBS, 4),
                             "shape": list(shape), "mean_us": round(ms * 1e3, 2)}
+            best["GBps_by_shape"] = every
             out[op] = best
         out["buffers"] = pairs
         out["footprint_bytes"] = 2 * pairs * nbytes

@@ -91,7 +91,8 @@ struct Shape {
   int threads;
   int unroll;
 };
-constexpr Shape kShapes[] = {{64, 4}, {128, 1}, {128, 2}, {256, 1}, {256, 4}};
+constexpr Shape kShapes[] = {{64, 1},  {64, 4},  {128, 1}, {128, 2}, {128, 4}, {256, 1},
+                             {256, 2}, {256, 4}, {512, 1}, {512, 2}, {1024, 1}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 
 // Workgroups for n chunks, or 0 when the grid would exceed HIP's limits
@@ -133,11 +134,17 @@ int run(int op, int shape, void *dst, const void *src, int64_t bytes, uint32_t v
   if (g == 0) return 1;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (shape) {
-    case 0: launch<64, 4>(op, dst, src, n, value, g, s); break;
-    case 1: launch<128, 1>(op, dst, src, n, value, g, s); break;
-    case 2: launch<128, 2>(op, dst, src, n, value, g, s); break;
-    case 3: launch<256, 1>(op, dst, src, n, value, g, s); break;
-    default: launch<256, 4>(op, dst, src, n, value, g, s); break;
+    case 0: launch<64, 1>(op, dst, src, n, value, g, s); break;
+    case 1: launch<64, 4>(op, dst, src, n, value, g, s); break;
+    case 2: launch<128, 1>(op, dst, src, n, value, g, s); break;
+    case 3: launch<128, 2>(op, dst, src, n, value, g, s); break;
+    case 4: launch<128, 4>(op, dst, src, n, value, g, s); break;
+    case 5: launch<256, 1>(op, dst, src, n, value, g, s); break;
+    case 6: launch<256, 2>(op, dst, src, n, value, g, s); break;
+    case 7: launch<256, 4>(op, dst, src, n, value, g, s); break;
+    case 8: launch<512, 1>(op, dst, src, n, value, g, s); break;
+    case 9: launch<512, 2>(op, dst, src, n, value, g, s); break;
+    default: launch<1024, 1>(op, dst, src, n, value, g, s); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
