@@ -126,6 +126,10 @@ def parse_args():
     p.add_argument("--profile-only", action="store_true",
                    help="time only the KV kernels (no CPU baseline, stream ceiling or "
                         "graph): the command profiler runs use")
+    p.add_argument("--detail", default=None, metavar="PATH",
+                   help="also write the full record (every stream shape, every config's "
+                        "full kernel, ceiling and CPU-baseline figures) to PATH as JSON; the "
+                        "line on stdout stays compact")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run three plain 1 GiB device copies: the known-size "
                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -774,12 +778,13 @@ def kernel_sources_digest() -> str:
     return h.hexdigest()
 
 
-def load_traffic(kind: str, workload: str, algo_bytes: int):
+def load_traffic(kind: str, workload: str, algo_bytes: int, root: Path = REPO):
     """HBM bytes per launch from the committed rocprofv3 counter summary of
-    this kernel kind and workload, with its file name, or (None, reason)
-    when there is none or it was taken of other bytes or other sources."""
+    this kernel kind and workload (root/profiles), with its file name, or
+    (None, reason) when there is none or it was taken of other bytes or
+    other kernel sources."""
     rel = f"profiles/traffic_{kind}_{workload}.json"
-    p = REPO / rel
+    p = root / rel
     if not p.exists():
         return None, f"{rel}: none"
     try:
@@ -875,6 +880,44 @@ def sweep_c3(args, dev, stream):
                       "fit": fits}), flush=True)
 
 
+# The stdout line stays short: the full figures go to --detail.
+
+def compact_kernel(k):
+    return {x: k[x] for x in ("launches", "mean_ms", "median_ms", "bytes_per_launch", "GBps",
+                              "frac", "tokens_per_s")}
+
+
+def compact_ceiling(c):
+    if c is None:
+        return None
+    return {op: {"GBps": c[op]["GBps"], "frac": c[op]["frac"], "shape": c[op]["shape"]}
+            for op in Probe.OPS}
+
+
+def compact_cpu(c):
+    if c is None:
+        return None
+    return {"value": c["value"], "unit": c["unit"], "cores": c["cores"],
+            "single_thread": c["single_thread"]["value"], "kind": c["kind"],
+            "cpu_model": c["cpu_model"], "sample": c["sample"]}
+
+
+def compact_config(r):
+    rf = r["roofline"]
+    out = {"workload": r["config"]["workload"], "value": r["value"],
+           "ms_per_step": r["ms_per_step"],
+           "kernels": {k: {x: v[x] for x in ("mean_ms", "median_ms", "GBps", "frac")}
+                       for k, v in r["kernels"].items()},
+           "roofline": {x: rf[x] for x in ("kernel", "frac", "frac_median", "traffic")}}
+    if r.get("stream_ceiling"):
+        out["ceiling_frac"] = {op: r["stream_ceiling"][op]["frac"] for op in ("copy", "expand")}
+    c = r.get("cpu_baseline")
+    if c:
+        out["cpu_baseline"] = {"value": c["value"], "cores": c["cores"],
+                               "single_thread": c["single_thread"]["value"], "kind": c["kind"]}
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -925,13 +968,19 @@ def main():
         for name in ("c1", "c3", "c4", "c5"):
             ks = max(K, -(-MIN_LAUNCHES[name] // {"c1": 22, "c4": 32}.get(name, 1)))
             configs[name] = run_config(name, dev, stream, ks, W, args, cpu)
-            print(f"config {name}: {configs[name]['kernels']}", file=sys.stderr, flush=True)
+            print(f"config {name}: " + ", ".join(
+                f"{k} {v['mean_ms'] * 1e3:.1f} us ({v['frac']:.3f})"
+                for k, v in configs[name]["kernels"].items()), file=sys.stderr, flush=True)
 
     cpu_res = None
     if cpu:
         cpu_res = cpu_baseline(w, args.cpu_seconds, CPU_SAMPLE_SEQS[head],
                                gather=head != "c3", scales=scales, table_fmt=args.table)
 
+    detail = {"kernels": res["kernels"], "roofline": roofline, "stream_ceiling": ceiling,
+              "write_graph": graph, "cpu_baseline": cpu_res, "configs": configs}
+    if args.detail:
+        Path(args.detail).write_text(json.dumps(detail) + "\n")
     out = {
         "metric": METRIC, "value": res["value"], "unit": "GB/s", "n_gpus": 1,
         "steps": K, "warmup": W, "ms_per_step": res["ms_per_step"],
@@ -942,12 +991,12 @@ def main():
         "config": cfg,
         "pct_of_peak": res["pct_of_peak"],
         "tokens_per_s": res["tokens_per_s"],
-        "kernels": res["kernels"],
+        "kernels": {k: compact_kernel(v) for k, v in res["kernels"].items()},
         "roofline": roofline,
-        "stream_ceiling": ceiling,
+        "stream_ceiling": compact_ceiling(ceiling),
         "write_graph": graph,
-        "cpu_baseline": cpu_res,
-        "configs": configs,
+        "cpu_baseline": compact_cpu(cpu_res),
+        "configs": {name: compact_config(r) for name, r in configs.items()},
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(out), flush=True)

@@ -1,0 +1,64 @@
+"""bench.py's bookkeeping, on the CPU: the provenance rule of
+roofline.traffic, the CPU model string, and the streaming-probe library's
+launch shapes (no kernel is launched)."""
+import json
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(REPO))
+
+import bench  # noqa: E402
+
+
+def _profile(tmp_path, **fields):
+    (tmp_path / "profiles").mkdir(exist_ok=True)
+    d = {"bytes_per_launch": 1000, "algorithmic_bytes": 990,
+         "kernel_sources_sha256": bench.kernel_sources_digest()}
+    d.update(fields)
+    (tmp_path / "profiles" / "traffic_gather_wl.json").write_text(json.dumps(d))
+
+
+def test_traffic_used_only_for_same_bytes_and_sources(tmp_path):
+    assert bench.load_traffic("gather", "wl", 990, tmp_path)[0] is None  # no summary
+    _profile(tmp_path)
+    val, src = bench.load_traffic("gather", "wl", 990, tmp_path)
+    assert val == 1000 and src == "profiles/traffic_gather_wl.json"
+    val, why = bench.load_traffic("gather", "wl", 991, tmp_path)
+    assert val is None and "990" in why
+    _profile(tmp_path, kernel_sources_sha256="0" * 64)
+    val, why = bench.load_traffic("gather", "wl", 990, tmp_path)
+    assert val is None and "other kernel sources" in why
+
+
+def test_kernel_sources_digest_covers_every_kernel_unit():
+    from kvx_amd import build as kbuild
+
+    units = [s for s in kbuild.SOURCES if s.endswith(".hip")]
+    assert "dispatch.hip" in units and any(u.startswith("kernels_") for u in units)
+    d = bench.kernel_sources_digest()
+    assert len(d) == 64 and d == bench.kernel_sources_digest()
+
+
+def test_committed_traffic_summaries_name_their_workload():
+    for p in (REPO / "profiles").glob("traffic_*.json"):
+        d = json.loads(p.read_text())
+        assert p.name == f"traffic_{d['kind']}_{d['workload']}.json"
+        assert 0.99 < d["bytes_per_launch"] / d["algorithmic_bytes"] < 1.05
+
+
+def test_cpu_model_string():
+    m = bench.cpu_model()
+    assert m == "unknown" or "family" in m
+
+
+def test_probe_shapes():
+    from kvx_amd import build as kbuild
+
+    if not kbuild.PROBE_LIB.exists():
+        pytest.skip("libkvx_amd_probe.so is not built")
+    shapes = bench.Probe().shapes
+    assert (64, 1) in shapes and (256, 1) in shapes
+    assert all(t in (64, 128, 256, 512, 1024) and u in (1, 2, 4) for t, u in shapes)

@@ -72,6 +72,21 @@ def check_gather_against_indexing(pc, w, ko, vo, ko_before, vo_before, seqs_per_
             del ref
 
 
+def ragged_equals_packed(pc, w, ko, vo, out_k, out_v, k_scale=None, v_scale=None):
+    """The workload's table as a RAGGED table (one block id per token) gathers
+    the same bytes as the PACKED gather into ko / vo: every gathered row, and
+    the untouched rows past each length (out_k / out_v still hold what ko / vo
+    held before their gather).  Canonical NHD caches with block-structured
+    RAGGED tables take the row-tile RAGGED kernel."""
+    indices, indptr = workloads.ragged_table(w)
+    table = paged.RaggedTable(torch.tensor(indices, device=DEV), torch.tensor(indptr, device=DEV))
+    assert paged.gather_kv(pc, out_k, out_v, table, torch.tensor(w.seq_lens, device=DEV),
+                           w.max_seq_len, k_scale=k_scale, v_scale=v_scale) == Status.OK
+    torch.cuda.synchronize()
+    assert torch.equal(i16(out_k), i16(ko))
+    assert torch.equal(i16(out_v), i16(vo))
+
+
 def sentinel_like(shape, dtype, fill=-5):
     t = torch.empty(shape, dtype=dtype, device=DEV)
     i16(t).fill_(fill)
@@ -229,6 +244,7 @@ def test_c4_full_fp8_quantize_and_dequant_gather():
     ref = paged.PagedCache(deq(pc.key_cache, ks), deq(pc.value_cache, vs), pc.k_layout,
                            pc.v_layout, pc.num_blocks, bs, H, D)
     check_gather_against_indexing(ref, w, ko, vo, kb, vb)
+    ragged_equals_packed(pc, w, ko, vo, kb, vb, k_scale=ks, v_scale=vs)
 
 
 def test_c5_full_long_context_200gb_pool():
@@ -259,6 +275,7 @@ def test_c5_full_long_context_200gb_pool():
     assert torch.equal(i16(ko[srow, idx]).reshape(-1, H, D), i16(key))
     assert torch.equal(i16(vo[srow, idx]).reshape(-1, H, D), i16(val))
     check_gather_against_indexing(pc, w, ko, vo, kb, vb, seqs_per_chunk=4)
+    ragged_equals_packed(pc, w, ko, vo, kb, vb)
 
 
 def test_token_write_grid_stride_loop():
