@@ -112,6 +112,10 @@ def parse_args():
                         "ascending as a fresh allocator hands blocks out, the random draw "
                         "sorted (random's footprint in ascending order), or ascending's "
                         "blocks permuted (ascending's footprint in random order)")
+    p.add_argument("--c2-order", default="random", choices=["random", "ascending"],
+                   help="c2: block assignment: a random permutation of the pool (the "
+                        "config), or ascending as a fresh allocator hands blocks out (the "
+                        "gather then reads the pool front to back)")
     p.add_argument("--c3-seqs", type=int, default=16,
                    help="c3: 2048-token chunks per write (pool 512 blocks per chunk)")
     p.add_argument("--sweep", default=None, choices=["c3"],
@@ -175,7 +179,9 @@ class Built:
 
 def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                  write_entry="launch", fp8="e4m3", scales="tensor", layout=None,
-                 heads=None, c3_seqs=16, c3_order="random", c3_gathers=False) -> Built:
+                 heads=None, c3_seqs=16, c3_order="random", c3_gathers=False,
+                 c2_order="random") -> Built:
+    import numpy as np
     import torch
 
     from kvx_amd import abi, paged, workloads as W
@@ -186,6 +192,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
            DType.F8_E4M3: torch.float8_e4m3fn, DType.F8_E5M2: torch.float8_e5m2}
     if name == "c3":
         w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order)
+    elif name == "c2":
+        w = W.c2_llama8b_decode(order=c2_order)
     else:
         w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
@@ -364,12 +372,20 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                 vs = paged.Scales(vals[1].float().contiguous(), gran)
             keep += [ks, vs]
         step = []
+        pools = []
         for _ in range(layers):
             pc, gc = cache_for(w)
             sigma = w.notes.get("io_sigma", 1.0)
             step.append(write_launch(pc, rows(w, sigma), rows(w, sigma), ks, vs))
             step.append(gather_launch(gc, ko, vo, ks, vs))
+            pools.append((gc.key_cache, gc.value_cache))
         steps.append(step)
+        if (table_fmt == "packed" and w.cache_dtype == w.io_dtype
+                and w.k_layout == w.v_layout == Layout.BLOCK_NHD):
+            # the gather's valid rows are a plain copy's worth of each pool
+            n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
+            extra["pool_copy"] = (pools, (ko, vo), int(n.sum()) * w.heads * w.head_dim
+                                  * W.dtype_bytes(w.cache_dtype))
         cfg = {"layers": layers}
     elif name == "c3":
         # four rotating buffer sets (> the 256 MB Infinity Cache)
@@ -393,6 +409,10 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
         keep += [ko, vo]
         steps.append([write_launch(pc, rows(w), rows(w)), gather_launch(gc, ko, vo)])
         cfg = {"layers": 1, "pool_bytes": 2 * pc.key_cache.numel() * pc.key_cache.element_size()}
+        if table_fmt == "packed" and w.k_layout == w.v_layout == Layout.BLOCK_NHD:
+            n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
+            extra["pool_copy"] = ([(gc.key_cache, gc.value_cache)], (ko, vo),
+                                  int(n.sum()) * w.heads * w.head_dim * 2)
     torch.cuda.synchronize()
     if table_fmt != "packed":
         w.name = f"{w.name}_{table_fmt}"
@@ -465,9 +485,12 @@ def summarize(ms_total, timed, K):
         med_ms = statistics.median(ms)
         nbytes = lst[0][1].nbytes
         gbps = nbytes / (mean_ms / 1e3) / 1e9
+        per_step = max(1, len(ms) // K)  # launches of this kind per step: c1/c2/c4 layers
         kernels[kind] = {
             "launches": len(ms), "mean_ms": round(mean_ms, 5),
             "median_ms": round(med_ms, 5),
+            "by_position_ms": [round(statistics.fmean(ms[j::per_step]), 5)
+                               for j in range(per_step)],
             "bytes_per_launch": nbytes,
             "GBps": round(gbps, 1),
             "GBps_median": round(nbytes / (med_ms / 1e3) / 1e9, 1),
@@ -572,6 +595,45 @@ class Probe:
         del bufs, sink, src_all, dst_all
         torch.cuda.empty_cache()
         return out
+
+    def pool_copy(self, pools, outs, nbytes, shape, stream, reps=3):
+        """A plain copy of each layer's own K and V pools (their first
+        `nbytes` each) into the gather's output buffers, with the copy
+        shape `shape`: the same bytes through the same physical memory as
+        that layer's gather, front to back.  {bytes per layer, mean / median
+        us over layers, GB/s, frac, us per layer}."""
+        import torch
+
+        k = self.shapes.index(tuple(shape))
+        ko, vo = outs
+        sh = stream.cuda_stream
+        for kc, vc in pools:
+            if min(kc.numel() * kc.element_size(), vc.numel() * vc.element_size(),
+                   ko.numel() * ko.element_size()) < nbytes:
+                raise ValueError("pool copy larger than a pool or the output")
+        per_layer = [[] for _ in pools]
+        for r in range(reps + 1):
+            evs = []
+            for kc, vc in pools:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for src, dst in ((kc, ko), (vc, vo)):
+                    if self.L.kvx_probe_copy(dst.data_ptr(), src.data_ptr(), nbytes, k, sh):
+                        raise RuntimeError("pool copy failed")
+                e1.record(stream)
+                evs.append((e0, e1))
+            torch.cuda.synchronize()
+            if r:  # the first pass warms up
+                for j, (e0, e1) in enumerate(evs):
+                    per_layer[j].append(e0.elapsed_time(e1) * 1e3)
+        us = [statistics.median(x) for x in per_layer]
+        mean_us = statistics.fmean(us)
+        gbps = 4 * nbytes / (mean_us / 1e6) / 1e9
+        return {"bytes_per_launch": 4 * nbytes, "mean_us": round(mean_us, 2),
+                "median_us": round(statistics.median(us), 2), "GBps": round(gbps, 1),
+                "frac": round(gbps / PEAK_HBM_GBS, 4), "shape": list(shape),
+                "by_layer_us": [round(x, 1) for x in us]}
 
 
 # ---------------------------------------------------------------------------
@@ -808,6 +870,19 @@ def roofline_of(summary, workload):
             "frac_median": round(k["GBps_median"] / PEAK_HBM_GBS, 4)}
 
 
+def stream_ceilings(b, nbytes, stream):
+    """The probe's ceilings for `nbytes` per side, plus (NHD copy gathers)
+    the copy of the built config's own pools; holds no reference to the
+    pools past its return, so that the caller's `del` frees them."""
+    probe = Probe()
+    ceiling = probe.ceiling(nbytes, stream)
+    if "pool_copy" in b.extra:
+        pools, outs, n = b.extra["pool_copy"]
+        ceiling["pool_copy"] = probe.pool_copy(pools, outs, n, ceiling["copy"]["shape"],
+                                               stream)
+    return ceiling
+
+
 def run_config(name, dev, stream, K, W, args, cpu: bool, **kw):
     """Build, time and summarise one configuration, then free it."""
     import torch
@@ -824,7 +899,7 @@ def run_config(name, dev, stream, K, W, args, cpu: bool, **kw):
     extras = {}
     if not args.profile_only:
         dom = res["kernels"][res["dominant"]]
-        extras["stream_ceiling"] = Probe().ceiling(dom["bytes_per_launch"] // 2, stream)
+        extras["stream_ceiling"] = stream_ceilings(b, dom["bytes_per_launch"] // 2, stream)
     w, steps = b.w, b.steps
     scales = b.extra.get("scales", (0.01, 0.01))
     del b
@@ -890,8 +965,13 @@ def compact_kernel(k):
 def compact_ceiling(c):
     if c is None:
         return None
-    return {op: {"GBps": c[op]["GBps"], "frac": c[op]["frac"], "shape": c[op]["shape"]}
-            for op in Probe.OPS}
+    out = {op: {"GBps": c[op]["GBps"], "frac": c[op]["frac"], "shape": c[op]["shape"]}
+           for op in Probe.OPS}
+    if "pool_copy" in c:
+        pc = c["pool_copy"]
+        out["pool_copy"] = {"GBps": pc["GBps"], "frac": pc["frac"], "shape": pc["shape"],
+                            "layer_us": [min(pc["by_layer_us"]), max(pc["by_layer_us"])]}
+    return out
 
 
 def compact_cpu(c):
@@ -910,7 +990,9 @@ def compact_config(r):
                        for k, v in r["kernels"].items()},
            "roofline": {x: rf[x] for x in ("kernel", "frac", "frac_median", "traffic")}}
     if r.get("stream_ceiling"):
-        out["ceiling_frac"] = {op: r["stream_ceiling"][op]["frac"] for op in ("copy", "expand")}
+        out["ceiling_frac"] = {op: r["stream_ceiling"][op]["frac"]
+                               for op in ("copy", "expand", "pool_copy")
+                               if op in r["stream_ceiling"]}
     c = r.get("cpu_baseline")
     if c:
         out["cpu_baseline"] = {"value": c["value"], "cores": c["cores"],
@@ -945,7 +1027,7 @@ def main():
     kw = dict(layers_override=args.layers, table_fmt=args.table,
               write_entry=args.write_entry, fp8=args.fp8, scales=args.scales,
               layout=args.layout, heads=args.heads, c3_seqs=args.c3_seqs,
-              c3_order=args.c3_order)
+              c3_order=args.c3_order, c2_order=args.c2_order)
     K, W = args.steps, args.warmup
     cpu = not args.no_cpu_baseline and not args.profile_only
 
@@ -956,7 +1038,7 @@ def main():
     ceiling = graph = None
     if not args.profile_only:
         dom = res["kernels"][res["dominant"]]
-        ceiling = Probe().ceiling(dom["bytes_per_launch"] // 2, stream)
+        ceiling = stream_ceilings(b, dom["bytes_per_launch"] // 2, stream)
         graph = write_graph(b.steps, stream)
     w, cfg = b.w, b.cfg
     scales = b.extra.get("scales", (0.01, 0.01))

@@ -170,7 +170,7 @@ def c1_tinyllama(seed: int = 1) -> Workload:
                     np.full(S, L, np.int32), L, layers=22)
 
 
-def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None):
+def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None, ascending=False):
     lens = rng.integers(lo, hi, size=S, endpoint=True).astype(np.int64)
     need = (lens + bs - 1) // bs
     mbps = (max_len + bs - 1) // bs
@@ -180,6 +180,8 @@ def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None):
         ids = rng.permutation(pool)
     else:
         ids = rng.choice(pool, size=used, replace=False)
+    if ascending:
+        ids = np.sort(ids)  # same draw, handed out in address order
     table = np.full((S, mbps), -1, np.int64)
     at = 0
     for s in range(S):
@@ -188,15 +190,24 @@ def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None):
     return lens, table, pool
 
 
-def c2_llama8b_decode(seed: int = 2, batch: int = 256) -> Workload:
+def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random") -> Workload:
+    """c2; order "random": the sequences' blocks are a random permutation of
+    the pool (the config); "ascending": the same lengths with sequence s
+    taking the next blocks of the pool in address order, as a fresh
+    allocator would hand them out, so that its gather reads the pool front
+    to back."""
+    if order not in ("random", "ascending"):
+        raise ValueError(order)
     rng = np.random.Generator(np.random.PCG64(seed))
     bs, L = 16, 8192
-    lens, table, pool = _decode_tables(rng, batch, 512, 8192, bs, L)
+    lens, table, pool = _decode_tables(rng, batch, 512, 8192, bs, L,
+                                       ascending=order == "ascending")
     pos = lens - 1  # the new token is the last position of each context
     slots = table[np.arange(batch), pos // bs] * bs + pos % bs
     pad = rng.choice(batch, size=int(round(0.05 * batch)), replace=False)
     slots[pad] = -1
-    return Workload("c2_llama3_8b_decode_bf16", seed, 8, 128, bs, pool, DType.BF16,
+    name = "c2_llama3_8b_decode_bf16" + ("" if order == "random" else f"_{order}")
+    return Workload(name, seed, 8, 128, bs, pool, DType.BF16,
                     DType.BF16, Layout.BLOCK_NHD, Layout.BLOCK_NHD, 8,
                     slots.astype(np.int64), None, table.astype(np.int32),
                     lens.astype(np.int32), L, layers=32,

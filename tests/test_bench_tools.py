@@ -62,3 +62,19 @@ def test_probe_shapes():
     shapes = bench.Probe().shapes
     assert (64, 1) in shapes and (256, 1) in shapes
     assert all(t in (64, 128, 256, 512, 1024) and u in (1, 2, 4) for t, u in shapes)
+
+
+def test_compact_line_keeps_ceiling_and_pool_copy():
+    op = {"GBps": 6600.0, "frac": 0.825, "shape": [64, 1], "mean_us": 1.0,
+          "GBps_by_shape": {"64x1": 6600.0}, "bytes_per_launch": 32}
+    full = {k: dict(op) for k in bench.Probe.OPS}
+    full["buffers"], full["footprint_bytes"] = 4, 128
+    full["pool_copy"] = {"GBps": 6700.0, "frac": 0.8375, "shape": [64, 1],
+                         "by_layer_us": [1401.0, 1369.0, 1380.5], "mean_us": 1383.5}
+    c = bench.compact_ceiling(full)
+    assert set(c) == set(bench.Probe.OPS) | {"pool_copy"}
+    assert c["pool_copy"]["layer_us"] == [1369.0, 1401.0]
+    assert "GBps_by_shape" not in c["copy"] and "by_layer_us" not in c["pool_copy"]
+    del full["pool_copy"]
+    assert set(bench.compact_ceiling(full)) == set(bench.Probe.OPS)
+    assert bench.compact_ceiling(None) is None
