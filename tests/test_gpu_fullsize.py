@@ -278,6 +278,46 @@ def test_c5_full_long_context_200gb_pool():
     ragged_equals_packed(pc, w, ko, vo, kb, vb)
 
 
+@pytest.mark.parametrize("cfg", ["c2", "c5"])
+def test_one_kv_head_rank_shape(cfg):
+    """One tensor-parallel rank's share of the c2 / c5 caches: one KV head of
+    eight (Llama-3-70B at TP8), so 256-byte rows and 16 chunks per row, with
+    the 8-head workload's tables, lengths and slots.  Write, then gather;
+    checked row by row against the slots and against indexing, by the round
+    trip of the written tokens, and against the RAGGED form of the table."""
+    w = workloads.CONFIGS[cfg]()
+    w.heads = 1
+    H, D, bs = w.heads, w.head_dim, w.block_size
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.bfloat16, DEV)
+    pc.key_cache.normal_()
+    pc.value_cache.normal_()
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    kw = {"tokens_per_seq": w.tokens_per_seq} if w.tokens_per_seq else {}
+    assert paged.write_kv(pc, key, val, slots, **kw) == Status.OK
+    torch.cuda.synchronize()
+    ok = slots >= 0
+    blk, off = slots[ok] // bs, slots[ok] % bs
+    assert torch.equal(i16(pc.key_cache[blk, off]), i16(key[ok]))
+    assert torch.equal(i16(pc.value_cache[blk, off]), i16(val[ok]))
+
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16, 3)
+    kb, vb = ko.clone(), vo.clone()
+    lens = torch.tensor(w.seq_lens, device=DEV)
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV), lens, L) == Status.OK
+    torch.cuda.synchronize()
+    # the written tokens are the last rows of their sequences
+    tps = w.tokens_per_seq or 1
+    seq = torch.arange(S, device=DEV).repeat_interleave(tps)
+    pos = (lens.long()[seq] - tps + torch.arange(tps, device=DEV).repeat(S))
+    assert torch.equal(i16(ko[seq[ok], pos[ok]]), i16(key[ok]))
+    assert torch.equal(i16(vo[seq[ok], pos[ok]]), i16(val[ok]))
+    check_gather_against_indexing(pc, w, ko, vo, kb, vb)
+    ragged_equals_packed(pc, w, ko, vo, kb, vb)
+
+
 def test_token_write_grid_stride_loop():
     """A write of more rows than the per-token kernel's grid holds (65536
     workgroups of 4 waves, one row per wave): its waves loop over the
