@@ -116,6 +116,10 @@ def parse_args():
                    help="c2: block assignment: a random permutation of the pool (the "
                         "config), or ascending as a fresh allocator hands blocks out (the "
                         "gather then reads the pool front to back)")
+    p.add_argument("--c3-shift", type=int, default=0,
+                   help="c3: every chunk starts this many tokens (0-15) into its first "
+                        "block, as a chunked prefill continuing a chunk that ended inside "
+                        "a block")
     p.add_argument("--c3-seqs", type=int, default=16,
                    help="c3: 2048-token chunks per write (pool 512 blocks per chunk)")
     p.add_argument("--sweep", default=None, choices=["c3"],
@@ -180,7 +184,7 @@ class Built:
 def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                  write_entry="launch", fp8="e4m3", scales="tensor", layout=None,
                  heads=None, c3_seqs=16, c3_order="random", c3_gathers=False,
-                 c2_order="random") -> Built:
+                 c2_order="random", c3_shift=0) -> Built:
     import numpy as np
     import torch
 
@@ -191,7 +195,7 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     tdt = {DType.BF16: torch.bfloat16, DType.F16: torch.float16,
            DType.F8_E4M3: torch.float8_e4m3fn, DType.F8_E5M2: torch.float8_e5m2}
     if name == "c3":
-        w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order)
+        w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order, shift=c3_shift)
     elif name == "c2":
         w = W.c2_llama8b_decode(order=c2_order)
     else:
@@ -1027,7 +1031,7 @@ def main():
     kw = dict(layers_override=args.layers, table_fmt=args.table,
               write_entry=args.write_entry, fp8=args.fp8, scales=args.scales,
               layout=args.layout, heads=args.heads, c3_seqs=args.c3_seqs,
-              c3_order=args.c3_order, c2_order=args.c2_order)
+              c3_order=args.c3_order, c2_order=args.c2_order, c3_shift=args.c3_shift)
     K, W = args.steps, args.warmup
     cpu = not args.no_cpu_baseline and not args.profile_only
 

@@ -751,16 +751,20 @@ __device__ __forceinline__ void group_runs(const WriteArgs &a, int64_t t0, int b
   }
 }
 
-// Run ownership for block sizes up to 32 (2 * bs slots fit one wave).  A
-// run here is a maximal stretch of tokens whose slots are valid, lie in one
-// block and follow each other (slot = previous slot + 1).  The workgroups
-// of group [t0, t0 + bs) own the runs that START in it; such a run ends
-// before t0 + 2 * bs - 1, since it holds at most bs tokens.  Every token
-// then has exactly one owner, and a prefill chunk that starts inside a
-// block has each of its blocks written whole by one workgroup instead of
-// split between two (whose shared 16-byte chunks would then be stored
-// piece by piece).  A whole block in order (write_tile_block's case) is one
-// run starting at t0 either way.
+// Run ownership for block sizes up to 32 (2 * bs slots fit one wave), for
+// tensors whose blocks are not row-major.  A run here is a maximal stretch
+// of tokens whose slots are valid, lie in one block and follow each other
+// (slot = previous slot + 1).  The workgroups of group [t0, t0 + bs) own
+// the runs that START in it; such a run ends before t0 + 2 * bs - 1, since
+// it holds at most bs tokens.  Every token then has exactly one owner, and
+// a prefill chunk that starts inside a block has each of its blocks written
+// whole by one workgroup instead of split between two, whose writes would
+// share cache lines (or 16-byte chunks, stored piece by piece).  On MI355X
+// (c3's size, x-packed K, chunks starting k = 1, 11 or 15 tokens into a
+// block) splitting the x-packed blocks measured 79 us against 55-62 us for
+// owned runs; only k = 8, whose halves are whole 128-byte lines, gained.
+// A whole block in order (write_tile_block's case) is one run starting at
+// t0 either way.
 //
 // Wave 0 loads the slots of tokens t0 - 1 .. t0 + 2 * bs - 2, one per lane,
 // and writes the owned runs to runs[] (LDS); *nruns = their count, or 0
@@ -825,15 +829,20 @@ __device__ __forceinline__ void owned_runs(const WriteArgs &a, int64_t t0, int b
   }
 }
 
-// Per-token write of the tokens [t0, t0 + bs) of a group that does not fill
-// a block, shared by `nwaves` waves: this workgroup's wave w is wave
-// wave0 + w of them and takes tokens wave0 + w, wave0 + w + nwaves, ...
+// Per-token write of one tensor (V when v, else K) for the tokens
+// [t0, t0 + n) of a group that does not fill a block, shared by `nwaves`
+// waves: this workgroup's wave w is wave wave0 + w of them and takes tokens
+// wave0 + w, wave0 + w + nwaves, ...
 template <class Op, bool IDX>
-__device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t0, int bs,
-                                                   float ks, float vs, int wave0, int nwaves) {
+__device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t0, int n, bool v,
+                                                   float uniform, int wave0, int nwaves) {
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
-  for (int o = wave0 + wave; o < bs; o += nwaves) {
+  const GeomBytes &g = v ? a.gv : a.gk;
+  const ScaleRef &sr = v ? a.vsc : a.ksc;
+  const char *io = v ? a.src_v : a.src_k;
+  char *cache = v ? a.dst_v : a.dst_k;
+  for (int o = wave0 + wave; o < n; o += nwaves) {
     const int64_t t = t0 + o;
     if (t >= a.num_tokens) break;
     const int64_t slot = load_index(a.slots, t, a.slot_is64);
@@ -841,24 +850,14 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
     int64_t b, off;
     split_slot(slot, a.block_size, b, off);
     if (b >= a.num_blocks) continue;
-    const char *sk = a.src_k + t * a.row_bytes;
-    const char *sv = a.src_v + t * a.row_bytes;
-    char *dk = a.dst_k + b * a.gk.s_block + off * a.gk.s_off;
-    char *dv = a.dst_v + b * a.gv.s_block + off * a.gv.s_off;
+    const char *src = io + t * a.row_bytes;
+    char *dst = cache + b * g.s_block + off * g.s_off;
     for (int c = lane; c < a.nchunks; c += kWave) {
       const uint32_t e = (uint32_t)c * (uint32_t)a.chunk_elems;
-      const Raw<Op::kSrc> xk = ld<Op::kSrc>(sk + (int64_t)c * Op::kSrc);
-      const Raw<Op::kSrc> xv = ld<Op::kSrc>(sv + (int64_t)c * Op::kSrc);
-      float sk = ks;
-      float sv = vs;
-      if constexpr (Op::kScaled && IDX) {
-        sk = scale_at(a.ksc, ks, b, e, (uint32_t)a.head_dim);
-        sv = scale_at(a.vsc, vs, b, e, (uint32_t)a.head_dim);
-      }
-      st<Op::kDst, kWriteNtStore>(dk + chunk_off(a.gk, e, (uint32_t)a.head_dim),
-                                  Op::apply(xk, sk));
-      st<Op::kDst, kWriteNtStore>(dv + chunk_off(a.gv, e, (uint32_t)a.head_dim),
-                                  Op::apply(xv, sv));
+      float sc = uniform;
+      if constexpr (Op::kScaled && IDX) sc = scale_at(sr, uniform, b, e, (uint32_t)a.head_dim);
+      st<Op::kDst, kWriteNtStore>(dst + chunk_off(g, e, (uint32_t)a.head_dim),
+                                  Op::apply(ld<Op::kSrc>(src + (int64_t)c * Op::kSrc), sc));
     }
   }
 }
@@ -878,8 +877,8 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
 //            stores it; chunks holding rows outside the run store those
 //            rows' pieces only.
 // A row-major tensor copies its rows straight through.  Any other group is
-// written token by token (K and V rows together), its tokens spread over
-// the waves of all 2 * tiles workgroups of the group.
+// written token by token, each tensor's tokens spread over the waves of
+// that tensor's `tiles` workgroups of the group.
 struct WriteTileArgs {
   int32_t tiles;          // tiles per block: cache row bytes / tw
   int32_t tw_log2;        // tile width, cache bytes per row
@@ -1065,11 +1064,15 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
 // them with a ballot, so the slot latency overlaps the data loads and no
 // barrier is needed to share the test.  Every wave reaches the same answer
 // from the same slots.
-// Shifted (block sizes up to 32, where owned_runs decides ownership): a
-// prefill chunk that starts inside a block makes the group's first k
-// tokens continue the run of token t0 - 1 and its next bs tokens fill the
-// following block; the group then owns exactly that block (one run
-// starting at t0 + k).  k follows from the first test's slot of t0, so the
+// Row-major split (row-major tensors, whose groups write their own
+// tokens): the group's first k tokens end one block in order and the rest
+// start another, as in a prefill chunk that starts inside a block; the
+// loaded rows go straight to both blocks.
+// Shifted (other layouts, block sizes up to 32, where owned_runs decides
+// ownership): a prefill chunk that starts inside a block makes the group's
+// first k tokens continue the run of token t0 - 1 and its next bs tokens
+// fill the following block; the group then owns exactly that block (one
+// run starting at t0 + k).  k follows from the first test's slot of t0, so the
 // loads of rows t0 + k .. are issued together with the slots that confirm
 // it, instead of after the run analysis and a barrier.
 // Returns false, having stored nothing, when the group is neither (or is
@@ -1129,6 +1132,43 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   const int64_t first = uniform64(slot);
   int64_t block = first >> wt.bs_log2;
   const bool in_order = lane >= bs || slot == first + lane;
+  if (run_log2 < 0 && (__ballot(!in_order) != 0 || (first & (bs - 1)) != 0)) {
+    // Row-major split: tokens t0 .. t0 + k - 1 end block A (offsets
+    // bs - k .. bs - 1) and t0 + k .. t0 + bs - 1 start block B; the rows
+    // loaded above are this group's own, stored straight to both blocks.
+    if (first < 0 || block >= a.num_blocks || (first & (bs - 1)) == 0) return false;
+    const int32_t k = bs - (int32_t)(first & (bs - 1));
+    const int64_t f2 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(
+                                      __shfl((int)(slot >> 32), k)) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readfirstlane(__shfl((int)slot, k)));
+    const int64_t block_b = f2 >> wt.bs_log2;
+    const bool bad = lane < k ? slot != first + lane : (lane < bs && slot != f2 + (lane - k));
+    if (__ballot(bad) != 0 || f2 < 0 || (f2 & (bs - 1)) != 0 || block_b >= a.num_blocks)
+      return false;
+    const ScaleRef &sr = v ? a.vsc : a.ksc;
+    const uint32_t hd = (uint32_t)a.head_dim;
+    const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
+    const int32_t rbc = (int32_t)wt.tiles << wt.tw_log2;  // cache bytes of a row
+    char *base = v ? a.dst_v : a.dst_k;
+    const int64_t sb = v ? a.gv.s_block : a.gk.s_block;
+    // byte m of the group's rows: row m / rbc of the group is row
+    // bs - k + m / rbc of block A, or row m / rbc - k of block B
+    const int64_t at_a = block * sb + (int64_t)(bs - k) * rbc;
+    const int64_t at_b = block_b * sb - (int64_t)k * rbc;
+#pragma unroll
+    for (int q = 0; q < kTileLoads; ++q) {
+      const int32_t u = tid + q * kBlockThreads;
+      if (u < total) {
+        const int32_t m = tile * region + (u << kDstLog2);
+        const bool in_a = m < k * rbc;
+        float sc = uniform;
+        if constexpr (Op::kScaled && IDX)
+          sc = scale_in_rows(sr, uniform, in_a ? block : block_b, elem(u), re, hd);
+        st<Op::kDst, kWriteNtStore>(base + ((in_a ? at_a : at_b) + m), Op::apply(x[q], sc));
+      }
+    }
+    return true;
+  }
   if (__ballot(!in_order) != 0 || first < 0 || (first & (bs - 1)) != 0 ||
       block >= a.num_blocks) {
     // Shifted: tokens t0 .. t0 + k - 1 hold first, first + 1, ... up to the
@@ -1207,10 +1247,16 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
     vs = a.vsc.p[0];
   }
   if (write_tile_block<Op, IDX>(a, wt, t0, tile, v, v ? vs : ks, lds)) return;
-  // Block sizes up to 32: the runs that start in the group (owned_runs);
-  // 64: the group's own tokens split into runs (group_runs).
+  // Which tokens this tensor's workgroups of the group write.  Row-major
+  // blocks (NHD) hold whole rows: each group writes its own tokens, split
+  // into runs (group_runs), so a block that a prefill chunk starts inside is
+  // written in two parts of whole rows.  Other layouts interleave a block's
+  // rows in 1-16 byte pieces; there, for block sizes up to 32, the group in
+  // which a run starts writes all of it (owned_runs), so that no cache line
+  // of a block is written in parts by two workgroups.
   __shared__ int32_t s_own[2];
-  if (wt.bs_log2 <= 5) {
+  const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
+  if (wt.bs_log2 <= 5 && run_log2 >= 0) {
     owned_runs(a, t0, wt.bs_log2, s_runs, &s_nruns, s_own);
   } else {
     group_runs(a, t0, wt.bs_log2, s_runs, &s_nruns);
@@ -1222,9 +1268,8 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
   __syncthreads();
   const int32_t nruns = s_nruns;
   if (nruns == 0) {
-    write_group_tokens<TokOp, IDX>(a, t0 + s_own[0], s_own[1] - s_own[0], ks, vs,
-                                   ((int)blockIdx.y * wt.tiles + tile) * kWavesPerBlock,
-                                   2 * wt.tiles * kWavesPerBlock);
+    write_group_tokens<TokOp, IDX>(a, t0 + s_own[0], s_own[1] - s_own[0], v, v ? vs : ks,
+                                   tile * kWavesPerBlock, wt.tiles * kWavesPerBlock);
     return;
   }
   for (int32_t i = 0; i < nruns; ++i) {

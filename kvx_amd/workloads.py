@@ -215,7 +215,7 @@ def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random") ->
 
 
 def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs: int = 16,
-                       order: str = "random") -> Workload:
+                       order: str = "random", shift: int = 0) -> Workload:
     """c3; `seqs` chunks of 2048 tokens over a pool of 512 blocks per
     sequence (16 and 8192 as configured).  order "random": the sequences'
     blocks are a seeded random draw from the pool; "ascending": sequence s
@@ -223,11 +223,16 @@ def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs:
     would hand them out.  Two orders separate what random blocks change:
     "sorted" is the random draw in ascending order (random's footprint,
     ascending's order), "compact" a random permutation of ascending's
-    blocks (ascending's footprint, random order)."""
+    blocks (ascending's footprint, random order).  shift > 0: every chunk
+    covers positions shift .. shift + 2047 of its sequence, so it starts
+    inside its first block (as a chunked prefill does after a chunk that
+    ended inside a block) and takes one more block."""
+    if not 0 <= shift < 16:
+        raise ValueError(shift)
     rng = np.random.Generator(np.random.PCG64(seed))
     S, chunk, bs = seqs, 2048, 16
     pool = 512 * S
-    mbps = chunk // bs
+    mbps = (shift + chunk + bs - 1) // bs
     draw = rng.permutation(pool)[: S * mbps]
     if order == "random":
         ids = draw
@@ -240,17 +245,19 @@ def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs:
     else:
         raise ValueError(order)
     table = ids.reshape(S, mbps).astype(np.int32)
-    pos = np.arange(chunk)
+    pos = shift + np.arange(chunk)
     slots = np.concatenate([_slots_for(pos, table[s], bs) for s in range(S)])
     name = "c3_llama3_8b_prefill_packedK_bf16"
     if S != 16:
         name += f"_s{S}"
     if order != "random":
         name += f"_{order}"
+    if shift:
+        name += f"_shift{shift}"
     return Workload(name, seed, 8, 128, bs, pool,
                     DType.BF16, DType.BF16, Layout.BLOCK_HND_PACKED, Layout(v_layout), 8,
-                    slots.astype(np.int64), chunk, table, np.full(S, chunk, np.int32),
-                    chunk)
+                    slots.astype(np.int64), chunk, table,
+                    np.full(S, shift + chunk, np.int32), shift + chunk)
 
 
 def c4_llama8b_fp8(seed: int = 4, batch: int = 128) -> Workload:

@@ -39,6 +39,7 @@ CASES = [
     (DType.BF16, "bhod", None, "bhdo", None, 64, 8, 16),  # HND with 32-byte runs
     (DType.F16, "bhdo", None, "bhdo", None, 2, 4, 32),    # block_size 2
     (DType.BF16, "bohd", None, "bhdo", None, 4, 1, 64),   # one head
+    (DType.BF16, "bhpox", 8, "bohd", None, 16, 8, 128),   # c3's pair: 16-byte runs / row-major V
 ]
 
 
