@@ -429,3 +429,35 @@ def test_tiles_quantizing_write_indexed_scales(kind, layouts):
 
     check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16,
                 cache_dtype=DType.F8_E4M3, k_scale=arg(), v_scale=arg())
+
+
+# (K order, K x, V order, V x): at least one tensor row-major ("bohd", NHD)
+_ROW_MAJOR_PAIRS = [("bohd", None, "bhpox", 8), ("bhpox", 8, "bohd", None),
+                    ("bohd", None, "bhdo", None), ("bhdo", None, "bohd", None),
+                    ("bohd", None, "bohd", None)]
+
+
+@pytest.mark.parametrize("seed", range(15))
+def test_tiles_write_row_major_ownership(seed):
+    """Seeded prefill chunks (random starts inside blocks, random lengths,
+    spoiled slots, both write entries) into caches where a row-major tensor
+    is written group by group, its own tokens only, beside a partner whose
+    runs belong to the group they start in: the whole cache must equal the
+    oracle's, every untouched byte included."""
+    rng = np.random.default_rng(900 + seed)
+    gen = torch.Generator().manual_seed(900 + seed)
+    ko_, kx, vo_, vx = _ROW_MAJOR_PAIRS[seed % len(_ROW_MAJOR_PAIRS)]
+    bs = int(rng.choice([4, 8, 16, 32, 64]))
+    H, D = [(8, 128), (4, 64), (2, 32)][seed % 3]
+    dt = [DType.BF16, DType.F16, DType.F8_E4M3][(seed // 3) % 3]
+    nb = 128
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    slots = _unaligned_chunk_slots(gen, nb, bs, seqs=5, spoil=int(rng.integers(0, 4)))
+    T = slots.numel()
+    io = DType.BF16 if dt == DType.F8_E4M3 else dt
+    key = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+    val = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+    scales = dict(k_scale=0.013, v_scale=0.007) if dt == DType.F8_E4M3 else {}
+    entry = "abi" if ko_ == vo_ and seed % 2 == 0 else "launch"  # seeds 4 and 14
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=dt,
+                entry=entry, **scales)
