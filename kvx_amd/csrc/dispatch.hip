@@ -114,8 +114,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   const int64_t D = p.head_dim;
   const int64_t row_cache = H * D * cs;
   const int bs_log2 = log2_exact(bs);
-  const int row_log2 = log2_exact(row_cache);
-  if (bs_log2 < 0 || row_log2 < 0 || row_cache < 16) return false;
+  if (bs_log2 < 0 || row_cache < 16) return false;
   const Geom *g[2] = {&p.gk, &p.gv};
   const void *src[2] = {p.src_k, p.src_v};
   void *dst[2] = {p.dst_k, p.dst_v};
@@ -142,7 +141,15 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   }
   if (!transposed) return false;  // row-major pairs: the flat kernels
   if ((D * cs) % src_chunk != 0) return false;  // chunks never straddle heads
-  int64_t tw = row_cache;
+  // Tile width: a power of two that divides the row and holds whole runs.
+  // A row that is not a power of two (6 or 12 heads, say) makes several
+  // tiles of its largest power-of-two divisor, when that still fills a tile:
+  // on MI355X (c2's table) HND gathers of 6 x 128 and 12 x 64 bf16 heads
+  // measured 0.676 of peak in 8 KiB tiles against 0.63 in gather_rows_kernel,
+  // 3 x 128 heads 0.587 in 4 KiB tiles against 0.623.
+  int64_t tw = row_cache & -row_cache;
+  if (tw < min_tw) return false;
+  if ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_TILE_BYTES) return false;
   while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
@@ -210,7 +217,7 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   const int64_t row_cache = H * D * cs;
   const int bs_log2 = log2_exact(bs);
   if (bs_log2 < 0 || bs > kWave || p.num_tokens < bs) return false;
-  if (log2_exact(row_cache) < 0 || row_cache < 16) return false;
+  if (row_cache < 16) return false;
   const int src_chunk = p.conv == kConvQuant ? 8 * is : 16;
   if (p.conv == kConvQuant && D % 8 != 0) return false;
   const Geom *g[2] = {&p.gk, &p.gv};
@@ -235,7 +242,13 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   if (!transposed) return false;
   const int64_t tile_bytes =
       p.conv == kConvQuant ? KVX_QUANT_TILE_BYTES : KVX_WRITE_TILE_BYTES;
-  int64_t tw = row_cache;
+  // as in plan_tiles: a power-of-two tile width that divides the row, and
+  // a full copy tile for a row that is not a power of two (c3's size into
+  // HND caches of 6 x 128 or 12 x 64 bf16 heads: 0.527 of peak against 0.43
+  // per token)
+  int64_t tw = row_cache & -row_cache;
+  if (tw < min_tw) return false;
+  if ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_WRITE_TILE_BYTES) return false;
   while (tw * bs > tile_bytes && tw / 2 >= min_tw) tw /= 2;
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;

@@ -62,17 +62,21 @@ constexpr int kTilePad = 16;
 #endif
 // Contiguous-block gather (gather_flat_kernel): threads per workgroup (also
 // those of the row-dense write, write_flat_kernel) and cache bytes per
-// tensor per workgroup.  A block's valid chunks are split
-// into power-of-two ranges of about this size, so that each lane copies one
-// 16-byte chunk of K and one of V.  On MI355X (c2, same box) 128 threads and
-// 2 KiB measured 3.7% faster than 256 threads and 4 KiB, 64 threads and
-// 1 KiB 1% slower (2% faster on c5's 64 KiB blocks); tiles that leave a
-// lane one chunk, or give it more than two, were 5-40% slower.
+// tensor per workgroup.  A block's valid chunks are split into a
+// power-of-two number of equal ranges of at most this size, so that each
+// lane copies one 16-byte chunk of K and one of V (2 KiB for power-of-two
+// rows).  On MI355X (c2, same box) 128 threads and 2 KiB measured 3.7%
+// faster than 256 threads and 4 KiB, 64 threads and 1 KiB 1% slower (2%
+// faster on c5's 64 KiB blocks); tiles that leave a lane one chunk, or give
+// it more than two, were 5-40% slower.  The 3 KiB bound changes only rows
+// whose chunk count is not a power of two: head_dim 96 or 80 (8 heads, bf16)
+// then splits into 192- or 160-chunk ranges instead of 96 or 80, 0.670 ->
+// 0.697 and 0.657 -> 0.693 of peak at c2's table.
 #ifndef KVX_FLAT_THREADS
 #define KVX_FLAT_THREADS 128
 #endif
 #ifndef KVX_FLAT_TILE_BYTES
-#define KVX_FLAT_TILE_BYTES 2048
+#define KVX_FLAT_TILE_BYTES 3072
 #endif
 // Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about this
 // many cache bytes of each tensor, in 256-thread workgroups.  The RAGGED

@@ -40,6 +40,12 @@ CASES = [
     (DType.F16, "bhdo", None, "bhdo", None, 2, 4, 32),    # block_size 2
     (DType.BF16, "bohd", None, "bhdo", None, 4, 1, 64),   # one head
     (DType.BF16, "bhpox", 8, "bohd", None, 16, 8, 128),   # c3's pair: 16-byte runs / row-major V
+    # rows whose bytes are not a power of two: several power-of-two tiles per row
+    (DType.BF16, "bhod", None, "bhod", None, 16, 6, 128),  # HND, 6 heads: 3 tiles of 512 B
+    (DType.BF16, "bhpox", 8, "bohd", None, 16, 12, 64),   # x-packed K / NHD V, 1536-byte rows
+    (DType.F8_E4M3, "bhod", None, "bhdo", None, 16, 12, 128),  # FP8 HND / token-innermost
+    (DType.F32, "bhdo", None, "bhod", None, 64, 5, 32),   # 640-byte rows: 5 tiles of 128 B
+    (DType.F16, "bhpox", 8, "bohd", None, 16, 3, 64),     # 384-byte rows: tiles too small
 ]
 
 
