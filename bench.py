@@ -96,8 +96,12 @@ def parse_args():
                         "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
                         "paged-attention pair (PACKED / RAGGED tables only)")
     p.add_argument("--heads", type=int, default=None,
-                   help="c2 / c5: KV heads per GPU (one tensor-parallel rank's shard: "
-                        "8 / TP); the block table, lengths and slots are unchanged")
+                   help="c2 / c3 / c5: KV heads per GPU (one tensor-parallel rank's shard is "
+                        "8 / TP; 6 or 12 are other models' counts); the block table, "
+                        "lengths and slots are unchanged")
+    p.add_argument("--head-dim", type=int, default=None,
+                   help="c2 / c3 / c5: elements per head (a multiple of 8, e.g. 96 or 80); "
+                        "heads x head_dim may not exceed the config's 8 x 128")
     p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
                    help="c4: FP8 format of the cache")
     p.add_argument("--scales", default="tensor",
@@ -181,10 +185,30 @@ class Built:
         self.extra = extra or {}
 
 
+def reshape_rows(w, name, heads=None, head_dim=None):
+    """--heads / --head-dim: give c2's, c3's or c5's rows another head count or head size
+    (the block table, lengths and slots stay); the row may not outgrow the config's,
+    so the pools fit wherever the config does."""
+    if heads is None and head_dim is None:
+        return
+    h = w.heads if heads is None else heads
+    d = w.head_dim if head_dim is None else head_dim
+    if name not in ("c2", "c3", "c5"):
+        raise SystemExit("--heads / --head-dim apply to c2, c3 and c5")
+    if h <= 0 or d <= 0 or d % 8 != 0 or h * d > w.heads * w.head_dim:
+        raise SystemExit("--heads and --head-dim: positive, head_dim a multiple of 8, "
+                         f"heads x head_dim at most {w.heads} x {w.head_dim}")
+    if heads is not None:
+        w.name = f"{w.name}_h{h}"
+    if head_dim is not None:
+        w.name = f"{w.name}_d{d}"
+    w.heads, w.head_dim = h, d
+
+
 def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                  write_entry="launch", fp8="e4m3", scales="tensor", layout=None,
                  heads=None, c3_seqs=16, c3_order="random", c3_gathers=False,
-                 c2_order="random", c3_shift=0) -> Built:
+                 c2_order="random", c3_shift=0, head_dim=None) -> Built:
     import numpy as np
     import torch
 
@@ -210,11 +234,7 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
         w.name = w.name.replace("fp8_e4m3", "fp8_e5m2")
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
-    if heads is not None:
-        if name not in ("c2", "c5") or heads <= 0 or w.heads % heads != 0:
-            raise SystemExit("--heads applies to c2 and c5 and must divide 8")
-        w.heads = heads
-        w.name = f"{w.name}_h{heads}"
+    reshape_rows(w, name, heads, head_dim)
     if layout is not None:
         if name not in ("c2", "c5"):
             raise SystemExit("--layout applies to c2 and c5")
@@ -1031,7 +1051,8 @@ def main():
     kw = dict(layers_override=args.layers, table_fmt=args.table,
               write_entry=args.write_entry, fp8=args.fp8, scales=args.scales,
               layout=args.layout, heads=args.heads, c3_seqs=args.c3_seqs,
-              c3_order=args.c3_order, c2_order=args.c2_order, c3_shift=args.c3_shift)
+              c3_order=args.c3_order, c2_order=args.c2_order, c3_shift=args.c3_shift,
+              head_dim=args.head_dim)
     K, W = args.steps, args.warmup
     cpu = not args.no_cpu_baseline and not args.profile_only
 

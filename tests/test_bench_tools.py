@@ -82,3 +82,23 @@ def test_compact_line_keeps_ceiling_and_pool_copy():
     del full["pool_copy"]
     assert set(bench.compact_ceiling(full)) == set(bench.Probe.OPS)
     assert bench.compact_ceiling(None) is None
+
+
+def test_reshape_rows():
+    from kvx_amd import workloads as W
+
+    w = W.CONFIGS["c5"]()
+    name = w.name
+    bench.reshape_rows(w, "c5")
+    assert (w.heads, w.head_dim, w.name) == (8, 128, name)
+    bench.reshape_rows(w, "c5", heads=6)
+    assert (w.heads, w.head_dim, w.name) == (6, 128, name + "_h6")
+    w = W.CONFIGS["c5"]()
+    bench.reshape_rows(w, "c5", heads=12, head_dim=64)
+    assert (w.heads, w.head_dim, w.name) == (12, 64, name + "_h12_d64")
+    w = W.c3_llama8b_prefill()
+    bench.reshape_rows(w, "c3", heads=6)
+    assert (w.heads, w.head_dim) == (6, 128)
+    for name_, h, d in [("c4", 4, None), ("c5", 12, 128), ("c5", None, 84), ("c5", 0, None)]:
+        with pytest.raises(SystemExit):
+            bench.reshape_rows(W.CONFIGS["c5"](), name_, h, d)
