@@ -104,6 +104,27 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 #ifndef KVX_TILE_BYTES
 #define KVX_TILE_BYTES 8192
 #endif
+// Tiles whose width is not a power of two: at most KVX_ODD_TILE_BYTES of
+// cache bytes per tensor, at least KVX_ODD_TILE_MIN.
+#ifndef KVX_ODD_TILE_BYTES
+#define KVX_ODD_TILE_BYTES 12288
+#endif
+#ifndef KVX_ODD_TILE_MIN
+#define KVX_ODD_TILE_MIN 4096
+#endif
+
+int64_t gcd64(int64_t a, int64_t b) {
+  while (b != 0) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// div_magic's multiplier for divisor d >= 2: ceil(2^32 / d).
+uint32_t magic_for(int64_t d) { return (uint32_t)(((uint64_t(1) << 32) + (uint64_t)d - 1) / (uint64_t)d); }
+
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
   const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
@@ -119,16 +140,25 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   const void *src[2] = {p.src_k, p.src_v};
   void *dst[2] = {p.dst_k, p.dst_v};
   int run_log2[2];
-  bool transposed = false;
+  int64_t run_bytes[2] = {0, 0};
+  bool transposed = false, odd_run = false;
   int64_t min_tw = 16;
+  int64_t unit = 16;  // a tile width holds whole runs and 16-byte chunks
   for (int i = 0; i < 2; ++i) {
     const int64_t w = dense_run_elems(*g[i], bs, H, D);
     if (w < 0) return false;
     run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
     if (w != H * D) {
-      if (run_log2[i] < 0) return false;
+      run_bytes[i] = w * cs;
+      if (run_log2[i] < 0) {
+        // runs that are not a power of two: 16-byte pieces, one run each
+        if (run_bytes[i] % 16 != 0) return false;
+        run_log2[i] = kRunOdd;
+        odd_run = true;
+      }
       transposed = true;
       if (w * cs > min_tw) min_tw = w * cs;
+      unit = unit / gcd64(unit, run_bytes[i]) * run_bytes[i];
     }
     // block addresses: base + index * pitch, all 16-byte aligned
     const uintptr_t base =
@@ -148,9 +178,36 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   // measured 0.676 of peak in 8 KiB tiles against 0.63 in gather_rows_kernel,
   // 3 x 128 heads 0.587 in 4 KiB tiles against 0.623.
   int64_t tw = row_cache & -row_cache;
-  if (tw < min_tw) return false;
-  if ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_TILE_BYTES) return false;
-  while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  if (odd_run || tw < min_tw ||
+      ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_TILE_BYTES)) {
+    // Otherwise the tile is a whole number of runs that divides the row,
+    // phase 2 dividing by chunks per row with a multiply-high (HND heads of
+    // 96 or 80 bf16 elements, three 256-byte heads).  Widths of whole
+    // 128-byte lines first, then the tile nearest KVX_TILE_BYTES, the wider
+    // on a tie.  On MI355X (c2's table, 4 layers) these gathers took 5-8%
+    // less time than in gather_rows_kernel; widths that split output lines
+    // between two workgroups (320 or 192 bytes) measured 7-12% slower than
+    // line-multiple ones (640 or 384 bytes), three 256-byte heads 20% slower
+    // in 4 KiB tiles than in 12 KiB ones, and HND 8 x 96 bf16 3% faster in
+    // 6 KiB tiles than in 12 KiB ones.
+    tw = -1;
+    if (row_cache % unit != 0) return false;
+    int64_t best = 0;
+    for (int64_t k = row_cache / unit; k >= 1; --k) {
+      if ((row_cache / unit) % k != 0) continue;
+      const int64_t w = unit * k, bytes = w * bs;
+      if (bytes < KVX_ODD_TILE_MIN || bytes > KVX_ODD_TILE_BYTES) continue;
+      const int64_t dist = bytes > KVX_TILE_BYTES ? bytes - KVX_TILE_BYTES : KVX_TILE_BYTES - bytes;
+      const int64_t score = (w % 128 == 0 ? 0 : (int64_t)1 << 40) + dist;
+      if (tw < 0 || score < best) {
+        tw = w;
+        best = score;
+      }
+    }
+    if (tw < 0) return false;
+  } else {
+    while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+  }
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
   t->table = p.block_table;
@@ -167,7 +224,12 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   t->blocks_per_seq = (int32_t)(ragged || by_len < p.max_blocks_per_seq ? by_len
                                                                        : p.max_blocks_per_seq);
   t->tiles = (int32_t)(row_cache / tw);
+  t->tw = (int32_t)tw;
   t->tw_log2 = log2_exact(tw);
+  // phase 2 chunks per row; div_magic is exact for u * cpr <= 2^32, and
+  // u * cpr < bs * tw * tw <= 2^16 * tw (bs * pitch <= 64 KiB below)
+  t->cpr = (int32_t)(tw / src_chunk);
+  t->cpr_magic = t->tw_log2 < 0 ? magic_for(t->cpr) : 0;
   t->pitch = (int32_t)pitch;
   t->max_seq_len = p.max_seq_len;
   t->num_blocks = p.num_blocks;
@@ -183,6 +245,10 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     t->t[i].s_block = g[i]->s_block * cs;
     t->t[i].sc = sc[i];
     t->t[i].run_log2 = run_log2[i];
+    // stage_tile_odd divides region offsets (< 64 KiB) by the run: exact
+    // for runs below 2^16 bytes
+    t->t[i].run_bytes = (int32_t)run_bytes[i];
+    t->t[i].run_magic = run_log2[i] == kRunOdd ? magic_for(run_bytes[i]) : 0;
     t->t[i].pad_ = 0;
   }
   *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;

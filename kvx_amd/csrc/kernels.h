@@ -42,6 +42,15 @@ constexpr int kMaxChunksPerLane = 4;
 // per thread in flight, and LDS row padding in bytes.
 constexpr int kTileLoads = 4;
 constexpr int kTilePad = 16;
+// run_log2 of a per-token run that is a multiple of 16 bytes but not a power
+// of two (HND heads of 96 or 80 bf16 elements): its length is in run_bytes.
+constexpr int32_t kRunOdd = 30;
+
+// x / d for a divisor d >= 2 whose magic m = ceil(2^32 / d): with
+// m = 2^32 / d + f (0 <= f < 1), x * m / 2^32 = x / d + x * f / 2^32 and
+// the error x * f / 2^32 < 1 / d whenever x * d <= 2^32, so the floor is
+// exact there.  The planners only pass (x, d) pairs that satisfy it.
+__device__ __forceinline__ uint32_t div_magic(uint32_t x, uint32_t m) { return __umulhi(x, m); }
 // Compile-time tuning knobs of the contiguous-block gather (defaults are the
 // measured best on MI355X): chunks per lane in flight for the copy and for
 // the FP8 dequantizing gather, and non-temporal (streaming) loads of the
@@ -1577,7 +1586,10 @@ struct TileTensor {
   char *dst;          // output tensor
   int64_t s_block;    // bytes
   ScaleRef sc;        // dequantizing ops only
-  int32_t run_log2;   // log2 bytes of a per-token run; -1 for row-major
+  int32_t run_log2;   // log2 bytes of a per-token run; -1 for row-major;
+                      // kRunOdd: run_bytes, a multiple of 16 bytes
+  int32_t run_bytes;
+  uint32_t run_magic;  // kRunOdd: div_magic's m for run_bytes
   int32_t pad_;
 };
 
@@ -1593,7 +1605,10 @@ struct TileArgs {
   int32_t max_blocks_per_seq;
   int32_t blocks_per_seq;
   int32_t tiles;          // tiles per block: cache row bytes / tw
-  int32_t tw_log2;        // tile width, cache bytes per row
+  int32_t tw;             // tile width, cache bytes per row
+  int32_t tw_log2;        // log2(tw), or -1 when tw is not a power of two
+  int32_t cpr;            // tw_log2 < 0: phase-2 chunks per tile row
+  uint32_t cpr_magic;     // tw_log2 < 0: div_magic's m for cpr
   int32_t pitch;          // LDS row pitch, bytes
   int32_t max_seq_len;
   int32_t num_blocks;
@@ -1685,6 +1700,107 @@ __device__ __forceinline__ void stage_tile_rows(const char *src, int64_t s_block
   }
 }
 
+// Phase 1 for runs of `run` bytes, a multiple of 16 but not a power of two:
+// each 16-byte chunk lies inside one run, whose index m / run (by
+// multiply-high) gives the row (index % bs) and the run's place in the row.
+__device__ __forceinline__ void stage_tile_odd(const char *region, char *lds, int32_t nbytes,
+                                               int32_t run, uint32_t run_magic, int32_t bs_log2,
+                                               int32_t pitch, int32_t rows) {
+  const uint32_t bsm = (1u << bs_log2) - 1;
+  constexpr int32_t kStep = kBlockThreads * 16;
+  for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
+    Raw<16> x[kTileLoads];
+    int32_t at[kTileLoads];
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+      at[u] = -1;
+      if (m < nbytes) {
+        const uint32_t q = div_magic((uint32_t)m, run_magic);
+        const int32_t o = (int32_t)(q & bsm);
+        if (o < rows) {
+          at[u] = o * pitch + (int32_t)(q >> bs_log2) * run + (m - (int32_t)q * run);
+          x[u] = ld<16, kGatherNtLoad>(region + m);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u)
+      if (at[u] >= 0) st<16>(lds + at[u], x[u]);
+  }
+}
+
+// stage_tile_rows for runs of `run` bytes (a multiple of 16, not a power of
+// two): 16-byte pieces, each inside one run.
+__device__ __forceinline__ void stage_tile_rows_odd(const char *src, int64_t s_block, int32_t off,
+                                                    const int64_t *ids, char *lds, int32_t nbytes,
+                                                    int32_t run, uint32_t run_magic,
+                                                    int32_t bs_log2, int32_t pitch, int32_t rows) {
+  const uint32_t bsm = (1u << bs_log2) - 1;
+  for (int32_t mm = (int32_t)threadIdx.x * 16; mm < nbytes; mm += kBlockThreads * 16) {
+    const uint32_t q = div_magic((uint32_t)mm, run_magic);
+    const int32_t o = (int32_t)(q & bsm);
+    if (o >= rows) continue;
+    const int64_t id = ids[o];
+    if (id < 0) continue;
+    st<16>(lds + o * pitch + (int32_t)(q >> bs_log2) * run + (mm - (int32_t)q * run),
+           ld<16, kGatherNtLoad>(src + id * s_block + off + mm));
+  }
+}
+
+// Phase 2: chunk c of row r covers cache bytes [c * kSrc, (c + 1) * kSrc)
+// of the tile, i.e. row elements e0 + c * G.  ODD: the tile width is not a
+// power of two, so r = u / cpr by multiply-high.
+template <class Op, int FMT, bool ODD>
+__device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const TileTensor &tt,
+                                                    const char *lds, char *out, int32_t rows,
+                                                    int32_t tile, int64_t bid, bool mixed,
+                                                    const int64_t *s_ids, float uniform) {
+  constexpr int kSrcLog2 = Op::kSrc == 16 ? 4 : Op::kSrc == 8 ? 3 : Op::kSrc == 4 ? 2
+                           : Op::kSrc == 2 ? 1 : 0;
+  const uint32_t hd = (uint32_t)a.head_dim;
+  const int32_t cpr_log2 = a.tw_log2 - kSrcLog2;
+  const int32_t total = ODD ? rows * a.cpr : rows << cpr_log2;
+  const uint32_t e0 = ((uint32_t)tile * (uint32_t)a.tw) >> a.cache_es_log2;
+  const int32_t cm = (1 << cpr_log2) - 1;
+  for (int32_t u0 = (int32_t)threadIdx.x; u0 < total; u0 += kTileLoads * kBlockThreads) {
+    Raw<Op::kSrc> x[kTileLoads];
+    int32_t rr[kTileLoads], cc[kTileLoads];
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if constexpr (ODD) {
+        rr[k] = (int32_t)div_magic((uint32_t)u, a.cpr_magic);
+        cc[k] = u - rr[k] * a.cpr;
+      } else {
+        rr[k] = u >> cpr_log2;
+        cc[k] = u & cm;
+      }
+      if (u < total) x[k] = ld<Op::kSrc>(lds + rr[k] * a.pitch + (cc[k] << kSrcLog2));
+    }
+#pragma unroll
+    for (int k = 0; k < kTileLoads; ++k) {
+      const int32_t u = u0 + k * kBlockThreads;
+      if (u < total) {
+        const int32_t r = rr[k];
+        int64_t rb = bid;
+        if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
+          if (mixed) {
+            rb = s_ids[r];
+            if (rb < 0) continue;
+          }
+        }
+        const uint32_t e = e0 + ((uint32_t)(cc[k] << kSrcLog2) >> a.cache_es_log2);
+        float sc = uniform;
+        if constexpr (Op::kScaled) sc = scale_at(tt.sc, uniform, rb, e, hd);
+        st<Op::kDst, kGatherNtStore>(out + (int64_t)r * a.out_row_bytes +
+                                         ((int64_t)e << a.io_es_log2),
+                                     Op::apply(x[k], sc));
+      }
+    }
+  }
+}
+
 // I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
 // indptr dtype.
 template <class Op, int FMT, bool I64, bool P64>
@@ -1763,8 +1879,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
   float uniform = 1.0f;
   if constexpr (Op::kScaled) uniform = tt.sc.p[0];
 
-  const int32_t tw = 1 << a.tw_log2;
-  const int32_t region = tw << a.bs_log2;
+  const int32_t region = a.tw << a.bs_log2;
   char *out = tt.dst + (s * a.max_seq_len + t0) * a.out_row_bytes;
   const uint32_t hd = (uint32_t)a.head_dim;
   const uint32_t re = (uint32_t)a.row_elems;
@@ -1795,7 +1910,10 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
 
   if (mixed) {
     const int32_t off = tile * region;
-    switch (tt.run_log2) {
+    if (tt.run_log2 == kRunOdd)
+      stage_tile_rows_odd(tt.src, tt.s_block, off, s_ids, lds, region, tt.run_bytes, tt.run_magic,
+                          a.bs_log2, a.pitch, rows);
+    else switch (tt.run_log2) {
       case 0: stage_tile_rows<1>(tt.src, tt.s_block, off, s_ids, lds, region, 0, a.bs_log2, a.pitch, rows); break;
       case 1: stage_tile_rows<2>(tt.src, tt.s_block, off, s_ids, lds, region, 1, a.bs_log2, a.pitch, rows); break;
       case 2: stage_tile_rows<4>(tt.src, tt.s_block, off, s_ids, lds, region, 2, a.bs_log2, a.pitch, rows); break;
@@ -1804,7 +1922,9 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     }
   } else {
     const char *src = blk + (int64_t)tile * region;
-    switch (tt.run_log2) {
+    if (tt.run_log2 == kRunOdd)
+      stage_tile_odd(src, lds, region, tt.run_bytes, tt.run_magic, a.bs_log2, a.pitch, rows);
+    else switch (tt.run_log2) {
       case 0: stage_tile<1>(src, lds, region, 0, a.bs_log2, a.pitch, rows); break;
       case 1: stage_tile<2>(src, lds, region, 1, a.bs_log2, a.pitch, rows); break;
       case 2: stage_tile<4>(src, lds, region, 2, a.bs_log2, a.pitch, rows); break;
@@ -1813,43 +1933,10 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     }
   }
   __syncthreads();
-
-  // Phase 2: chunk c of row r covers cache bytes [c * kSrc, (c + 1) * kSrc)
-  // of the tile, i.e. row elements e0 + c * G.
-  constexpr int kSrcLog2 = Op::kSrc == 16 ? 4 : Op::kSrc == 8 ? 3 : Op::kSrc == 4 ? 2
-                           : Op::kSrc == 2 ? 1 : 0;
-  const int32_t cpr_log2 = a.tw_log2 - kSrcLog2;
-  const int32_t total = rows << cpr_log2;
-  const uint32_t e0 = ((uint32_t)tile << a.tw_log2) >> a.cache_es_log2;
-  const int32_t cm = (1 << cpr_log2) - 1;
-  for (int32_t u0 = (int32_t)threadIdx.x; u0 < total; u0 += kTileLoads * kBlockThreads) {
-    Raw<Op::kSrc> x[kTileLoads];
-#pragma unroll
-    for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
-      if (u < total) x[k] = ld<Op::kSrc>(lds + (u >> cpr_log2) * a.pitch + ((u & cm) << kSrcLog2));
-    }
-#pragma unroll
-    for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
-      if (u < total) {
-        const int32_t r = u >> cpr_log2;
-        int64_t rb = bid;
-        if constexpr (FMT == KVX_BLOCK_TABLE_RAGGED) {
-          if (mixed) {
-            rb = s_ids[r];
-            if (rb < 0) continue;
-          }
-        }
-        const uint32_t e = e0 + ((uint32_t)((u & cm) << kSrcLog2) >> a.cache_es_log2);
-        float sc = uniform;
-        if constexpr (Op::kScaled) sc = scale_at(tt.sc, uniform, rb, e, hd);
-        st<Op::kDst, kGatherNtStore>(out + (int64_t)r * a.out_row_bytes +
-                                         ((int64_t)e << a.io_es_log2),
-                                     Op::apply(x[k], sc));
-      }
-    }
-  }
+  if (a.tw_log2 < 0)
+    unstage_gather_tile<Op, FMT, true>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
+  else
+    unstage_gather_tile<Op, FMT, false>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
 }
 
 // Rows of sequence s that exist (t < n) for an indexed-format workgroup,

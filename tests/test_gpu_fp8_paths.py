@@ -6,10 +6,13 @@ reach, through the C ABI, bit-identical to the CPU oracle:
       rows are not contiguous: HND, x-packed, and vLLM's value cache
       [num_blocks, H, D, block_size] (CUSTOM);
   gather_rows_kernel with the dequantizing op   PACKED gathers of HND
-      caches whose row bytes are not a power of two (head_dim 96, or 6
-      heads), which the LDS tile kernel does not take;
+      caches whose heads are 40 FP8 bytes (runs the LDS tile kernel cannot
+      cut into 16-byte pieces);
   gather_indexed_kernel with the dequantizing op   RAGGED and KV_OFFSETS
-      gathers of the same caches.
+      gathers of the same caches;
+  gather_tiles_kernel with odd tiles   PACKED, RAGGED and KV_OFFSETS
+      gathers of HND caches with 96-byte runs (head_dim 96) or rows of six
+      64-byte runs, whose tile widths are not a power of two.
 
 Each runs E4M3 and E5M2 with per-tensor, per-head and (where the table
 format allows) per-block and per-block-head scales.
@@ -71,7 +74,8 @@ def test_quantizing_decode_write_token_path(layout, fp8, kind):
                 k_scale=ks, v_scale=vs)
 
 
-SHAPES = [(8, 96), (6, 64)]  # row bytes 768 and 384 per FP8 row: not powers of two
+# FP8 rows of 768, 384 and 160 bytes: not powers of two
+SHAPES = [(8, 96), (6, 64), (4, 40)]
 
 
 @pytest.mark.parametrize("kind", KINDS)

@@ -7,7 +7,8 @@ write and :226-267 gather semantics).
 
 Gather cases cover every LDS piece size (1, 2, 4, 8, 16 bytes), runs
 shorter than one 16-byte load (block_size * run < 16), blocks split into
-several tiles, a row-major partner tensor, partial last blocks, block ids
+several tiles, runs and tile widths that are not a power of two (HND heads
+of 96 or 80 elements, rows of 3 or 6 heads), a row-major partner tensor, partial last blocks, block ids
 < 0 and >= num_blocks, seq_len beyond max_seq_len, int64 indices, and the
 FP8 dequantizing gather with per-tensor, per-head and per-block-head
 scales.  RAGGED cases cover tiles whose rows all name one block, tiles whose
@@ -45,7 +46,13 @@ CASES = [
     (DType.BF16, "bhpox", 8, "bohd", None, 16, 12, 64),   # x-packed K / NHD V, 1536-byte rows
     (DType.F8_E4M3, "bhod", None, "bhdo", None, 16, 12, 128),  # FP8 HND / token-innermost
     (DType.F32, "bhdo", None, "bhod", None, 64, 5, 32),   # 640-byte rows: 5 tiles of 128 B
-    (DType.F16, "bhpox", 8, "bohd", None, 16, 3, 64),     # 384-byte rows: tiles too small
+    (DType.F16, "bhpox", 8, "bohd", None, 16, 3, 64),     # 384-byte rows: one 6 KiB tile
+    # runs or tile widths that are not a power of two (multiply-high division)
+    (DType.BF16, "bhod", None, "bhod", None, 16, 8, 96),  # HND 192-byte runs, 768-byte tiles
+    (DType.BF16, "bhod", None, "bohd", None, 32, 8, 80),  # 160-byte runs, 320-byte tiles
+    (DType.BF16, "bhod", None, "bhod", None, 64, 8, 96),  # 8 tiles of one run per row
+    (DType.F8_E4M3, "bhod", None, "bhpox", 16, 16, 8, 96),  # FP8 96-byte runs / x-packed
+    (DType.BF16, "bhdo", None, "bhod", None, 16, 3, 128),  # 2- / 256-byte runs, 768-byte tile
 ]
 
 
