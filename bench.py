@@ -91,7 +91,8 @@ def parse_args():
                         "PyTorch-ROCm op _C_cache_ops.reshape_and_cache_flash_kvx "
                         "(c1, c2, c4, c5: NHD caches)")
     p.add_argument("--layout", default=None, choices=["nhd", "hnd", "packed", "vllm"],
-                   help="c2 / c5: cache layout of K and V (default NHD).  packed: "
+                   help="c2 / c3 / c5: cache layout of K and V (default NHD; c3: K "
+                        "HND_PACKED x = 8, V NHD).  packed: "
                         "HND_PACKED x = 8; vllm: K HND_PACKED x = 8 and V "
                         "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
                         "paged-attention pair (PACKED / RAGGED tables only)")
@@ -236,8 +237,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
         w.name = f"{w.name}_scale_{scales}"
     reshape_rows(w, name, heads, head_dim)
     if layout is not None:
-        if name not in ("c2", "c5"):
-            raise SystemExit("--layout applies to c2 and c5")
+        if name not in ("c2", "c3", "c5"):
+            raise SystemExit("--layout applies to c2, c3 and c5")
         if write_entry == "torch_op":
             raise SystemExit("--layout combines with the launch entry")
         if table_fmt == "kv_offsets" and layout == "vllm":

@@ -125,6 +125,35 @@ int64_t gcd64(int64_t a, int64_t b) {
 // div_magic's multiplier for divisor d >= 2: ceil(2^32 / d).
 uint32_t magic_for(int64_t d) { return (uint32_t)(((uint64_t(1) << 32) + (uint64_t)d - 1) / (uint64_t)d); }
 
+// Tile width of whole runs (a multiple of `unit`) that divides the row, for
+// rows or runs that are not a power of two, phase 2 dividing by chunks per
+// row with a multiply-high (HND heads of 96 or 80 bf16 elements, three
+// 256-byte heads): widths of whole 128-byte lines first, then the tile
+// nearest `target` bytes, the wider on a tie, within KVX_ODD_TILE_MIN and
+// max(target, KVX_ODD_TILE_BYTES); -1 if none.  On MI355X (c2's table, 4
+// layers) such gathers took 5-8% less time than in gather_rows_kernel;
+// widths that split output lines between two workgroups (320 or 192
+// bytes) measured 7-12% slower than line-multiple ones (640 or 384 bytes),
+// three 256-byte heads 20% slower in 4 KiB tiles than in 12 KiB ones, and
+// HND 8 x 96 bf16 3% faster in 6 KiB tiles than in 12 KiB ones.
+int64_t odd_tile_width(int64_t row, int64_t unit, int64_t bs, int64_t target) {
+  if (row % unit != 0) return -1;
+  const int64_t cap = target > KVX_ODD_TILE_BYTES ? target : KVX_ODD_TILE_BYTES;
+  int64_t tw = -1, best = 0;
+  for (int64_t k = row / unit; k >= 1; --k) {
+    if ((row / unit) % k != 0) continue;
+    const int64_t w = unit * k, bytes = w * bs;
+    if (bytes < KVX_ODD_TILE_MIN || bytes > cap) continue;
+    const int64_t dist = bytes > target ? bytes - target : target - bytes;
+    const int64_t score = (w % 128 == 0 ? 0 : (int64_t)1 << 40) + dist;
+    if (tw < 0 || score < best) {
+      tw = w;
+      best = score;
+    }
+  }
+  return tw;
+}
+
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
   const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
@@ -180,30 +209,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   int64_t tw = row_cache & -row_cache;
   if (odd_run || tw < min_tw ||
       ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_TILE_BYTES)) {
-    // Otherwise the tile is a whole number of runs that divides the row,
-    // phase 2 dividing by chunks per row with a multiply-high (HND heads of
-    // 96 or 80 bf16 elements, three 256-byte heads).  Widths of whole
-    // 128-byte lines first, then the tile nearest KVX_TILE_BYTES, the wider
-    // on a tie.  On MI355X (c2's table, 4 layers) these gathers took 5-8%
-    // less time than in gather_rows_kernel; widths that split output lines
-    // between two workgroups (320 or 192 bytes) measured 7-12% slower than
-    // line-multiple ones (640 or 384 bytes), three 256-byte heads 20% slower
-    // in 4 KiB tiles than in 12 KiB ones, and HND 8 x 96 bf16 3% faster in
-    // 6 KiB tiles than in 12 KiB ones.
-    tw = -1;
-    if (row_cache % unit != 0) return false;
-    int64_t best = 0;
-    for (int64_t k = row_cache / unit; k >= 1; --k) {
-      if ((row_cache / unit) % k != 0) continue;
-      const int64_t w = unit * k, bytes = w * bs;
-      if (bytes < KVX_ODD_TILE_MIN || bytes > KVX_ODD_TILE_BYTES) continue;
-      const int64_t dist = bytes > KVX_TILE_BYTES ? bytes - KVX_TILE_BYTES : KVX_TILE_BYTES - bytes;
-      const int64_t score = (w % 128 == 0 ? 0 : (int64_t)1 << 40) + dist;
-      if (tw < 0 || score < best) {
-        tw = w;
-        best = score;
-      }
-    }
+    tw = odd_tile_width(row_cache, unit, bs, KVX_TILE_BYTES);
     if (tw < 0) return false;
   } else {
     while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
@@ -289,16 +295,28 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   const Geom *g[2] = {&p.gk, &p.gv};
   const void *src[2] = {p.src_k, p.src_v};
   const void *dst[2] = {p.dst_k, p.dst_v};
-  bool transposed = false;
+  bool transposed = false, odd_run = false;
   int64_t min_tw = 16;
+  int64_t unit = 16;  // a tile width holds whole runs and 16-byte chunks
   for (int i = 0; i < 2; ++i) {
     const int64_t w = dense_run_elems(*g[i], bs, H, D);
     if (w < 0) return false;
     wt->run_log2[i] = w == H * D ? -1 : log2_exact(w * cs);
+    wt->run_bytes[i] = 0;
+    wt->run_magic[i] = 0;
     if (w != H * D) {
-      if (wt->run_log2[i] < 0) return false;
+      if (wt->run_log2[i] < 0) {
+        // runs that are not a power of two: 16-byte pieces, one run each
+        if ((w * cs) % 16 != 0) return false;
+        wt->run_log2[i] = kRunOdd;
+        wt->run_bytes[i] = (int32_t)(w * cs);
+        // unstage_tile_odd divides region offsets (< 64 KiB) by the run
+        wt->run_magic[i] = magic_for(w * cs);
+        odd_run = true;
+      }
       transposed = true;
       if (w * cs > min_tw) min_tw = w * cs;
+      unit = unit / gcd64(unit, w * cs) * (w * cs);
     }
     if ((reinterpret_cast<uintptr_t>(dst[i]) | (uintptr_t)(g[i]->s_block * cs)) % 16 != 0)
       return false;
@@ -311,15 +329,27 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   // as in plan_tiles: a power-of-two tile width that divides the row, and
   // a full copy tile for a row that is not a power of two (c3's size into
   // HND caches of 6 x 128 or 12 x 64 bf16 heads: 0.527 of peak against 0.43
-  // per token)
+  // per token); otherwise a tile of whole runs (odd_tile_width): at c3's
+  // size, 3 heads of 128 measured 0.61 of peak against 0.11 per token for
+  // an x-packed K, 0.58 against 0.055 for vLLM's K / V pair and 0.68 against
+  // 0.50 for HND; HND 8 x 80 0.61 against 0.50, 8 x 96 0.60 against 0.57
   int64_t tw = row_cache & -row_cache;
-  if (tw < min_tw) return false;
-  if ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_WRITE_TILE_BYTES) return false;
-  while (tw * bs > tile_bytes && tw / 2 >= min_tw) tw /= 2;
+  if (odd_run || tw < min_tw ||
+      ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_WRITE_TILE_BYTES)) {
+    tw = odd_tile_width(row_cache, unit, bs, tile_bytes);
+    if (tw < 0) return false;
+  } else {
+    while (tw * bs > tile_bytes && tw / 2 >= min_tw) tw /= 2;
+  }
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
   wt->tiles = (int32_t)(row_cache / tw);
+  wt->tw = (int32_t)tw;
   wt->tw_log2 = log2_exact(tw);
+  // phase 1 chunks per row (Op::kDst cache bytes each: 16, or 8 FP8 bytes);
+  // div_magic is exact since u * cpr < bs * tw * tw <= 2^16 * tw
+  wt->cpr = (int32_t)(tw / (p.conv == kConvQuant ? 8 : 16));
+  wt->cpr_magic = wt->tw_log2 < 0 ? magic_for(wt->cpr) : 0;
   wt->pitch = (int32_t)pitch;
   wt->bs_log2 = bs_log2;
   wt->cache_es_log2 = log2_exact(cs);

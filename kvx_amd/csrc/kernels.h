@@ -894,13 +894,33 @@ __device__ __forceinline__ void write_group_tokens(const WriteArgs &a, int64_t t
 // that tensor's `tiles` workgroups of the group.
 struct WriteTileArgs {
   int32_t tiles;          // tiles per block: cache row bytes / tw
-  int32_t tw_log2;        // tile width, cache bytes per row
+  int32_t tw;             // tile width, cache bytes per row
+  int32_t tw_log2;        // log2(tw), or -1 when tw is not a power of two
+  int32_t cpr;            // tw_log2 < 0: phase-1 chunks per tile row
+  uint32_t cpr_magic;     // tw_log2 < 0: div_magic's m for cpr
   int32_t pitch;          // LDS row pitch, bytes
   int32_t bs_log2;
-  int32_t run_log2[2];    // K, V: log2 bytes of a per-token run; -1 row-major
+  int32_t run_log2[2];    // K, V: log2 bytes of a per-token run; -1 row-major;
+                          // kRunOdd: run_bytes, a multiple of 16 bytes
+  int32_t run_bytes[2];
+  uint32_t run_magic[2];  // kRunOdd: div_magic's m for run_bytes
   int32_t cache_es_log2;  // log2 cache element bytes
   int32_t io_es_log2;     // log2 io element bytes
 };
+
+// Row and chunk of tile chunk u (cpr chunks per tile row): shifts when the
+// tile width is a power of two, a multiply-high division otherwise (ODD).
+template <bool ODD>
+__device__ __forceinline__ int32_t tile_row(int32_t u, int32_t cpr_log2, const WriteTileArgs &wt) {
+  if constexpr (ODD) return (int32_t)div_magic((uint32_t)u, wt.cpr_magic);
+  else return u >> cpr_log2;
+}
+template <bool ODD>
+__device__ __forceinline__ int32_t tile_col(int32_t u, int32_t row, int32_t cpr_log2,
+                                            const WriteTileArgs &wt) {
+  if constexpr (ODD) return u - row * wt.cpr;
+  else return u & ((1 << cpr_log2) - 1);
+}
 
 // Piece k (PIECE bytes) of a 16-byte chunk, read from p into x (x's other
 // pieces untouched; x starts zeroed for PIECE < 4).
@@ -979,10 +999,46 @@ __device__ __forceinline__ void unstage_tile(char *region, const char *lds, int3
   }
 }
 
+// Phase 2 for runs of `run` bytes, a multiple of 16 but not a power of two:
+// every 16-byte chunk lies inside one run of one row, and is stored whole
+// when that row is in [lo, hi).
 template <bool FULL>
+__device__ __forceinline__ void unstage_tile_odd(char *region, const char *lds, int32_t nbytes,
+                                                 int32_t run, uint32_t run_magic, int32_t bs_log2,
+                                                 int32_t pitch, int32_t lo, int32_t hi) {
+  const uint32_t bsm = (1u << bs_log2) - 1;
+  constexpr int32_t kStep = kBlockThreads * 16;
+  for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
+    Raw<16> x[kTileLoads];
+    bool ok[kTileLoads];
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u) {
+      const int32_t m = m0 + u * kStep;
+      const uint32_t q = div_magic((uint32_t)m, run_magic);
+      const int32_t o = (int32_t)(q & bsm);
+      ok[u] = m < nbytes && (FULL || (o >= lo && o < hi));
+      if (ok[u]) x[u] = ld<16>(lds + o * pitch + (int32_t)(q >> bs_log2) * run + (m - (int32_t)q * run));
+    }
+#pragma unroll
+    for (int u = 0; u < kTileLoads; ++u)
+      if (ok[u]) st<16, kWriteNtStore>(region + m0 + u * kStep, x[u]);
+  }
+}
+
+// ODD: the tile width is not a power of two, as it is for every run that
+// is not (a multiple of such a run never is one), so only then can
+// run_log2 be kRunOdd.
+template <bool FULL, bool ODD>
 __device__ __forceinline__ void unstage_any(char *dst, const char *lds, int32_t region,
                                             int32_t run_log2, const WriteTileArgs &wt,
-                                            const GroupRun &r) {
+                                            const GroupRun &r, bool v) {
+  if constexpr (ODD) {
+    if (run_log2 == kRunOdd) {
+      unstage_tile_odd<FULL>(dst, lds, region, wt.run_bytes[v], wt.run_magic[v], wt.bs_log2,
+                             wt.pitch, r.lo, r.hi);
+      return;
+    }
+  }
   switch (run_log2) {
     case 0: unstage_tile<1, FULL>(dst, lds, region, 0, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
     case 1: unstage_tile<2, FULL>(dst, lds, region, 1, wt.bs_log2, wt.pitch, r.lo, r.hi); break;
@@ -996,7 +1052,7 @@ __device__ __forceinline__ void unstage_any(char *dst, const char *lds, int32_t 
 
 // One run of a group through one tile of one tensor: rows [r.lo, r.hi) of
 // block r.block from the io rows of tokens t0 + r.tok, ...
-template <class Op, bool IDX>
+template <class Op, bool IDX, bool ODD>
 __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTileArgs &wt,
                                                const GroupRun &r, int64_t t0, int32_t tile,
                                                bool v, float uniform, char *lds) {
@@ -1005,13 +1061,13 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
   const char *src = (v ? a.src_v : a.src_k) + (t0 + r.tok) * a.row_bytes;
   char *blk = v ? a.dst_v + r.block * a.gv.s_block : a.dst_k + r.block * a.gk.s_block;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
-  const int32_t region = (1 << wt.tw_log2) << wt.bs_log2;
+  const int32_t region = wt.tw << wt.bs_log2;
   const int tid = (int)threadIdx.x;
 
   if (run_log2 < 0) {
     // Row-major block: rows [lo, hi) are one span of the block and of the
     // source rows.
-    const int32_t row_bytes_c = (int32_t)wt.tiles << wt.tw_log2;
+    const int32_t row_bytes_c = wt.tiles * wt.tw;
     const int32_t span_lo = r.lo * row_bytes_c;
     const int32_t span_hi = r.hi * row_bytes_c;
     const int32_t lo = tile * region > span_lo ? tile * region : span_lo;
@@ -1032,17 +1088,18 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
   constexpr int kDstLog2 = Op::kDst == 16 ? 4 : Op::kDst == 8 ? 3 : Op::kDst == 4 ? 2
                            : Op::kDst == 2 ? 1 : 0;
   const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
-  const int32_t total = (r.hi - r.lo) << cpr_log2;
-  const int32_t cm = (1 << cpr_log2) - 1;
-  const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
+  const int32_t total = ODD ? (r.hi - r.lo) * wt.cpr : (r.hi - r.lo) << cpr_log2;
+  const uint32_t e0 = ((uint32_t)tile * (uint32_t)wt.tw) >> wt.cache_es_log2;
   for (int32_t u0 = tid; u0 < total; u0 += kTileLoads * kBlockThreads) {
     Raw<Op::kSrc> x[kTileLoads];
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
       const int32_t u = u0 + k * kBlockThreads;
       if (u < total) {
-        const uint32_t e = e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
-        x[k] = ld<Op::kSrc, kWriteNtLoad>(src + (int64_t)(u >> cpr_log2) * a.row_bytes +
+        const int32_t row = tile_row<ODD>(u, cpr_log2, wt);
+        const int32_t col = tile_col<ODD>(u, row, cpr_log2, wt);
+        const uint32_t e = e0 + ((uint32_t)(col << kDstLog2) >> wt.cache_es_log2);
+        x[k] = ld<Op::kSrc, kWriteNtLoad>(src + (int64_t)row * a.row_bytes +
                                           ((int64_t)e << wt.io_es_log2));
       }
     }
@@ -1050,22 +1107,23 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
     for (int k = 0; k < kTileLoads; ++k) {
       const int32_t u = u0 + k * kBlockThreads;
       if (u < total) {
+        const int32_t row = tile_row<ODD>(u, cpr_log2, wt);
+        const int32_t col = tile_col<ODD>(u, row, cpr_log2, wt);
         float sc = uniform;
         if constexpr (Op::kScaled && IDX) {
-          const uint32_t e = e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
+          const uint32_t e = e0 + ((uint32_t)(col << kDstLog2) >> wt.cache_es_log2);
           sc = scale_at(sr, uniform, r.block, e, hd);
         }
-        st<Op::kDst>(lds + (r.lo + (u >> cpr_log2)) * wt.pitch + ((u & cm) << kDstLog2),
-                     Op::apply(x[k], sc));
+        st<Op::kDst>(lds + (r.lo + row) * wt.pitch + (col << kDstLog2), Op::apply(x[k], sc));
       }
     }
   }
   __syncthreads();
   char *dst = blk + (int64_t)tile * region;
   if (r.lo == 0 && r.hi == (1 << wt.bs_log2)) {
-    unstage_any<true>(dst, lds, region, run_log2, wt, r);
+    unstage_any<true, ODD>(dst, lds, region, run_log2, wt, r, v);
   } else {
-    unstage_any<false>(dst, lds, region, run_log2, wt, r);
+    unstage_any<false, ODD>(dst, lds, region, run_log2, wt, r, v);
   }
 }
 
@@ -1092,15 +1150,15 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
 // the short last group, or its tile needs more than one pass): the caller
 // then runs the general run analysis.  The speculative loads stay within the
 // io rows of tokens < num_tokens.
-template <class Op, bool IDX>
+template <class Op, bool IDX, bool ODD>
 __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const WriteTileArgs &wt,
                                                  int64_t t0, int32_t tile, bool v,
                                                  float uniform, char *lds) {
   constexpr int kDstLog2 = Op::kDst == 16 ? 4 : Op::kDst == 8 ? 3 : Op::kDst == 4 ? 2
                            : Op::kDst == 2 ? 1 : 0;
   const int32_t bs = 1 << wt.bs_log2;
-  const int32_t region = (1 << wt.tw_log2) << wt.bs_log2;  // cache bytes of the tile
-  const int32_t total = region >> kDstLog2;                // chunks of the tile
+  const int32_t region = wt.tw << wt.bs_log2;  // cache bytes of the tile
+  const int32_t total = region >> kDstLog2;    // chunks of the tile
   if (t0 + bs > a.num_tokens || total > kTileLoads * kBlockThreads) return false;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
   const char *io = v ? a.src_v : a.src_k;
@@ -1112,15 +1170,16 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   // Source of chunk u for a run starting at token tb.  Row-major cache: the
   // tile is bytes [tile * region, (tile + 1) * region) of the block, which
   // hold io elements e = byte >> cache_es_log2 counted from row tb.
-  // Otherwise: chunk u is chunk (u & cm) of the tile's columns of row
-  // tb + (u >> cpr_log2).
+  // Otherwise: chunk u is chunk tile_col(u) of the tile's columns of row
+  // tb + tile_row(u).
   const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
-  const int32_t cm = (1 << cpr_log2) - 1;
-  const uint32_t e0 = ((uint32_t)tile << wt.tw_log2) >> wt.cache_es_log2;
+  const uint32_t e0 = ((uint32_t)tile * (uint32_t)wt.tw) >> wt.cache_es_log2;
+  auto row_of = [&](int32_t u) { return tile_row<ODD>(u, cpr_log2, wt); };
+  auto col_of = [&](int32_t u) { return tile_col<ODD>(u, row_of(u), cpr_log2, wt); };
   auto elem = [&](int32_t u) -> uint32_t {  // io element of chunk u within its row run
     return run_log2 < 0
                ? (uint32_t)((tile * region + (u << kDstLog2)) >> wt.cache_es_log2)
-               : e0 + ((uint32_t)((u & cm) << kDstLog2) >> wt.cache_es_log2);
+               : e0 + ((uint32_t)(col_of(u) << kDstLog2) >> wt.cache_es_log2);
   };
   Raw<Op::kSrc> x[kTileLoads];
   auto load_rows = [&](int64_t tb) {
@@ -1131,7 +1190,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
       if (u < total) {
         x[k] = ld<Op::kSrc, kWriteNtLoad>(
             run_log2 < 0 ? src + ((int64_t)elem(u) << wt.io_es_log2)
-                         : src + (int64_t)(u >> cpr_log2) * a.row_bytes +
+                         : src + (int64_t)row_of(u) * a.row_bytes +
                                ((int64_t)elem(u) << wt.io_es_log2));
       }
     }
@@ -1161,7 +1220,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
     const ScaleRef &sr = v ? a.vsc : a.ksc;
     const uint32_t hd = (uint32_t)a.head_dim;
     const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
-    const int32_t rbc = (int32_t)wt.tiles << wt.tw_log2;  // cache bytes of a row
+    const int32_t rbc = wt.tiles * wt.tw;  // cache bytes of a row
     char *base = v ? a.dst_v : a.dst_k;
     const int64_t sb = v ? a.gv.s_block : a.gk.s_block;
     // byte m of the group's rows: row m / rbc of the group is row
@@ -1224,8 +1283,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
     if (u < total) {
       float sc = uniform;
       if constexpr (Op::kScaled && IDX) sc = scale_at(sr, uniform, block, elem(u), hd);
-      st<Op::kDst>(lds + (u >> cpr_log2) * wt.pitch + ((u & cm) << kDstLog2),
-                   Op::apply(x[k], sc));
+      st<Op::kDst>(lds + row_of(u) * wt.pitch + (col_of(u) << kDstLog2), Op::apply(x[k], sc));
     }
   }
   __syncthreads();
@@ -1235,7 +1293,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   r.hi = bs;
   r.tok = 0;
   r.pad_ = 0;
-  unstage_any<true>(blk + (int64_t)tile * region, lds, region, run_log2, wt, r);
+  unstage_any<true, ODD>(blk + (int64_t)tile * region, lds, region, run_log2, wt, r, v);
   return true;
 }
 
@@ -1243,7 +1301,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
 // path's op, whose chunk fits the cache geometry (WriteArgs' chunking).
 // IDX: indexed (per-head / per-block) scales are looked up per chunk; the
 // per-tensor instances carry no lookup code (registers decide occupancy).
-template <class Op, class TokOp, bool IDX>
+template <class Op, class TokOp, bool IDX, bool ODD>
 __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
                                                                     WriteTileArgs wt) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -1259,7 +1317,7 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
-  if (write_tile_block<Op, IDX>(a, wt, t0, tile, v, v ? vs : ks, lds)) return;
+  if (write_tile_block<Op, IDX, ODD>(a, wt, t0, tile, v, v ? vs : ks, lds)) return;
   // Which tokens this tensor's workgroups of the group write.  Row-major
   // blocks (NHD) hold whole rows: each group writes its own tokens, split
   // into runs (group_runs), so a block that a prefill chunk starts inside is
@@ -1287,7 +1345,7 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
   }
   for (int32_t i = 0; i < nruns; ++i) {
     if (i > 0) __syncthreads();  // the LDS tile is reused
-    write_tile_run<Op, IDX>(a, wt, s_runs[i], t0, tile, v, v ? vs : ks, lds);
+    write_tile_run<Op, IDX, ODD>(a, wt, s_runs[i], t0, tile, v, v ? vs : ks, lds);
   }
 }
 
@@ -2357,15 +2415,24 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
   if (w.tiles) {
     using TOp = typename TileOpOf<Op>::type;
     const dim3 g((uint32_t)w.tile_grid, 2);
+    const bool odd = w.wt.tw_log2 < 0;  // tile width not a power of two
     if constexpr (Op::kScaled) {
       if (a.ksc.indexed || a.vsc.indexed) {
-        hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true>), g, dim3(kBlockThreads),
-                           w.tile_lds, s, a, w.wt);
+        if (odd)
+          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, true>), g, dim3(kBlockThreads),
+                             w.tile_lds, s, a, w.wt);
+        else
+          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, false>), g, dim3(kBlockThreads),
+                             w.tile_lds, s, a, w.wt);
         return;
       }
     }
-    hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false>), g, dim3(kBlockThreads), w.tile_lds,
-                       s, a, w.wt);
+    if (odd)
+      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, true>), g, dim3(kBlockThreads),
+                         w.tile_lds, s, a, w.wt);
+    else
+      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, false>), g, dim3(kBlockThreads),
+                         w.tile_lds, s, a, w.wt);
   } else if (w.flat_grid > 0) {
     const dim3 g((uint32_t)w.flat_grid), b(kFlatThreads);
     if (kWriteFlatUniformSlot && a.nchunks_log2 >= 6) {

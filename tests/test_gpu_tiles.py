@@ -15,7 +15,8 @@ scales.  RAGGED cases cover tiles whose rows all name one block, tiles whose
 rows name different blocks or invalid ones, short indptr ranges and int64
 indptr.  Write cases cover the same layouts with groups that fill a block
 in order, groups that do not (partial, out of order, invalid slots, a
-ragged tail), and the quantizing FP8 write.
+ragged tail), and the quantizing FP8 write, also with tile widths that are
+not a power of two.
 """
 import numpy as np
 import pytest
@@ -445,6 +446,37 @@ def test_tiles_quantizing_write_indexed_scales(kind, layouts):
 
 
 # (K order, K x, V order, V x): at least one tensor row-major ("bohd", NHD)
+@pytest.mark.parametrize("kind", ["tensor", SG.PER_BLOCK_HEAD])
+@pytest.mark.parametrize("fp8", [DType.F8_E4M3, DType.F8_E5M2])
+@pytest.mark.parametrize("shape", [("bhod", None, "bhod", None, 8, 96),
+                                   ("bhpox", 16, "bhdo", None, 3, 128),
+                                   ("bhod", None, "bohd", None, 8, 80)],
+                         ids=["hnd-8x96", "xpacked-tokinner-3x128", "hnd-nhd-8x80"])
+def test_tiles_quantizing_write_odd_tiles(shape, fp8, kind):
+    """The quantizing tiled write with tile widths that are not a power of
+    two (96- and 80-byte FP8 runs, 384-byte rows): whole blocks, spoiled
+    groups and chunks that start inside blocks."""
+    ko_, kx, vo_, vx, H, D = shape
+    gen = torch.Generator().manual_seed(700 + 4 * H + int(fp8) + 2 * (kind != "tensor"))
+    bs, nb = 16, 64
+    pc, kb, vb = custom_cache(fp8, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    blocks = torch.randperm(nb // 2, generator=gen)[:6]
+    full = (blocks[:, None] * bs + torch.arange(bs)).reshape(-1)
+    full[7] = -1
+    chunks = _chunk_slots(gen, nb // 2, bs, S=3, chunk=2 * bs + 7) + (nb // 2) * bs
+    slots = torch.cat([full, chunks])
+    T = slots.numel()
+    key = (torch.randn((T, H, D), generator=gen) * 4).to(torch.bfloat16).to(DEV)
+    val = (torch.randn((T, H, D), generator=gen) * 0.5).to(torch.bfloat16).to(DEV)
+    if kind == "tensor":
+        ks, vs = 0.012, 0.0019
+    else:
+        ks, vs = (ScaleArg(kind, torch.empty(nb, H).uniform_(0.002, 0.05, generator=gen).numpy(),
+                           stride=(1, nb)) for _ in range(2))
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16, cache_dtype=fp8,
+                k_scale=ks, v_scale=vs)
+
+
 _ROW_MAJOR_PAIRS = [("bohd", None, "bhpox", 8), ("bhpox", 8, "bohd", None),
                     ("bohd", None, "bhdo", None), ("bhdo", None, "bohd", None),
                     ("bohd", None, "bohd", None)]
