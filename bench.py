@@ -121,6 +121,9 @@ def parse_args():
                    help="c2: block assignment: a random permutation of the pool (the "
                         "config), or ascending as a fresh allocator hands blocks out (the "
                         "gather then reads the pool front to back)")
+    p.add_argument("--block-size", type=int, default=None,
+                   help="c2: tokens per block (a power of two; the config's is 16), same "
+                        "lengths, the pool drawn in blocks of this size")
     p.add_argument("--c3-shift", type=int, default=0,
                    help="c3: every chunk starts this many tokens (0-15) into its first "
                         "block, as a chunked prefill continuing a chunk that ended inside "
@@ -209,7 +212,7 @@ def reshape_rows(w, name, heads=None, head_dim=None):
 def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                  write_entry="launch", fp8="e4m3", scales="tensor", layout=None,
                  heads=None, c3_seqs=16, c3_order="random", c3_gathers=False,
-                 c2_order="random", c3_shift=0, head_dim=None) -> Built:
+                 c2_order="random", c3_shift=0, head_dim=None, block_size=None) -> Built:
     import numpy as np
     import torch
 
@@ -222,7 +225,7 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     if name == "c3":
         w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order, shift=c3_shift)
     elif name == "c2":
-        w = W.c2_llama8b_decode(order=c2_order)
+        w = W.c2_llama8b_decode(order=c2_order, block_size=block_size or 16)
     else:
         w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
@@ -236,6 +239,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
     reshape_rows(w, name, heads, head_dim)
+    if block_size is not None and name != "c2":
+        raise SystemExit("--block-size applies to c2")
     if layout is not None:
         if name not in ("c2", "c3", "c5"):
             raise SystemExit("--layout applies to c2, c3 and c5")
@@ -1053,7 +1058,7 @@ def main():
               write_entry=args.write_entry, fp8=args.fp8, scales=args.scales,
               layout=args.layout, heads=args.heads, c3_seqs=args.c3_seqs,
               c3_order=args.c3_order, c2_order=args.c2_order, c3_shift=args.c3_shift,
-              head_dim=args.head_dim)
+              head_dim=args.head_dim, block_size=args.block_size)
     K, W = args.steps, args.warmup
     cpu = not args.no_cpu_baseline and not args.profile_only
 

@@ -104,6 +104,10 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 #ifndef KVX_TILE_BYTES
 #define KVX_TILE_BYTES 8192
 #endif
+// Narrowest tile width (cache bytes per row) the halving above goes to.
+#ifndef KVX_TILE_MIN_WIDTH
+#define KVX_TILE_MIN_WIDTH 128
+#endif
 // Tiles whose width is not a power of two: at most KVX_ODD_TILE_BYTES of
 // cache bytes per tensor, at least KVX_ODD_TILE_MIN.
 #ifndef KVX_ODD_TILE_BYTES
@@ -153,6 +157,12 @@ int64_t odd_tile_width(int64_t row, int64_t unit, int64_t bs, int64_t target) {
   }
   return tw;
 }
+
+// gather_rows_kernel: cache row bytes per tensor of one workgroup's share
+// of a block, at least (blocks of up to KVX_ROWS_TILE_BYTES stay whole).
+#ifndef KVX_ROWS_TILE_BYTES
+#define KVX_ROWS_TILE_BYTES 32768
+#endif
 
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
@@ -212,7 +222,14 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     tw = odd_tile_width(row_cache, unit, bs, KVX_TILE_BYTES);
     if (tw < 0) return false;
   } else {
-    while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw) tw /= 2;
+    // halve toward KVX_TILE_BYTES, but not below one 128-byte output line per
+    // row (blocks of 128 or 256 tokens then take 16 or 32 KiB tiles): on
+    // MI355X (c2's lengths, bf16 x-packed blocks of 128 / 256 tokens) 2315 /
+    // 6752 -> 1789 / 1823 us per layer, where narrower rows split output
+    // lines between workgroups.  (Runs of whole lines, HND, also gathered
+    // faster in these tiles than in gather_rows_kernel at every block size
+    // that fits: 16-128 tokens, 4-12% at c2's size.)
+    while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw && tw / 2 >= KVX_TILE_MIN_WIDTH) tw /= 2;
   }
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
@@ -587,6 +604,22 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
            ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
            a.split_log2 < 16 && grid_fits(blocks << (a.split_log2 + 1), kFlatThreads))
+      ++a.split_log2;
+    const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
+    if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
+    a.blocks_per_seq = (int32_t)per_seq;
+  } else if (a.bs_log2 >= 0) {
+    // gather_rows_kernel: a power-of-two block's rows split into
+    // 1 << split_log2 equal ranges of at least KVX_ROWS_TILE_BYTES of cache
+    // rows per tensor (and one full pass of the row groups), so that big
+    // blocks still give the grid enough workgroups: on MI355X (c2's lengths
+    // in 256-token HND blocks, bf16) 2009 -> 1775 us per layer
+    const int64_t per_pass = (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
+    int64_t want = KVX_ROWS_TILE_BYTES / (row_elems * cs);
+    if (want < per_pass) want = per_pass;
+    const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
+    while ((p.block_size >> (a.split_log2 + 1)) >= want && a.split_log2 < 16 &&
+           grid_fits(blocks << (a.split_log2 + 1), kBlockThreads))
       ++a.split_log2;
     const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
     if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;

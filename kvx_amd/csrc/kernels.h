@@ -1389,7 +1389,7 @@ struct GatherArgs {
   int32_t chunk_elems;
   int32_t lpt_log2;
   int32_t flat;  // cache rows of a block are contiguous for K and V
-  int32_t split_log2;  // flat only: workgroups per block = 1 << split_log2
+  int32_t split_log2;  // PACKED flat and row gathers: workgroups per block = 1 << split_log2
   int32_t format;      // kvx_block_table_format_t
   int32_t nchunks_log2;  // indexed flat: nchunks is a power of two
   int32_t bs_log2;       // log2(block_size), or -1 when not a power of two
@@ -1416,16 +1416,21 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
   const int64_t s = su;
-  const int32_t lb = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
+  // part `part` of 1 << split_log2 equal row ranges of logical block lb
+  const uint32_t w = wg - su * (uint32_t)a.blocks_per_seq;
+  const int32_t lb = (int32_t)(w >> a.split_log2);
+  const int32_t part = (int32_t)(w & ((1u << a.split_log2) - 1));
   if (lb >= a.max_blocks_per_seq) return false;
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
   const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
-  const int64_t t0 = (int64_t)lb * a.block_size;
+  const int32_t per_part = a.block_size >> a.split_log2;
+  const int32_t r0 = part * per_part;  // first row of the part in the block
+  const int64_t t0 = (int64_t)lb * a.block_size + r0;
   if (t0 >= n) return false;
   if (bid < 0 || bid >= a.num_blocks) return false;
   const int64_t rem = n - t0;
-  j.rows = rem < a.block_size ? (int32_t)rem : a.block_size;
+  j.rows = rem < per_part ? (int32_t)rem : per_part;
   j.bid = bid;
   j.ks = 1.0f;
   j.vs = 1.0f;
@@ -1433,8 +1438,8 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
     j.ks = a.ksc.p[0];
     j.vs = a.vsc.p[0];
   }
-  j.ck = a.src_k + bid * a.gk.s_block;
-  j.cv = a.src_v + bid * a.gv.s_block;
+  j.ck = a.src_k + bid * a.gk.s_block + (int64_t)r0 * a.gk.s_off;
+  j.cv = a.src_v + bid * a.gv.s_block + (int64_t)r0 * a.gv.s_off;
   const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
   j.ok = a.dst_k + out0;
   j.ov = a.dst_v + out0;

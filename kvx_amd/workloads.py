@@ -190,16 +190,20 @@ def _decode_tables(rng, S, lo, hi, bs, max_len, pool_blocks=None, ascending=Fals
     return lens, table, pool
 
 
-def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random") -> Workload:
+def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random",
+                      block_size: int = 16) -> Workload:
     """c2; order "random": the sequences' blocks are a random permutation of
     the pool (the config); "ascending": the same lengths with sequence s
     taking the next blocks of the pool in address order, as a fresh
     allocator would hand them out, so that its gather reads the pool front
-    to back."""
+    to back.  block_size other than the config's 16 keeps the lengths and
+    draws a pool of the larger or smaller blocks."""
     if order not in ("random", "ascending"):
         raise ValueError(order)
+    if block_size <= 0 or block_size & (block_size - 1):
+        raise ValueError(block_size)
     rng = np.random.Generator(np.random.PCG64(seed))
-    bs, L = 16, 8192
+    bs, L = block_size, 8192
     lens, table, pool = _decode_tables(rng, batch, 512, 8192, bs, L,
                                        ascending=order == "ascending")
     pos = lens - 1  # the new token is the last position of each context
@@ -207,6 +211,8 @@ def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random") ->
     pad = rng.choice(batch, size=int(round(0.05 * batch)), replace=False)
     slots[pad] = -1
     name = "c2_llama3_8b_decode_bf16" + ("" if order == "random" else f"_{order}")
+    if bs != 16:
+        name += f"_bs{bs}"
     return Workload(name, seed, 8, 128, bs, pool, DType.BF16,
                     DType.BF16, Layout.BLOCK_NHD, Layout.BLOCK_NHD, 8,
                     slots.astype(np.int64), None, table.astype(np.int32),

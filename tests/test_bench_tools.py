@@ -102,3 +102,14 @@ def test_reshape_rows():
     for name_, h, d in [("c4", 4, None), ("c5", 12, 128), ("c5", None, 84), ("c5", 0, None)]:
         with pytest.raises(SystemExit):
             bench.reshape_rows(W.CONFIGS["c5"](), name_, h, d)
+
+
+def test_c2_block_size_keeps_lengths():
+    from kvx_amd import workloads as W
+
+    a, b = W.c2_llama8b_decode(), W.c2_llama8b_decode(block_size=128)
+    assert (a.seq_lens == b.seq_lens).all() and b.name == a.name + "_bs128"
+    assert b.num_blocks == int(((b.seq_lens.astype("int64") + 127) // 128).sum())
+    assert sorted(b.block_table[b.block_table >= 0].tolist()) == list(range(b.num_blocks))
+    with pytest.raises(ValueError):
+        W.c2_llama8b_decode(block_size=48)
