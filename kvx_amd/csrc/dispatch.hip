@@ -27,14 +27,17 @@ bool aligned(const void *p, int64_t b) {
 }
 
 // True when chunks of g elements (g*esize bytes each) stay inside one
-// contiguous cache piece and every cache address they use is aligned.
+// contiguous cache piece and every cache address they use is aligned.  A
+// block of one token never steps by the offset stride (a size-1 axis, whose
+// stride can be anything, e.g. 1 for vLLM's [num_blocks, H, D, 1] value
+// cache).
 bool cache_chunk_ok(const Geom &g, const void *base, int esize, int head_dim,
-                    int ge) {
+                    int ge, int64_t block_size) {
   const int64_t bytes = (int64_t)ge * esize;
   if (ge > 1 && g.s_inner != 1) return false;
   if (g.pack % ge != 0 || head_dim % ge != 0) return false;
   if (!aligned(base, bytes)) return false;
-  const int64_t strides[4] = {g.s_block, g.s_off, g.s_head, g.s_piece};
+  const int64_t strides[4] = {g.s_block, block_size == 1 ? 0 : g.s_off, g.s_head, g.s_piece};
   for (int64_t st : strides) {
     if ((st * esize) % bytes != 0) return false;
   }
@@ -45,10 +48,10 @@ bool cache_chunk_ok(const Geom &g, const void *base, int esize, int head_dim,
 // side is contiguous with rows of H*D elements of io_size bytes.
 int pick_chunk(const Geom &gk, const Geom &gv, const void *ck, const void *cv,
                int cache_size, const void *ik, const void *iv, int io_size,
-               int head_dim, int max_chunk_bytes_cache) {
+               int head_dim, int max_chunk_bytes_cache, int64_t block_size) {
   for (int ge = max_chunk_bytes_cache / cache_size; ge >= 1; ge /= 2) {
-    if (!cache_chunk_ok(gk, ck, cache_size, head_dim, ge)) continue;
-    if (!cache_chunk_ok(gv, cv, cache_size, head_dim, ge)) continue;
+    if (!cache_chunk_ok(gk, ck, cache_size, head_dim, ge, block_size)) continue;
+    if (!cache_chunk_ok(gv, cv, cache_size, head_dim, ge, block_size)) continue;
     const int64_t io_bytes = (int64_t)ge * io_size;
     if (!aligned(ik, io_bytes) || !aligned(iv, io_bytes)) continue;
     return ge;
@@ -77,11 +80,21 @@ int log2_exact(int64_t v) {
   return lg;
 }
 
+// Row (head, dim) elements at consecutive addresses: row-major layouts, and
+// any dense layout whose block holds one row (HND, x-packed or token axis
+// innermost with block_size 1 store a row as H * D consecutive elements).
+// On MI355X (c2's lengths in one-token blocks) such gathers took 1592-1615 us
+// per layer in the flat kernel against 3517-3551 us in the tile kernels.
+bool row_elems_contiguous(const Geom &g, int64_t D) {
+  return g.s_inner == 1 && g.s_head == D && (g.pack == D || g.s_piece == g.pack);
+}
+
 // Elements of one per-token contiguous run when `g` is a dense block in
 // (run, offset, within-run) order, element e of row o at
 // (e / W) * bs * W + o * W + e % W, else -1: W = H * D (row-major), D (HND),
 // x (x-packed) or 1 (token axis innermost).  Any block stride.
 int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
+  if (bs == 1 && row_elems_contiguous(g, D)) return H * D;  // one row: row-major
   const int64_t p = g.pack;
   const bool split = p < D;  // d = (d / p) * p + d % p with its own strides
   if (g.s_inner == 1 && (!split || g.s_piece == p)) {
@@ -397,7 +410,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int is = dtype_size((kvx_dtype_t)p.io_dtype);
   const int max_bytes = (p.conv == kConvQuant) ? 8 : 16;
   const int ge = pick_chunk(p.gk, p.gv, p.dst_k, p.dst_v, cs, p.src_k,
-                            p.src_v, is, p.head_dim, max_bytes);
+                            p.src_v, is, p.head_dim, max_bytes, p.block_size);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
 
   WriteArgs a;
@@ -430,9 +443,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   // write_flat_kernel: K and V rows hold H * D consecutive elements and the
   // chunk count is a power of two.
-  auto row_dense = [&](const Geom &g) {
-    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
-  };
+  auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim); };
   a.nchunks_log2 = log2_exact(a.nchunks);
   wl.flat_grid = 0;
   if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
@@ -469,8 +480,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   // power-of-two row length, take gather_ragged_tile_kernel.
   const int64_t row_elems_all = (int64_t)p.heads * p.head_dim;
   auto rows_contig = [&](const Geom &g) {
-    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim &&
-           g.s_off == row_elems_all;
+    return row_elems_contiguous(g, p.head_dim) && (g.s_off == row_elems_all || p.block_size == 1);
   };
   const bool ragged_tile =
       p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv) &&
@@ -511,7 +521,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     }
   }
   const int ge = pick_chunk(p.gk, p.gv, base_k, base_v, cs, p.dst_k,
-                            p.dst_v, is, p.head_dim, max_bytes);
+                            p.dst_v, is, p.head_dim, max_bytes, p.block_size);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
 
   GatherArgs a;
@@ -552,8 +562,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   // Rows of a block form one contiguous run when each row is H*D
   // consecutive elements and consecutive offsets are one row apart.
   auto rows_contiguous = [&](const Geom &g) {
-    return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim &&
-           g.s_off == row_elems;
+    return row_elems_contiguous(g, p.head_dim) && (g.s_off == row_elems || p.block_size == 1);
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
@@ -564,9 +573,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     // rows.  Rows that are H*D contiguous elements (any row stride) and a
     // power-of-two chunk count take the flat kernel; otherwise the row
     // kernel, with at least one full pass of its row groups.
-    auto row_dense = [&](const Geom &g) {
-      return g.s_inner == 1 && g.pack == p.head_dim && g.s_head == p.head_dim;
-    };
+    auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim); };
     a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
     if (ragged_tile && a.nchunks_log2 >= 0) {
       // R rows of about KVX_FLAT_TILE_BYTES of cache per tensor: a power of

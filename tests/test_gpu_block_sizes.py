@@ -1,0 +1,163 @@
+"""GPU parity of blocks at the ends of the block-size range, through the C
+ABI, bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:93-124 write
+and :226-267 gather semantics).
+
+Blocks of one token: every dense layout (HND, x-packed, token axis
+innermost) then stores a row as H * D consecutive elements and takes the
+row-major kernels (write_flat_kernel, gather_flat_kernel, the RAGGED tile
+and KV_OFFSETS flat gathers), for copies and FP8 casts.
+
+Blocks of 128 and 256 tokens take paths that smaller ones do not:
+  gather_rows_kernel   a block's rows split over several workgroups (HND
+      rows whose 64 KiB tile does not fit LDS, padded blocks, FP8 heads of
+      40 bytes with the dequantizing op), parts that start past seq_len,
+      parts cut by seq_len, and ids < 0 or >= num_blocks;
+  gather_tiles_kernel  tiles of one 128-byte line per row (x-packed and
+      token-innermost blocks, 16 and 32 KiB tiles) and 32 KiB HND tiles.
+"""
+import pytest
+import torch
+
+from kvx_amd.abi import DType, ScaleGranularity as SG
+
+import numpy as np
+
+from kvx_amd import paged
+from kvx_amd.abi import Layout
+
+from gpu_helpers import (TORCH_DT, OffsetsPool, ScaleArg, check_gather, check_gather_offsets,
+                         check_gather_ragged, check_write, custom_cache, random_fill)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+# (cache dtype, K order, K x, V order, V x, block_size, H, D, pad)
+CASES = [
+    (DType.BF16, "bhod", None, "bhod", None, 256, 8, 128, 0),   # HND: row kernel, split
+    (DType.BF16, "bhod", None, "bhod", None, 128, 8, 128, 0),   # HND: 32 KiB tiles
+    (DType.BF16, "bhpox", 8, "bohd", None, 256, 8, 128, 0),     # x-packed: 128-byte tiles
+    (DType.BF16, "bhdo", None, "bhpox", 8, 128, 8, 128, 0),     # token-innermost / x-packed
+    (DType.F16, "obhd", None, "hbod", None, 128, 4, 64, 1),     # padded: row kernel, split
+    (DType.F32, "bhod", None, "bohd", None, 256, 2, 64, 0),     # 512-byte HND runs, NHD V
+]
+
+
+def _ids(c):
+    return f"{c[0].name}-{c[1]}{c[2] or ''}-{c[3]}{c[4] or ''}-bs{c[5]}-H{c[6]}-D{c[7]}-pad{c[8]}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+@pytest.mark.parametrize("idx64", [False, True])
+def test_big_block_gather(case, idx64):
+    dt, ko_, kx, vo_, vx, bs, H, D, pad = case
+    gen = torch.Generator().manual_seed(900 + CASES.index(case) * 2 + int(idx64))
+    nb = 10
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen, pad=pad)
+    S = 4
+    L = 2 * bs + bs // 2 + 3  # a partial last block
+    mbps = (L + bs - 1) // bs
+    table = torch.randint(0, nb, (S, mbps), generator=gen)
+    table[1, 0], table[2, 1] = -1, nb + 1
+    # a full row, one past max_seq_len, lengths that end inside a block's
+    # first, middle and last parts
+    lens = torch.tensor([L, L + bs, bs + 5, 2 * bs - 3])
+    itype = torch.int64 if idx64 else torch.int32
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather(pc, kb, vb, ko, vo, table.to(itype).to(DEV), lens.to(itype).to(DEV), L,
+                 cache_dtype=dt, io_dtype=dt)
+
+
+@pytest.mark.parametrize("kind", ["tensor", SG.PER_BLOCK_HEAD])
+@pytest.mark.parametrize("fp8", [DType.F8_E4M3, DType.F8_E5M2])
+def test_big_block_dequant_row_split(fp8, kind):
+    """FP8 HND heads of 40 bytes (no 16-byte pieces for a tile) in blocks of
+    256 tokens: the dequantizing row kernel, each block in two parts."""
+    gen = torch.Generator().manual_seed(950 + int(fp8) + 2 * (kind != "tensor"))
+    H, D, bs, nb = 8, 40, 256, 8
+    pc, kb, vb = custom_cache(fp8, nb, bs, H, D, "bhod", "bhod", None, None, gen)
+    S, L = 3, 2 * bs + 17
+    table = torch.randint(-1, nb, (S, (L + bs - 1) // bs), generator=gen).to(torch.int32)
+    lens = torch.tensor([L, 300, 9], dtype=torch.int32)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    if kind == "tensor":
+        ks, vs = 0.021, 0.0043
+    else:
+        ks, vs = (ScaleArg(kind, torch.empty(nb, H).uniform_(0.002, 0.05, generator=gen).numpy(),
+                           stride=(1, nb)) for _ in range(2))
+    check_gather(pc, kb, vb, ko, vo, table.to(DEV), lens.to(DEV), L, cache_dtype=fp8,
+                 io_dtype=DType.BF16, k_scale=ks, v_scale=vs)
+
+
+ONE = [("bhod", None, "bhod", None), ("bhpox", 8, "bhdo", None), ("bhdo", None, "bohd", None)]
+
+
+@pytest.mark.parametrize("orders", ONE, ids=["hnd", "xpacked-tokinner", "tokinner-nhd"])
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F8_E4M3])
+def test_one_token_blocks(orders, dt):
+    """Decode and prefill writes, PACKED and RAGGED gathers of blocks of one
+    token; FP8 caches quantize bf16 rows and dequantize to bf16."""
+    ko_, kx, vo_, vx = orders
+    seed = 980 + ONE.index(orders) * 2 + (dt != DType.BF16)
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    H, D, nb = 8, 64, 600
+    pc, kb, vb = custom_cache(dt, nb, 1, H, D, ko_, vo_, kx, vx, gen)
+    fp8 = dt != DType.BF16
+    io = DType.BF16
+    ks, vs = (0.013, 0.0071) if fp8 else (None, None)
+    # decode: scattered slots, some -1 or past the pool
+    T = 37
+    slots = torch.randperm(nb, generator=gen)[:T]
+    slots[3], slots[8] = -1, nb + 2
+    key = (torch.randn((T, H, D), generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    val = torch.randn((T, H, D), generator=gen).to(torch.bfloat16).to(DEV)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=dt,
+                k_scale=ks, v_scale=vs)
+    # prefill: 3 chunks of 64 tokens, each on its own random blocks
+    S, tps = 3, 64
+    ids = torch.randperm(nb, generator=gen)[: S * tps]
+    key = (torch.randn((S * tps, H, D), generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    val = torch.randn((S * tps, H, D), generator=gen).to(torch.bfloat16).to(DEV)
+    check_write(pc, kb, vb, key, val, ids.to(DEV), io_dtype=io, cache_dtype=dt,
+                tokens_per_seq=tps, k_scale=ks, v_scale=vs)
+    # PACKED and RAGGED gathers of those sequences, plus invalid ids
+    L = tps + 3
+    table = torch.full((S, L), -1, dtype=torch.int32)
+    table[:, :tps] = ids.reshape(S, tps).to(torch.int32)
+    table[1, 5], table[2, 9] = -1, nb + 1
+    lens = torch.tensor([L, tps, 17], dtype=torch.int32)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather(pc, kb, vb, ko, vo, table.to(DEV), lens.to(DEV), L, cache_dtype=dt,
+                 io_dtype=io, k_scale=ks, v_scale=vs)
+    counts = rng.integers(0, L + 3, size=S)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    indices = rng.integers(-1, nb + 2, size=max(int(indptr[-1]), 1)).astype(np.int32)
+    rt = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, rt, lens.to(DEV), L, cache_dtype=dt, io_dtype=io,
+                        k_scale=ks, v_scale=vs)
+
+
+@pytest.mark.parametrize("layout", [Layout.BLOCK_HND, Layout.BLOCK_HND_PACKED])
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F8_E5M2])
+def test_one_token_blocks_kv_offsets(layout, dt):
+    """KV_OFFSETS gathers of one-token HND / x-packed blocks from a primary
+    and a secondary pool."""
+    seed = 990 + (layout == Layout.BLOCK_HND_PACKED) * 2 + (dt != DType.BF16)
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed)
+    H, D, nb, S, L = 4, 128, 300, 4, 50
+    pool = OffsetsPool(layout, layout, dt, nb, 1, H, D, pitch_pad=16, gen=gen)
+    raw = rng.integers(0, nb + 2, size=(S, 1, 2, L)).astype(np.uint32)
+    raw |= (rng.random(raw.shape) < 0.3).astype(np.uint32) << 31
+    offsets = torch.from_numpy(raw.view(np.int32)).to(DEV)
+    lens = torch.from_numpy(rng.integers(-1, L + 4, size=S).astype(np.int32)).to(DEV)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks, vs = (0.02, 0.005) if dt != DType.BF16 else (None, None)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=DType.BF16,
+                         k_scale=ks, v_scale=vs)
