@@ -122,8 +122,9 @@ def parse_args():
                         "config), or ascending as a fresh allocator hands blocks out (the "
                         "gather then reads the pool front to back)")
     p.add_argument("--block-size", type=int, default=None,
-                   help="c2: tokens per block (a power of two; the config's is 16), same "
-                        "lengths, the pool drawn in blocks of this size")
+                   help="c2 / c3: tokens per block (a power of two; the configs' is 16), "
+                        "same lengths (c2) or chunks and pool tokens (c3), the pool drawn in "
+                        "blocks of this size")
     p.add_argument("--c3-shift", type=int, default=0,
                    help="c3: every chunk starts this many tokens (0-15) into its first "
                         "block, as a chunked prefill continuing a chunk that ended inside "
@@ -223,7 +224,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     tdt = {DType.BF16: torch.bfloat16, DType.F16: torch.float16,
            DType.F8_E4M3: torch.float8_e4m3fn, DType.F8_E5M2: torch.float8_e5m2}
     if name == "c3":
-        w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order, shift=c3_shift)
+        w = W.c3_llama8b_prefill(seqs=c3_seqs, order=c3_order, shift=c3_shift,
+                                 block_size=block_size or 16)
     elif name == "c2":
         w = W.c2_llama8b_decode(order=c2_order, block_size=block_size or 16)
     else:
@@ -239,8 +241,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
     reshape_rows(w, name, heads, head_dim)
-    if block_size is not None and name != "c2":
-        raise SystemExit("--block-size applies to c2")
+    if block_size is not None and name not in ("c2", "c3"):
+        raise SystemExit("--block-size applies to c2 and c3")
     if layout is not None:
         if name not in ("c2", "c3", "c5"):
             raise SystemExit("--layout applies to c2, c3 and c5")

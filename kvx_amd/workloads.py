@@ -221,7 +221,8 @@ def c2_llama8b_decode(seed: int = 2, batch: int = 256, order: str = "random",
 
 
 def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs: int = 16,
-                       order: str = "random", shift: int = 0) -> Workload:
+                       order: str = "random", shift: int = 0,
+                       block_size: int = 16) -> Workload:
     """c3; `seqs` chunks of 2048 tokens over a pool of 512 blocks per
     sequence (16 and 8192 as configured).  order "random": the sequences'
     blocks are a seeded random draw from the pool; "ascending": sequence s
@@ -232,12 +233,15 @@ def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs:
     blocks (ascending's footprint, random order).  shift > 0: every chunk
     covers positions shift .. shift + 2047 of its sequence, so it starts
     inside its first block (as a chunked prefill does after a chunk that
-    ended inside a block) and takes one more block."""
-    if not 0 <= shift < 16:
+    ended inside a block) and takes one more block.  block_size other than
+    the config's 16 keeps the pool's tokens (8192 per sequence)."""
+    if block_size <= 0 or block_size & (block_size - 1) or block_size > 2048:
+        raise ValueError(block_size)
+    if not 0 <= shift < block_size:
         raise ValueError(shift)
     rng = np.random.Generator(np.random.PCG64(seed))
-    S, chunk, bs = seqs, 2048, 16
-    pool = 512 * S
+    S, chunk, bs = seqs, 2048, block_size
+    pool = 8192 // bs * S
     mbps = (shift + chunk + bs - 1) // bs
     draw = rng.permutation(pool)[: S * mbps]
     if order == "random":
@@ -260,6 +264,8 @@ def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs:
         name += f"_{order}"
     if shift:
         name += f"_shift{shift}"
+    if bs != 16:
+        name += f"_bs{bs}"
     return Workload(name, seed, 8, 128, bs, pool,
                     DType.BF16, DType.BF16, Layout.BLOCK_HND_PACKED, Layout(v_layout), 8,
                     slots.astype(np.int64), chunk, table,

@@ -113,3 +113,16 @@ def test_c2_block_size_keeps_lengths():
     assert sorted(b.block_table[b.block_table >= 0].tolist()) == list(range(b.num_blocks))
     with pytest.raises(ValueError):
         W.c2_llama8b_decode(block_size=48)
+
+
+def test_c3_block_size_keeps_chunks():
+    from kvx_amd import workloads as W
+
+    a, b = W.c3_llama8b_prefill(), W.c3_llama8b_prefill(block_size=128)
+    assert (a.name, a.num_blocks, a.block_table.shape) == (
+        "c3_llama3_8b_prefill_packedK_bf16", 8192, (16, 128))
+    assert b.name == a.name + "_bs128" and b.num_blocks == 1024 and b.block_table.shape == (16, 16)
+    assert W.write_bytes(a) == W.write_bytes(b)
+    assert len(set(b.slots.tolist())) == b.slots.size and (b.slots // 128 < 1024).all()
+    with pytest.raises(ValueError):
+        W.c3_llama8b_prefill(block_size=24)
