@@ -3,7 +3,9 @@ that do not need the CPU oracle to run at that size:
 
   - write -> gather round trip: every written row comes back bit-exact at its
     sequence position (c2 also on vLLM's x-packed K / token-innermost V pair,
-    with PACKED and RAGGED tables);
+    with PACKED and RAGGED tables; c2 and c3 also with other rows and block
+    sizes: HND heads of 96 or 80 elements, three heads, blocks of 1, 128
+    and 256 tokens);
   - the whole gather equals an independent implementation (torch advanced
     indexing of the paged cache on int16 views), row by row, and rows past
     seq_len keep the output's prior contents;
@@ -316,6 +318,106 @@ def test_one_kv_head_rank_shape(cfg):
     assert torch.equal(i16(vo[seq[ok], pos[ok]]), i16(val[ok]))
     check_gather_against_indexing(pc, w, ko, vo, kb, vb)
     ragged_equals_packed(pc, w, ko, vo, kb, vb)
+
+
+SHAPES = [  # (name, K / V layout, heads, head_dim, block_size)
+    ("hnd_8x96", Layout.BLOCK_HND, 8, 96, 16),          # tiles of whole 192-byte runs
+    ("xpacked_3x128", Layout.BLOCK_HND_PACKED, 3, 128, 16),  # 768-byte tile rows
+    ("xpacked_bs256", Layout.BLOCK_HND_PACKED, 8, 128, 256),  # 128-byte tile rows
+    ("hnd_bs256", Layout.BLOCK_HND, 8, 128, 256),        # row kernel, 16 parts per block
+    ("hnd_bs1", Layout.BLOCK_HND, 8, 128, 1),            # one-token blocks: row-major kernels
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[c[0] for c in SHAPES])
+def test_c2_full_other_shapes(shape):
+    """c2's lengths, slots and table for other rows and block sizes: decode
+    write, then gather; checked against the slots, against indexing, by the
+    round trip of the written tokens, and against the RAGGED form of the
+    table."""
+    _, lay, H, D, bs = shape
+    w = workloads.c2_llama8b_decode(block_size=bs)
+    w.heads, w.head_dim = H, D
+    pc = paged.alloc_cache(w.num_blocks, bs, H, D, torch.bfloat16, DEV, lay, lay, w.pack)
+    pc.key_cache.normal_()
+    pc.value_cache.normal_()
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots) == Status.OK
+    torch.cuda.synchronize()
+    ok = slots >= 0
+    blk, off = slots[ok] // bs, slots[ok] % bs
+    kview, vview = block_view(pc.key_cache, lay, w.pack), block_view(pc.value_cache, lay, w.pack)
+    assert torch.equal(i16(kview[blk, off]), i16(key[ok]))
+    assert torch.equal(i16(vview[blk, off]), i16(val[ok]))
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16, 3)
+    kb, vb = ko.clone(), vo.clone()
+    lens = torch.tensor(w.seq_lens, device=DEV)
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV), lens, L) == Status.OK
+    torch.cuda.synchronize()
+    seq = torch.arange(S, device=DEV)
+    pos = lens.long() - 1
+    assert torch.equal(i16(ko[seq[ok], pos[ok]]), i16(key[ok]))
+    assert torch.equal(i16(vo[seq[ok], pos[ok]]), i16(val[ok]))
+    check_gather_against_indexing(pc, w, ko, vo, kb, vb)
+    ragged_equals_packed(pc, w, ko, vo, kb, vb)
+
+
+WRITE_SHAPES = [  # (name, layouts, heads, head_dim, block_size)
+    ("xpacked_3x128", "packed", 3, 128, 16),
+    ("vllm_3x128", "vllm", 3, 128, 16),
+    ("hnd_8x80", "hnd", 8, 80, 16),
+    ("hnd_bs128", "hnd", 8, 128, 128),
+    ("vllm_bs1", "vllm", 8, 128, 1),
+]
+
+
+@pytest.mark.parametrize("shape", WRITE_SHAPES, ids=[c[0] for c in WRITE_SHAPES])
+def test_c3_full_other_shapes(shape):
+    """c3's prefill chunks into caches of other rows and block sizes (tiles
+    of whole runs, the per-token path of 128-token blocks, one-token
+    blocks): every written row in place, untouched blocks unchanged, and the
+    gather returning the input rows."""
+    _, lay, H, D, bs = shape
+    w = workloads.c3_llama8b_prefill(block_size=bs)
+    w.heads, w.head_dim = H, D
+    nb = w.num_blocks
+    if lay == "vllm":
+        kc = torch.empty(paged.cache_shape(Layout.BLOCK_HND_PACKED, nb, bs, H, D, 8),
+                         dtype=torch.bfloat16, device=DEV)
+        vstore = torch.empty((nb, H, D, bs), dtype=torch.bfloat16, device=DEV)
+        pc = paged.PagedCache(kc, paged.custom_view(vstore, "bhdo"), Layout.BLOCK_HND_PACKED,
+                              Layout.BLOCK_CUSTOM, nb, bs, H, D)
+        fills = (kc, vstore)
+    else:
+        code = {"packed": Layout.BLOCK_HND_PACKED, "hnd": Layout.BLOCK_HND}[lay]
+        pc = paged.alloc_cache(nb, bs, H, D, torch.bfloat16, DEV, code, code, 8)
+        fills = (pc.key_cache, pc.value_cache)
+    for t in fills:
+        i16(t).fill_(-7)
+    key = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    val = torch.randn((w.num_tokens, H, D), device=DEV).to(torch.bfloat16)
+    slots = torch.tensor(w.slots, device=DEV)
+    assert paged.write_kv(pc, key, val, slots, tokens_per_seq=w.tokens_per_seq) == Status.OK
+    torch.cuda.synchronize()
+    kview = block_view(pc.key_cache, pc.k_layout, 8)
+    vview = block_view(pc.value_cache, pc.v_layout, 8)
+    blk, off = slots // bs, slots % bs
+    assert torch.equal(i16(kview[blk, off]), i16(key))
+    assert torch.equal(i16(vview[blk, off]), i16(val))
+    used = torch.zeros(nb, dtype=torch.bool, device=DEV)
+    used[torch.tensor(w.block_table, device=DEV).long().flatten()] = True
+    for t in fills:
+        assert bool((i16(t[~used]) == -7).all())
+    S, L = w.seq_count, w.max_seq_len
+    ko, vo = sentinel_like((S, L, H, D), torch.bfloat16), sentinel_like((S, L, H, D), torch.bfloat16)
+    assert paged.gather_kv(pc, ko, vo, torch.tensor(w.block_table, device=DEV),
+                           torch.tensor(w.seq_lens, device=DEV), L) == Status.OK
+    torch.cuda.synchronize()
+    assert torch.equal(i16(ko.reshape(-1, H, D)), i16(key))
+    assert torch.equal(i16(vo.reshape(-1, H, D)), i16(val))
 
 
 def test_token_write_grid_stride_loop():
