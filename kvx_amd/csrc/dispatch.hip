@@ -28,16 +28,17 @@ bool aligned(const void *p, int64_t b) {
 
 // True when chunks of g elements (g*esize bytes each) stay inside one
 // contiguous cache piece and every cache address they use is aligned.  A
-// block of one token never steps by the offset stride (a size-1 axis, whose
-// stride can be anything, e.g. 1 for vLLM's [num_blocks, H, D, 1] value
-// cache).
+// block of one token never steps by the offset stride, nor a cache of one
+// head by the head stride (size-1 axes, whose strides can be anything, e.g.
+// 1 for vLLM's [num_blocks, H, D, 1] value cache).
 bool cache_chunk_ok(const Geom &g, const void *base, int esize, int head_dim,
-                    int ge, int64_t block_size) {
+                    int ge, int64_t block_size, int64_t heads) {
   const int64_t bytes = (int64_t)ge * esize;
   if (ge > 1 && g.s_inner != 1) return false;
   if (g.pack % ge != 0 || head_dim % ge != 0) return false;
   if (!aligned(base, bytes)) return false;
-  const int64_t strides[4] = {g.s_block, block_size == 1 ? 0 : g.s_off, g.s_head, g.s_piece};
+  const int64_t strides[4] = {g.s_block, block_size == 1 ? 0 : g.s_off, heads == 1 ? 0 : g.s_head,
+                              g.s_piece};
   for (int64_t st : strides) {
     if ((st * esize) % bytes != 0) return false;
   }
@@ -48,10 +49,10 @@ bool cache_chunk_ok(const Geom &g, const void *base, int esize, int head_dim,
 // side is contiguous with rows of H*D elements of io_size bytes.
 int pick_chunk(const Geom &gk, const Geom &gv, const void *ck, const void *cv,
                int cache_size, const void *ik, const void *iv, int io_size,
-               int head_dim, int max_chunk_bytes_cache, int64_t block_size) {
+               int head_dim, int max_chunk_bytes_cache, int64_t block_size, int64_t heads) {
   for (int ge = max_chunk_bytes_cache / cache_size; ge >= 1; ge /= 2) {
-    if (!cache_chunk_ok(gk, ck, cache_size, head_dim, ge, block_size)) continue;
-    if (!cache_chunk_ok(gv, cv, cache_size, head_dim, ge, block_size)) continue;
+    if (!cache_chunk_ok(gk, ck, cache_size, head_dim, ge, block_size, heads)) continue;
+    if (!cache_chunk_ok(gv, cv, cache_size, head_dim, ge, block_size, heads)) continue;
     const int64_t io_bytes = (int64_t)ge * io_size;
     if (!aligned(ik, io_bytes) || !aligned(iv, io_bytes)) continue;
     return ge;
@@ -83,10 +84,12 @@ int log2_exact(int64_t v) {
 // Row (head, dim) elements at consecutive addresses: row-major layouts, and
 // any dense layout whose block holds one row (HND, x-packed or token axis
 // innermost with block_size 1 store a row as H * D consecutive elements).
-// On MI355X (c2's lengths in one-token blocks) such gathers took 1592-1615 us
-// per layer in the flat kernel against 3517-3551 us in the tile kernels.
-bool row_elems_contiguous(const Geom &g, int64_t D) {
-  return g.s_inner == 1 && g.s_head == D && (g.pack == D || g.s_piece == g.pack);
+// With one head the head stride is never used (HND with H = 1 is row-major
+// whenever rows are D elements apart).  On MI355X (c2's lengths in
+// one-token blocks) such gathers took 1592-1615 us per layer in the flat
+// kernel against 3517-3551 us in the tile kernels.
+bool row_elems_contiguous(const Geom &g, int64_t D, int64_t H) {
+  return g.s_inner == 1 && (g.s_head == D || H == 1) && (g.pack == D || g.s_piece == g.pack);
 }
 
 // Elements of one per-token contiguous run when `g` is a dense block in
@@ -94,7 +97,8 @@ bool row_elems_contiguous(const Geom &g, int64_t D) {
 // (e / W) * bs * W + o * W + e % W, else -1: W = H * D (row-major), D (HND),
 // x (x-packed) or 1 (token axis innermost).  Any block stride.
 int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
-  if (bs == 1 && row_elems_contiguous(g, D)) return H * D;  // one row: row-major
+  // one row, or rows of one head D elements apart: row-major
+  if (row_elems_contiguous(g, D, H) && (bs == 1 || g.s_off == H * D)) return H * D;
   const int64_t p = g.pack;
   const bool split = p < D;  // d = (d / p) * p + d % p with its own strides
   if (g.s_inner == 1 && (!split || g.s_piece == p)) {
@@ -116,6 +120,12 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 // tile (8 KiB measured best against 4 and 16 KiB).
 #ifndef KVX_TILE_BYTES
 #define KVX_TILE_BYTES 8192
+#endif
+#ifndef KVX_TILE_SMALL_BYTES
+#define KVX_TILE_SMALL_BYTES 4096
+#endif
+#ifndef KVX_TILE_SMALL_THREADS
+#define KVX_TILE_SMALL_THREADS 128
 #endif
 // Narrowest tile width (cache bytes per row) the halving above goes to.
 #ifndef KVX_TILE_MIN_WIDTH
@@ -267,6 +277,13 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   t->cpr = (int32_t)(tw / src_chunk);
   t->cpr_magic = t->tw_log2 < 0 ? magic_for(t->cpr) : 0;
   t->pitch = (int32_t)pitch;
+  // Tiles of at most KVX_TILE_SMALL_BYTES run in KVX_TILE_SMALL_THREADS-thread
+  // workgroups: twice as many resident workgroups per CU, so as many bytes
+  // in flight as the 8 KiB tiles of wider rows.  On MI355X (c2's table, one
+  // KV head) x-packed gathers took 198.8 us against 259.9 us in 256-thread
+  // workgroups and 209.7 us in 64-thread ones; HND two-token blocks 1585
+  // against 2058 us per layer.
+  t->threads = tw * bs <= KVX_TILE_SMALL_BYTES ? KVX_TILE_SMALL_THREADS : kBlockThreads;
   t->max_seq_len = p.max_seq_len;
   t->num_blocks = p.num_blocks;
   t->head_dim = p.head_dim;
@@ -289,7 +306,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   }
   *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
   *lds_bytes = (uint32_t)(bs * pitch);
-  return grid_fits(*grid, kBlockThreads);
+  return grid_fits(*grid, t->threads);
 }
 
 // Tiled block write plan (write_tiles_kernel): at least bs tokens,
@@ -410,7 +427,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int is = dtype_size((kvx_dtype_t)p.io_dtype);
   const int max_bytes = (p.conv == kConvQuant) ? 8 : 16;
   const int ge = pick_chunk(p.gk, p.gv, p.dst_k, p.dst_v, cs, p.src_k,
-                            p.src_v, is, p.head_dim, max_bytes, p.block_size);
+                            p.src_v, is, p.head_dim, max_bytes, p.block_size, p.heads);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
 
   WriteArgs a;
@@ -443,7 +460,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
   // write_flat_kernel: K and V rows hold H * D consecutive elements and the
   // chunk count is a power of two.
-  auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim); };
+  auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim, p.heads); };
   a.nchunks_log2 = log2_exact(a.nchunks);
   wl.flat_grid = 0;
   if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
@@ -480,7 +497,8 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   // power-of-two row length, take gather_ragged_tile_kernel.
   const int64_t row_elems_all = (int64_t)p.heads * p.head_dim;
   auto rows_contig = [&](const Geom &g) {
-    return row_elems_contiguous(g, p.head_dim) && (g.s_off == row_elems_all || p.block_size == 1);
+    return row_elems_contiguous(g, p.head_dim, p.heads) &&
+           (g.s_off == row_elems_all || p.block_size == 1);
   };
   const bool ragged_tile =
       p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv) &&
@@ -521,7 +539,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     }
   }
   const int ge = pick_chunk(p.gk, p.gv, base_k, base_v, cs, p.dst_k,
-                            p.dst_v, is, p.head_dim, max_bytes, p.block_size);
+                            p.dst_v, is, p.head_dim, max_bytes, p.block_size, p.heads);
   const int64_t row_elems = (int64_t)p.heads * p.head_dim;
 
   GatherArgs a;
@@ -562,7 +580,8 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   // Rows of a block form one contiguous run when each row is H*D
   // consecutive elements and consecutive offsets are one row apart.
   auto rows_contiguous = [&](const Geom &g) {
-    return row_elems_contiguous(g, p.head_dim) && (g.s_off == row_elems || p.block_size == 1);
+    return row_elems_contiguous(g, p.head_dim, p.heads) &&
+           (g.s_off == row_elems || p.block_size == 1);
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
@@ -573,7 +592,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     // rows.  Rows that are H*D contiguous elements (any row stride) and a
     // power-of-two chunk count take the flat kernel; otherwise the row
     // kernel, with at least one full pass of its row groups.
-    auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim); };
+    auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim, p.heads); };
     a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
     if (ragged_tile && a.nchunks_log2 >= 0) {
       // R rows of about KVX_FLAT_TILE_BYTES of cache per tensor: a power of

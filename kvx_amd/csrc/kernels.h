@@ -1673,6 +1673,7 @@ struct TileArgs {
   int32_t cpr;            // tw_log2 < 0: phase-2 chunks per tile row
   uint32_t cpr_magic;     // tw_log2 < 0: div_magic's m for cpr
   int32_t pitch;          // LDS row pitch, bytes
+  int32_t threads;        // workgroup size (128 for small tiles, else 256)
   int32_t max_seq_len;
   int32_t num_blocks;
   int32_t head_dim;
@@ -1717,7 +1718,7 @@ __device__ __forceinline__ void stage_tile(const char *region, char *lds, int32_
                                            int32_t rows) {
   const int32_t bsm = (1 << bs_log2) - 1;
   const int32_t runm = (1 << run_log2) - 1;
-  constexpr int32_t kStep = kBlockThreads * 16;
+  const int32_t kStep = (int32_t)blockDim.x * 16;
   for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
     Raw<16> x[kTileLoads];
 #pragma unroll
@@ -1752,7 +1753,7 @@ __device__ __forceinline__ void stage_tile_rows(const char *src, int64_t s_block
                                                 int32_t rows) {
   const int32_t bsm = (1 << bs_log2) - 1;
   const int32_t runm = (1 << run_log2) - 1;
-  for (int32_t mm = (int32_t)threadIdx.x * PIECE; mm < nbytes; mm += kBlockThreads * PIECE) {
+  for (int32_t mm = (int32_t)threadIdx.x * PIECE; mm < nbytes; mm += (int32_t)blockDim.x * PIECE) {
     const int32_t o = (mm >> run_log2) & bsm;
     if (o >= rows) continue;
     const int64_t id = ids[o];
@@ -1770,7 +1771,7 @@ __device__ __forceinline__ void stage_tile_odd(const char *region, char *lds, in
                                                int32_t run, uint32_t run_magic, int32_t bs_log2,
                                                int32_t pitch, int32_t rows) {
   const uint32_t bsm = (1u << bs_log2) - 1;
-  constexpr int32_t kStep = kBlockThreads * 16;
+  const int32_t kStep = (int32_t)blockDim.x * 16;
   for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
     Raw<16> x[kTileLoads];
     int32_t at[kTileLoads];
@@ -1800,7 +1801,7 @@ __device__ __forceinline__ void stage_tile_rows_odd(const char *src, int64_t s_b
                                                     int32_t run, uint32_t run_magic,
                                                     int32_t bs_log2, int32_t pitch, int32_t rows) {
   const uint32_t bsm = (1u << bs_log2) - 1;
-  for (int32_t mm = (int32_t)threadIdx.x * 16; mm < nbytes; mm += kBlockThreads * 16) {
+  for (int32_t mm = (int32_t)threadIdx.x * 16; mm < nbytes; mm += (int32_t)blockDim.x * 16) {
     const uint32_t q = div_magic((uint32_t)mm, run_magic);
     const int32_t o = (int32_t)(q & bsm);
     if (o >= rows) continue;
@@ -1826,12 +1827,12 @@ __device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const Til
   const int32_t total = ODD ? rows * a.cpr : rows << cpr_log2;
   const uint32_t e0 = ((uint32_t)tile * (uint32_t)a.tw) >> a.cache_es_log2;
   const int32_t cm = (1 << cpr_log2) - 1;
-  for (int32_t u0 = (int32_t)threadIdx.x; u0 < total; u0 += kTileLoads * kBlockThreads) {
+  for (int32_t u0 = (int32_t)threadIdx.x; u0 < total; u0 += kTileLoads * (int32_t)blockDim.x) {
     Raw<Op::kSrc> x[kTileLoads];
     int32_t rr[kTileLoads], cc[kTileLoads];
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
+      const int32_t u = u0 + k * (int32_t)blockDim.x;
       if constexpr (ODD) {
         rr[k] = (int32_t)div_magic((uint32_t)u, a.cpr_magic);
         cc[k] = u - rr[k] * a.cpr;
@@ -1843,7 +1844,7 @@ __device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const Til
     }
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
+      const int32_t u = u0 + k * (int32_t)blockDim.x;
       if (u < total) {
         const int32_t r = rr[k];
         int64_t rb = bid;
@@ -1952,7 +1953,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     const int32_t lo = tile * region;
     const int64_t valid = ((int64_t)rows << a.cache_es_log2) * re;
     const int32_t hi = (int32_t)(lo + region < valid ? lo + region : valid);
-    for (int32_t m = lo + (int32_t)threadIdx.x * Op::kSrc; m < hi; m += kBlockThreads * Op::kSrc) {
+    for (int32_t m = lo + (int32_t)threadIdx.x * Op::kSrc; m < hi; m += (int32_t)blockDim.x * Op::kSrc) {
       const uint32_t e = (uint32_t)m >> a.cache_es_log2;
       int64_t rb = bid;
       const char *b = blk;
@@ -2508,11 +2509,9 @@ template <class Op, int FMT, bool P64>
 void launch_tiles_fmt(const TileArgs &t, bool i64, int64_t grid, uint32_t lds, hipStream_t s) {
   const dim3 g((uint32_t)grid, 2);
   if (i64) {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, true, P64>), g, dim3(kBlockThreads), lds, s,
-                       t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, true, P64>), g, dim3(t.threads), lds, s, t);
   } else {
-    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, false, P64>), g, dim3(kBlockThreads), lds,
-                       s, t);
+    hipLaunchKernelGGL((gather_tiles_kernel<Op, FMT, false, P64>), g, dim3(t.threads), lds, s, t);
   }
 }
 

@@ -2,9 +2,8 @@
 ABI, bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:93-124 write
 and :226-267 gather semantics).
 
-Blocks of one token: every dense layout (HND, x-packed, token axis
-innermost) then stores a row as H * D consecutive elements and takes the
-row-major kernels (write_flat_kernel, gather_flat_kernel, the RAGGED tile
+Blocks of one token, and HND caches of one head: every such dense layout
+stores a row as H * D consecutive elements and takes the row-major kernels (write_flat_kernel, gather_flat_kernel, the RAGGED tile
 and KV_OFFSETS flat gathers), for copies and FP8 casts.
 
 Blocks of 128 and 256 tokens take paths that smaller ones do not:
@@ -161,3 +160,53 @@ def test_one_token_blocks_kv_offsets(layout, dt):
     ks, vs = (0.02, 0.005) if dt != DType.BF16 else (None, None)
     check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=DType.BF16,
                          k_scale=ks, v_scale=vs)
+
+
+HEAD1 = [("bhod", None, "bhod", None), ("bhpox", 8, "bhdo", None), ("bhpox", 8, "bohd", None)]
+
+
+@pytest.mark.parametrize("orders", HEAD1, ids=["hnd", "vllm-pair", "xpacked-nhd"])
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F8_E4M3])
+def test_one_head(orders, dt):
+    """One KV head (a tensor-parallel rank's shard): HND is then row-major
+    (flat kernels); x-packed and token-innermost blocks make 4 KiB tiles
+    (128-thread workgroups).  Decode and prefill writes, PACKED and RAGGED
+    gathers."""
+    ko_, kx, vo_, vx = orders
+    seed = 1010 + HEAD1.index(orders) * 2 + (dt != DType.BF16)
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    H, D, bs, nb = 1, 128, 16, 64
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    ks, vs = (0.013, 0.0071) if dt != DType.BF16 else (None, None)
+    T = 29
+    slots = torch.randperm(nb * bs, generator=gen)[:T]
+    slots[4] = -1
+    key = (torch.randn((T, H, D), generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    val = torch.randn((T, H, D), generator=gen).to(torch.bfloat16).to(DEV)
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=DType.BF16, cache_dtype=dt,
+                k_scale=ks, v_scale=vs)
+    S, tps = 3, 40
+    blocks = torch.randperm(nb, generator=gen)[: S * 4].reshape(S, 4)
+    pos = torch.arange(tps) + 5  # chunks starting inside their first block
+    ids = torch.cat([blocks[s, pos // bs] * bs + pos % bs for s in range(S)])
+    key = (torch.randn((S * tps, H, D), generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    val = torch.randn((S * tps, H, D), generator=gen).to(torch.bfloat16).to(DEV)
+    check_write(pc, kb, vb, key, val, ids.to(DEV), io_dtype=DType.BF16, cache_dtype=dt,
+                tokens_per_seq=tps, k_scale=ks, v_scale=vs)
+    L = 4 * bs
+    table = blocks.to(torch.int32)
+    table[1, 2] = -1
+    lens = torch.tensor([L, tps + 5, 7], dtype=torch.int32)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather(pc, kb, vb, ko, vo, table.to(DEV), lens.to(DEV), L, cache_dtype=dt,
+                 io_dtype=DType.BF16, k_scale=ks, v_scale=vs)
+    counts = rng.integers(0, L + 3, size=S)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    indices = rng.integers(-1, nb + 2, size=max(int(indptr[-1]), 1)).astype(np.int32)
+    rt = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    ko = random_fill(torch.empty((S, L, H, D), dtype=torch.bfloat16, device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, rt, lens.to(DEV), L, cache_dtype=dt,
+                        io_dtype=DType.BF16, k_scale=ks, v_scale=vs)

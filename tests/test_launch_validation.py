@@ -442,9 +442,9 @@ def big_gather(layout, S, L, H, D, bs, fmt="packed"):
 
 
 def test_gather_grid_past_hip_limits(kvx_lib):
-    # gather_rows_kernel (HND rows of 12 bytes: no LDS tile), 256 threads:
-    # 4096 x 4096 workgroups = 2^32 work-items
-    assert G(kvx_lib, *big_gather(Layout.BLOCK_HND, 4096, 65536, 1, 6, 16)) == UNS
+    # gather_rows_kernel (HND runs of 12 bytes, two heads: no LDS tile, not
+    # row-major), 256 threads: 4096 x 4096 workgroups = 2^32 work-items
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_HND, 4096, 65536, 2, 6, 16)) == UNS
     # gather_flat_kernel (canonical NHD), 128 threads, blocks no longer
     # split: 8192 x 4096 workgroups = 2^32 work-items
     assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16)) == UNS
