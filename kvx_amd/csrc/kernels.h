@@ -130,6 +130,13 @@ __device__ __forceinline__ uint32_t div_magic(uint32_t x, uint32_t m) { return _
 #define KVX_OFFSETS_TILE 1
 #endif
 constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
+// The copy gather takes per-tile entries for rows of at most this many
+// cache bytes: on MI355X (c2's table, bf16) one KV head (256-byte rows)
+// measured 200.8 against 211.7 us and two heads 413.9 against 423.0 us,
+// while c2's 2 KiB rows measured 1614.7 against 1526.5 us.
+#ifndef KVX_OFFSETS_TILE_COPY_ROW
+#define KVX_OFFSETS_TILE_COPY_ROW 512
+#endif
 // FP8 cache bytes per chunk of the dequantizing gathers (8 or 16): 16-byte
 // chunks measured 3% faster for the RAGGED kernels that load a block id per
 // chunk (gather_indexed_flat_kernel; half the id loads) and 20-40% slower
@@ -2198,11 +2205,13 @@ constexpr int indexed_flat_threads() {
                                                        : kBlockThreads;
 }
 
-template <class Op, int FMT, bool I64, bool P64>
+// TILE (KV_OFFSETS only): table entries per workgroup tile.
+template <class Op, int FMT, bool I64, bool P64,
+          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
 __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
     GatherArgs a) {
   constexpr int kT = indexed_flat_threads<Op, FMT>();
-  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled;
+  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
   const int64_t s = su;
@@ -2476,7 +2485,12 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
     }
   } else if constexpr (!P64) {
     if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
-      if (a.flat) {
+      if (a.flat && !Op::kScaled && kOffsetsTile &&
+          (int64_t)a.nchunks * Op::kSrc <= KVX_OFFSETS_TILE_COPY_ROW) {
+        hipLaunchKernelGGL(
+            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false, true>), g, b,
+            0, s, a);
+      } else if (a.flat) {
         hipLaunchKernelGGL(
             (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>), g, b, 0,
             s, a);
