@@ -121,11 +121,8 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 #ifndef KVX_TILE_BYTES
 #define KVX_TILE_BYTES 8192
 #endif
-#ifndef KVX_TILE_SMALL_BYTES
-#define KVX_TILE_SMALL_BYTES 4096
-#endif
-#ifndef KVX_TILE_SMALL_THREADS
-#define KVX_TILE_SMALL_THREADS 128
+#ifndef KVX_TILE_BYTES_PER_THREAD
+#define KVX_TILE_BYTES_PER_THREAD 32
 #endif
 // Narrowest tile width (cache bytes per row) the halving above goes to.
 #ifndef KVX_TILE_MIN_WIDTH
@@ -277,13 +274,16 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   t->cpr = (int32_t)(tw / src_chunk);
   t->cpr_magic = t->tw_log2 < 0 ? magic_for(t->cpr) : 0;
   t->pitch = (int32_t)pitch;
-  // Tiles of at most KVX_TILE_SMALL_BYTES run in KVX_TILE_SMALL_THREADS-thread
-  // workgroups: twice as many resident workgroups per CU, so as many bytes
-  // in flight as the 8 KiB tiles of wider rows.  On MI355X (c2's table, one
-  // KV head) x-packed gathers took 198.8 us against 259.9 us in 256-thread
-  // workgroups and 209.7 us in 64-thread ones; HND two-token blocks 1585
+  // Workgroups of about one thread per KVX_TILE_BYTES_PER_THREAD bytes of
+  // tile (64 to 256 threads): smaller tiles run in smaller workgroups, more
+  // of them resident per CU, so that as many bytes are in flight as for the
+  // 8 KiB tiles of wider rows.  On MI355X (c2's table, one KV head) 4 KiB
+  // x-packed tiles took 198.8 us in 128-thread workgroups against 259.9 us
+  // in 256-thread and 209.7 us in 64-thread ones; HND two-token blocks 1585
   // against 2058 us per layer.
-  t->threads = tw * bs <= KVX_TILE_SMALL_BYTES ? KVX_TILE_SMALL_THREADS : kBlockThreads;
+  t->threads = kBlockThreads;
+  while (t->threads > 64 && tw * bs < (int64_t)t->threads * KVX_TILE_BYTES_PER_THREAD)
+    t->threads /= 2;
   t->max_seq_len = p.max_seq_len;
   t->num_blocks = p.num_blocks;
   t->head_dim = p.head_dim;
