@@ -906,6 +906,7 @@ struct WriteTileArgs {
   int32_t cpr;            // tw_log2 < 0: phase-1 chunks per tile row
   uint32_t cpr_magic;     // tw_log2 < 0: div_magic's m for cpr
   int32_t pitch;          // LDS row pitch, bytes
+  int32_t threads;        // workgroup size (64-256, by tile bytes)
   int32_t bs_log2;
   int32_t run_log2[2];    // K, V: log2 bytes of a per-token run; -1 row-major;
                           // kRunOdd: run_bytes, a multiple of 16 bytes
@@ -960,7 +961,7 @@ __device__ __forceinline__ void unstage_tile(char *region, const char *lds, int3
                                              int32_t lo, int32_t hi) {
   const int32_t bsm = (1 << bs_log2) - 1;
   const int32_t runm = (1 << run_log2) - 1;
-  constexpr int32_t kStep = kBlockThreads * 16;
+  const int32_t kStep = (int32_t)blockDim.x * 16;
   for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
     Raw<16> x[kTileLoads];
     bool whole[kTileLoads];
@@ -1014,7 +1015,7 @@ __device__ __forceinline__ void unstage_tile_odd(char *region, const char *lds, 
                                                  int32_t run, uint32_t run_magic, int32_t bs_log2,
                                                  int32_t pitch, int32_t lo, int32_t hi) {
   const uint32_t bsm = (1u << bs_log2) - 1;
-  constexpr int32_t kStep = kBlockThreads * 16;
+  const int32_t kStep = (int32_t)blockDim.x * 16;
   for (int32_t m0 = (int32_t)threadIdx.x * 16; m0 < nbytes; m0 += kTileLoads * kStep) {
     Raw<16> x[kTileLoads];
     bool ok[kTileLoads];
@@ -1080,7 +1081,7 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
     const int32_t lo = tile * region > span_lo ? tile * region : span_lo;
     const int32_t hi = (tile + 1) * region < span_hi ? (tile + 1) * region : span_hi;
     const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
-    for (int32_t m = lo + tid * Op::kDst; m < hi; m += kBlockThreads * Op::kDst) {
+    for (int32_t m = lo + tid * Op::kDst; m < hi; m += (int32_t)blockDim.x * Op::kDst) {
       const uint32_t e = (uint32_t)(m - span_lo) >> wt.cache_es_log2;
       float sc = uniform;
       if constexpr (Op::kScaled && IDX) sc = scale_in_rows(sr, uniform, r.block, e, re, hd);
@@ -1097,11 +1098,11 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
   const int32_t cpr_log2 = wt.tw_log2 - kDstLog2;
   const int32_t total = ODD ? (r.hi - r.lo) * wt.cpr : (r.hi - r.lo) << cpr_log2;
   const uint32_t e0 = ((uint32_t)tile * (uint32_t)wt.tw) >> wt.cache_es_log2;
-  for (int32_t u0 = tid; u0 < total; u0 += kTileLoads * kBlockThreads) {
+  for (int32_t u0 = tid; u0 < total; u0 += kTileLoads * (int32_t)blockDim.x) {
     Raw<Op::kSrc> x[kTileLoads];
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
+      const int32_t u = u0 + k * (int32_t)blockDim.x;
       if (u < total) {
         const int32_t row = tile_row<ODD>(u, cpr_log2, wt);
         const int32_t col = tile_col<ODD>(u, row, cpr_log2, wt);
@@ -1112,7 +1113,7 @@ __device__ __forceinline__ void write_tile_run(const WriteArgs &a, const WriteTi
     }
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = u0 + k * kBlockThreads;
+      const int32_t u = u0 + k * (int32_t)blockDim.x;
       if (u < total) {
         const int32_t row = tile_row<ODD>(u, cpr_log2, wt);
         const int32_t col = tile_col<ODD>(u, row, cpr_log2, wt);
@@ -1166,7 +1167,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   const int32_t bs = 1 << wt.bs_log2;
   const int32_t region = wt.tw << wt.bs_log2;  // cache bytes of the tile
   const int32_t total = region >> kDstLog2;    // chunks of the tile
-  if (t0 + bs > a.num_tokens || total > kTileLoads * kBlockThreads) return false;
+  if (t0 + bs > a.num_tokens || total > kTileLoads * (int32_t)blockDim.x) return false;
   const int32_t run_log2 = v ? wt.run_log2[1] : wt.run_log2[0];
   const char *io = v ? a.src_v : a.src_k;
   const int tid = (int)threadIdx.x;
@@ -1193,7 +1194,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
     const char *src = io + tb * a.row_bytes;
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = tid + k * kBlockThreads;
+      const int32_t u = tid + k * (int32_t)blockDim.x;
       if (u < total) {
         x[k] = ld<Op::kSrc, kWriteNtLoad>(
             run_log2 < 0 ? src + ((int64_t)elem(u) << wt.io_es_log2)
@@ -1236,7 +1237,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
     const int64_t at_b = block_b * sb - (int64_t)k * rbc;
 #pragma unroll
     for (int q = 0; q < kTileLoads; ++q) {
-      const int32_t u = tid + q * kBlockThreads;
+      const int32_t u = tid + q * (int32_t)blockDim.x;
       if (u < total) {
         const int32_t m = tile * region + (u << kDstLog2);
         const bool in_a = m < k * rbc;
@@ -1275,7 +1276,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
     const uint32_t re = (uint32_t)a.nchunks * (uint32_t)a.chunk_elems;  // H * D
 #pragma unroll
     for (int k = 0; k < kTileLoads; ++k) {
-      const int32_t u = tid + k * kBlockThreads;
+      const int32_t u = tid + k * (int32_t)blockDim.x;
       if (u < total) {
         float sc = uniform;
         if constexpr (Op::kScaled && IDX) sc = scale_in_rows(sr, uniform, block, elem(u), re, hd);
@@ -1286,7 +1287,7 @@ __device__ __forceinline__ bool write_tile_block(const WriteArgs &a, const Write
   }
 #pragma unroll
   for (int k = 0; k < kTileLoads; ++k) {
-    const int32_t u = tid + k * kBlockThreads;
+    const int32_t u = tid + k * (int32_t)blockDim.x;
     if (u < total) {
       float sc = uniform;
       if constexpr (Op::kScaled && IDX) sc = scale_at(sr, uniform, block, elem(u), hd);
@@ -1346,8 +1347,9 @@ __global__ __launch_bounds__(kBlockThreads) void write_tiles_kernel(WriteArgs a,
   __syncthreads();
   const int32_t nruns = s_nruns;
   if (nruns == 0) {
+    const int wpb = (int)(blockDim.x / kWave);  // waves per workgroup
     write_group_tokens<TokOp, IDX>(a, t0 + s_own[0], s_own[1] - s_own[0], v, v ? vs : ks,
-                                   tile * kWavesPerBlock, wt.tiles * kWavesPerBlock);
+                                   tile * wpb, wt.tiles * wpb);
     return;
   }
   for (int32_t i = 0; i < nruns; ++i) {
@@ -2434,19 +2436,19 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
     if constexpr (Op::kScaled) {
       if (a.ksc.indexed || a.vsc.indexed) {
         if (odd)
-          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, true>), g, dim3(kBlockThreads),
+          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, true>), g, dim3(w.wt.threads),
                              w.tile_lds, s, a, w.wt);
         else
-          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, false>), g, dim3(kBlockThreads),
+          hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, true, false>), g, dim3(w.wt.threads),
                              w.tile_lds, s, a, w.wt);
         return;
       }
     }
     if (odd)
-      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, true>), g, dim3(kBlockThreads),
+      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, true>), g, dim3(w.wt.threads),
                          w.tile_lds, s, a, w.wt);
     else
-      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, false>), g, dim3(kBlockThreads),
+      hipLaunchKernelGGL((write_tiles_kernel<TOp, Op, false, false>), g, dim3(w.wt.threads),
                          w.tile_lds, s, a, w.wt);
   } else if (w.flat_grid > 0) {
     const dim3 g((uint32_t)w.flat_grid), b(kFlatThreads);
