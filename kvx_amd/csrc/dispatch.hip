@@ -500,8 +500,8 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
 kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   const int cs = dtype_size((kvx_dtype_t)p.cache_dtype);
   const int is = dtype_size((kvx_dtype_t)p.io_dtype);
-  // RAGGED gathers of caches whose block rows are contiguous, with a
-  // power-of-two row length, take gather_ragged_tile_kernel.
+  // RAGGED gathers of caches whose block rows are contiguous take
+  // gather_ragged_tile_kernel.
   const int64_t row_elems_all = (int64_t)p.heads * p.head_dim;
   auto rows_contig = [&](const Geom &g) {
     return row_elems_contiguous(g, p.head_dim, p.heads) &&
@@ -509,7 +509,6 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   };
   const bool ragged_tile =
       p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv) &&
-      log2_exact(row_elems_all) >= 0 &&
       (p.conv == kConvDequant ? KVX_RAGGED_TILE_DEQUANT != 0 : KVX_RAGGED_TILE_COPY != 0);
   const int max_bytes =
       p.conv != kConvDequant ? 16
@@ -593,15 +592,20 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
   a.nchunks_log2 = log2_exact(a.nchunks);
+  a.nchunks_magic = a.nchunks_log2 < 0 ? magic_for(a.nchunks) : 0;
   a.bs_log2 = log2_exact(p.block_size);
   if (p.format != KVX_BLOCK_TABLE_PACKED) {
     // indexed formats: tiles of rows, about TILE_BYTES of each tensor's cache
-    // rows.  Rows that are H*D contiguous elements (any row stride) and a
-    // power-of-two chunk count take the flat kernel; otherwise the row
-    // kernel, with at least one full pass of its row groups.
+    // rows.  Rows that are H*D contiguous elements (any row stride) take the
+    // flat kernels, which find a chunk's row by a shift or, for chunk counts
+    // that are not a power of two (DeepSeek's 576-element MLA rows: 72), by
+    // a multiply-high, exact while tile chunks * nchunks <= 2^32 (so at most
+    // 1024 chunks per row there); otherwise the row kernel, with at least
+    // one full pass of its row groups.
     auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim, p.heads); };
-    a.flat = row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0;
-    if (ragged_tile && a.nchunks_log2 >= 0) {
+    const bool chunks_ok = a.nchunks_log2 >= 0 || a.nchunks <= 1024;
+    a.flat = row_dense(p.gk) && row_dense(p.gv) && chunks_ok;
+    if (ragged_tile && chunks_ok) {
       // R rows of about KVX_FLAT_TILE_BYTES of cache per tensor: a power of
       // two <= 64 (one block id per lane) that divides block_size
       int64_t want = KVX_FLAT_TILE_BYTES / (row_elems * cs);

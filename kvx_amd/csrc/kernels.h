@@ -131,9 +131,12 @@ __device__ __forceinline__ uint32_t div_magic(uint32_t x, uint32_t m) { return _
 #endif
 constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
 // The copy gather takes per-tile entries for rows of at most this many
-// cache bytes: on MI355X (c2's table, bf16) one KV head (256-byte rows)
-// measured 200.8 against 211.7 us and two heads 413.9 against 423.0 us,
-// while c2's 2 KiB rows measured 1614.7 against 1526.5 us.
+// cache bytes, and for rows whose chunk count is not a power of two: on
+// MI355X (c2's table, bf16) one KV head (256-byte rows) measured 200.8
+// against 211.7 us and two heads 413.9 against 423.0 us, 576-element MLA
+// rows 1050 us against 1185 us per chunk (1142 us in gather_indexed_kernel)
+// and 6 x 128 rows 1290 against 1392 us, while c2's 2 KiB rows measured
+// 1614.7 against 1526.5 us.
 #ifndef KVX_OFFSETS_TILE_COPY_ROW
 #define KVX_OFFSETS_TILE_COPY_ROW 512
 #endif
@@ -1400,7 +1403,8 @@ struct GatherArgs {
   int32_t flat;  // cache rows of a block are contiguous for K and V
   int32_t split_log2;  // PACKED flat and row gathers: workgroups per block = 1 << split_log2
   int32_t format;      // kvx_block_table_format_t
-  int32_t nchunks_log2;  // indexed flat: nchunks is a power of two
+  int32_t nchunks_log2;  // log2(nchunks), or -1 when not a power of two
+  uint32_t nchunks_magic;  // nchunks_log2 < 0: div_magic's m for nchunks
   int32_t bs_log2;       // log2(block_size), or -1 when not a power of two
   int32_t ragged_tile;   // RAGGED: gather_ragged_tile_kernel
 };
@@ -1409,6 +1413,13 @@ struct GatherArgs {
 // output rows, or false when the block is skipped (past seq_len or
 // max_seq_len, beyond max_blocks_per_seq, or a block id outside
 // [0, num_blocks)).  seq_len and the block id are wave-uniform scalar loads.
+// Row of chunk gi of a run of rows of nchunks chunks each (the flat indexed
+// gathers): a shift when nchunks is a power of two, else a multiply-high
+// (dispatch keeps gi * nchunks <= 2^32).
+__device__ __forceinline__ uint32_t row_of_chunk(const GatherArgs &a, uint32_t gi) {
+  return a.nchunks_log2 >= 0 ? gi >> a.nchunks_log2 : div_magic(gi, a.nchunks_magic);
+}
+
 struct BlockJob {
   const char *ck;
   const char *cv;
@@ -2251,11 +2262,10 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
-  const uint32_t total = (uint32_t)rows << a.nchunks_log2;
+  const uint32_t total = (uint32_t)rows * (uint32_t)a.nchunks;
   const uint32_t both = 2 * total;
-  const uint32_t cmask = (1u << a.nchunks_log2) - 1u;
   const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
-  // Chunk f: K for f < total, V above; row r = index >> nchunks_log2.  Each
+  // Chunk f: K for f < total, V above; row r = index / nchunks.  Each
   // pass resolves kIndexedUnroll chunks' rows, then loads them all, then
   // stores them, so the table and data latencies overlap across chunks.
   for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * kT) {
@@ -2272,8 +2282,8 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
       sc[u] = isv[u] ? vs : ks;
       if (f < both) {
         const uint32_t gi = f - (isv[u] ? total : 0u);
-        const uint32_t r = gi >> a.nchunks_log2;
-        const uint32_t c = gi & cmask;
+        const uint32_t r = row_of_chunk(a, gi);
+        const uint32_t c = gi - r * (uint32_t)a.nchunks;
         if constexpr (kTile) {
           const char *base = isv[u] ? tv : tk;
           src[u] = base == nullptr ? nullptr
@@ -2349,7 +2359,7 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
-  const uint32_t total = (uint32_t)rows << a.nchunks_log2;
+  const uint32_t total = (uint32_t)rows * (uint32_t)a.nchunks;
   const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes;
   if (one) {
     flat_copy<Op>(a, a.src_k + first * a.gk.s_block + o0 * a.gk.s_off,
@@ -2358,11 +2368,10 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     return;
   }
   // Rows in several blocks (or skipped): chunk f is K for f < total, V
-  // above; row r = index >> nchunks_log2 takes its id from lane r.  The
+  // above; row r = index / nchunks takes its id from lane r.  The
   // loop trip count is the same for every thread, so every lane joins each
   // shuffle.
   const uint32_t both = 2 * total;
-  const uint32_t cmask = (1u << a.nchunks_log2) - 1u;
   for (uint32_t base = 0; base < both; base += U * kFlatThreads) {
     const char *src[U];
     char *dst[U];
@@ -2372,14 +2381,14 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
       const uint32_t f = base + u * kFlatThreads + threadIdx.x;
       const bool v = f >= total;
       const uint32_t gi = f - (v ? total : 0u);
-      const uint32_t r = f < both ? gi >> a.nchunks_log2 : 0u;
+      const uint32_t r = f < both ? row_of_chunk(a, gi) : 0u;
       const int32_t rid = __shfl(id, (int)r);
       src[u] = nullptr;
       dst[u] = nullptr;
       sc[u] = v ? vs : ks;
       if (f < both && rid >= 0) {
         const GeomBytes &g = v ? a.gv : a.gk;
-        const uint32_t c = gi & cmask;
+        const uint32_t c = gi - r * (uint32_t)a.nchunks;
         src[u] = (v ? a.src_v : a.src_k) + rid * g.s_block + (int64_t)(o0 + r) * g.s_off +
                  (int64_t)c * Op::kSrc;
         dst[u] = (v ? a.dst_v : a.dst_k) + out0 + (int64_t)r * a.out_row_bytes +
@@ -2488,7 +2497,7 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
   } else if constexpr (!P64) {
     if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
       if (a.flat && !Op::kScaled && kOffsetsTile &&
-          (int64_t)a.nchunks * Op::kSrc <= KVX_OFFSETS_TILE_COPY_ROW) {
+          ((int64_t)a.nchunks * Op::kSrc <= KVX_OFFSETS_TILE_COPY_ROW || a.nchunks_log2 < 0)) {
         hipLaunchKernelGGL(
             (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false, true>), g, b,
             0, s, a);

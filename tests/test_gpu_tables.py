@@ -297,6 +297,40 @@ def test_kv_offsets_trtllm_pairs():
                          io_dtype=DType.BF16)
 
 
+ODD_CHUNKS = [(1, 576, DType.BF16), (6, 128, DType.BF16), (3, 80, DType.F16),
+              (1, 576, DType.F8_E4M3)]
+
+
+@pytest.mark.parametrize("shape", ODD_CHUNKS, ids=["mla576", "6x128", "f16-3x80", "fp8-mla576"])
+@pytest.mark.parametrize("spoil", [0, 4])
+def test_row_major_chunk_counts_not_pow2(shape, spoil):
+    """Canonical NHD caches whose rows hold a chunk count that is not a power
+    of two (DeepSeek's 576-element MLA rows: 72 chunks; 6 x 128; 3 x 80):
+    the RAGGED row-tile kernel (one-block and per-row paths, with `spoil`
+    ids spoiled) and the KV_OFFSETS flat kernel (per-tile and per-chunk
+    table entries), copies and the FP8 dequantizing gather."""
+    H, D, dt = shape
+    seed = 7500 + ODD_CHUNKS.index(shape) * 2 + (spoil > 0)
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator().manual_seed(seed)
+    fp8 = dt == DType.F8_E4M3
+    io = DType.BF16 if fp8 else dt
+    ks, vs = (0.019, 0.0043) if fp8 else (None, None)
+    bs, nb = 16, 40
+    pc, kb, vb = make_cache(NHD, NHD, dt, nb, bs, H, D, gen=gen)
+    S, L = 5, 120
+    table = block_run_table(rng, S, L, nb, bs, np.int32, np.int64, spoil=spoil)
+    lens = lens_tensor(rng, S, L, np.int32)
+    ko, vo = out_pair(S, L, H, D, io, gen)
+    check_gather_ragged(pc, kb, vb, ko, vo, table, lens, L, cache_dtype=dt, io_dtype=io,
+                        k_scale=ks, v_scale=vs)
+    pool = OffsetsPool(NHD, NHD, dt, nb, bs, H, D, pitch_pad=32, gen=gen)
+    offsets = offsets_table(rng, S, (L + bs - 1) // bs, nb)
+    ko, vo = out_pair(S, L, H, D, io, gen)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=io,
+                         k_scale=ks, v_scale=vs)
+
+
 def test_ragged_malformed_indptr_stays_in_bounds():
     """indptr that decreases or points past the indices array: rows whose
     token index falls outside [0, indices_count) are skipped, the rest
