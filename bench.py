@@ -97,11 +97,11 @@ def parse_args():
                         "KVX_LAYOUT_BLOCK_CUSTOM [num_blocks, H, D, block_size], vLLM's "
                         "paged-attention pair (PACKED / RAGGED tables only)")
     p.add_argument("--heads", type=int, default=None,
-                   help="c2 / c3 / c5: KV heads per GPU (one tensor-parallel rank's shard is "
+                   help="c2 - c5: KV heads per GPU (one tensor-parallel rank's shard is "
                         "8 / TP; 6 or 12 are other models' counts); the block table, "
                         "lengths and slots are unchanged")
     p.add_argument("--head-dim", type=int, default=None,
-                   help="c2 / c3 / c5: elements per head (a multiple of 8, e.g. 96 or 80); "
+                   help="c2 - c5: elements per head (a multiple of 8, e.g. 96 or 80); "
                         "heads x head_dim may not exceed the config's 8 x 128")
     p.add_argument("--fp8", default="e4m3", choices=["e4m3", "e5m2"],
                    help="c4: FP8 format of the cache")
@@ -191,15 +191,15 @@ class Built:
 
 
 def reshape_rows(w, name, heads=None, head_dim=None):
-    """--heads / --head-dim: give c2's, c3's or c5's rows another head count or head size
+    """--heads / --head-dim: give c2's, c3's, c4's or c5's rows another head count or head size
     (the block table, lengths and slots stay); the row may not outgrow the config's,
     so the pools fit wherever the config does."""
     if heads is None and head_dim is None:
         return
     h = w.heads if heads is None else heads
     d = w.head_dim if head_dim is None else head_dim
-    if name not in ("c2", "c3", "c5"):
-        raise SystemExit("--heads / --head-dim apply to c2, c3 and c5")
+    if name not in ("c2", "c3", "c4", "c5"):
+        raise SystemExit("--heads / --head-dim apply to c2, c3, c4 and c5")
     if h <= 0 or d <= 0 or d % 8 != 0 or h * d > w.heads * w.head_dim:
         raise SystemExit("--heads and --head-dim: positive, head_dim a multiple of 8, "
                          f"heads x head_dim at most {w.heads} x {w.head_dim}")

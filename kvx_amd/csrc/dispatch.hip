@@ -465,14 +465,19 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   // 2-4% slower (8% with blocks in ascending order).
   wl.grid = (int)(want < 65536 ? want : 65536);
   wl.tiles = plan_write_tiles(p, cs, is, &wl.wt, &wl.tile_grid, &wl.tile_lds);
-  // write_flat_kernel: K and V rows hold H * D consecutive elements and the
-  // chunk count is a power of two.
+  // write_flat_kernel: K and V rows hold H * D consecutive elements.  A
+  // chunk count that is not a power of two (576-element MLA rows: 72) finds
+  // a chunk's token by multiply-high, exact while the largest flat index
+  // times nchunks stays within 2^32.
   auto row_dense = [&](const Geom &g) { return row_elems_contiguous(g, p.head_dim, p.heads); };
   a.nchunks_log2 = log2_exact(a.nchunks);
+  a.nchunks_magic = a.nchunks_log2 < 0 ? magic_for(a.nchunks) : 0;
   wl.flat_grid = 0;
-  if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && a.nchunks_log2 >= 0) {
-    const int64_t fg = (((int64_t)p.num_tokens << a.nchunks_log2) + kFlatThreads - 1) /
-                       kFlatThreads;
+  const int64_t flat_total = (int64_t)p.num_tokens * a.nchunks;
+  const bool flat_div_ok =
+      a.nchunks_log2 >= 0 || (flat_total + kFlatThreads) * a.nchunks <= (int64_t(1) << 32);
+  if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && flat_div_ok) {
+    const int64_t fg = (flat_total + kFlatThreads - 1) / kFlatThreads;
     if (grid_fits(fg, kFlatThreads)) wl.flat_grid = fg;  // else write_kernel's grid-stride loop
   }
   hipStream_t s = as_stream(stream);

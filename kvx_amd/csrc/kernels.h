@@ -560,7 +560,8 @@ struct WriteArgs {
   int32_t chunk_elems;  // G
   int32_t row_bytes;    // bytes of one io row
   int32_t lpt_log2;
-  int32_t nchunks_log2;  // write_flat_kernel: nchunks is a power of two
+  int32_t nchunks_log2;  // write_flat_kernel: log2(nchunks), or -1
+  uint32_t nchunks_magic;  // nchunks_log2 < 0: div_magic's m for nchunks
 };
 
 template <class Op>
@@ -674,9 +675,13 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
 template <class Op, bool S64, bool UNIFORM>
 __global__ __launch_bounds__(kFlatThreads) void write_flat_kernel(WriteArgs a) {
   const int64_t f = (int64_t)blockIdx.x * kFlatThreads + threadIdx.x;
-  const int64_t t = f >> a.nchunks_log2;
+  // token and chunk of f: shifts, or (chunk counts that are not a power of
+  // two, e.g. 576-element MLA rows) a multiply-high, which the launch keeps
+  // exact (f < 2^32 and f * nchunks <= 2^32)
+  const int64_t t = a.nchunks_log2 >= 0 ? f >> a.nchunks_log2
+                                        : (int64_t)div_magic((uint32_t)f, a.nchunks_magic);
   if (t >= a.num_tokens) return;
-  const int32_t c = (int32_t)(f & ((1 << a.nchunks_log2) - 1));
+  const int32_t c = (int32_t)(f - t * a.nchunks);
   const Raw<Op::kSrc> xk = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_k + t * a.row_bytes +
                                                            (int64_t)c * Op::kSrc);
   const Raw<Op::kSrc> xv = ld<Op::kSrc, kTokenWriteNtLoad>(a.src_v + t * a.row_bytes +

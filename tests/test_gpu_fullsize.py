@@ -423,21 +423,52 @@ def test_c3_full_other_shapes(shape):
 def test_token_write_grid_stride_loop():
     """A write of more rows than the per-token kernel's grid holds (65536
     workgroups of 4 waves, one row per wave): its waves loop over the
-    remaining rows.  Three heads make 48 chunks per row, not a power of two,
-    so the write takes write_kernel rather than write_flat_kernel.  NHD
-    caches, random distinct slots with -1 and out-of-range entries; every
-    written row and every untouched block is checked with torch indexing."""
+    remaining rows.  NHD caches whose head rows are padded (stride D + 8) are
+    neither row-dense nor dense blocks, so the write takes write_kernel.
+    Random distinct slots with -1 and out-of-range entries; every written
+    row, every pad element and every untouched block is checked with torch
+    indexing."""
     H, D, bs = 3, 128, 16
     T = 300_000
     nb = (T + T // 4) // bs
     gen = torch.Generator(device=DEV).manual_seed(77)
+    kst = torch.empty((nb, bs, H, D + 8), dtype=torch.bfloat16, device=DEV)
+    vst = torch.empty_like(kst)
+    kst.view(torch.int16).random_(generator=gen)
+    vst.view(torch.int16).random_(generator=gen)
+    pc = paged.PagedCache(kst[..., :D], vst[..., :D], Layout.BLOCK_NHD, Layout.BLOCK_NHD, nb, bs,
+                          H, D)
+    k0, v0 = kst.clone(), vst.clone()
+    slots = torch.randperm(nb * bs, generator=gen, device=DEV)[:T]
+    slots[torch.rand(T, generator=gen, device=DEV) < 0.05] = -1
+    slots[torch.rand(T, generator=gen, device=DEV) < 0.01] = nb * bs + 7  # past the blocks
+    key = torch.empty((T, H, D), dtype=torch.bfloat16, device=DEV).normal_(generator=gen)
+    val = torch.empty_like(key).normal_(generator=gen)
+    assert paged.write_kv(pc, key, val, slots) == Status.OK
+    torch.cuda.synchronize()
+    ok = (slots >= 0) & (slots < nb * bs)
+    want_k, want_v = k0.view(-1, H, D + 8), v0.view(-1, H, D + 8)
+    want_k[slots[ok], :, :D] = key[ok]
+    want_v[slots[ok], :, :D] = val[ok]
+    assert torch.equal(i16(kst).view(-1, H, D + 8), i16(want_k))
+    assert torch.equal(i16(vst).view(-1, H, D + 8), i16(want_v))
+
+
+def test_flat_write_rows_not_pow2_chunks():
+    """300,000 NHD rows of three heads (48 chunks, not a power of two): the
+    flat write finds each chunk's token by multiply-high over 14.4 M flat
+    indices.  Same checks as above."""
+    H, D, bs = 3, 128, 16
+    T = 300_000
+    nb = (T + T // 4) // bs
+    gen = torch.Generator(device=DEV).manual_seed(78)
     pc = paged.alloc_cache(nb, bs, H, D, torch.bfloat16, DEV)
     pc.key_cache.view(torch.int16).random_(generator=gen)
     pc.value_cache.view(torch.int16).random_(generator=gen)
     k0, v0 = pc.key_cache.clone(), pc.value_cache.clone()
     slots = torch.randperm(nb * bs, generator=gen, device=DEV)[:T]
     slots[torch.rand(T, generator=gen, device=DEV) < 0.05] = -1
-    slots[torch.rand(T, generator=gen, device=DEV) < 0.01] = nb * bs + 7  # past the blocks
+    slots[torch.rand(T, generator=gen, device=DEV) < 0.01] = nb * bs + 7
     key = torch.empty((T, H, D), dtype=torch.bfloat16, device=DEV).normal_(generator=gen)
     val = torch.empty_like(key).normal_(generator=gen)
     assert paged.write_kv(pc, key, val, slots) == Status.OK

@@ -20,7 +20,7 @@ from kvx_amd import paged
 from kvx_amd.abi import DType, Layout
 
 from gpu_helpers import (TORCH_DT, OffsetsPool, ScaleArg, check_gather_offsets,
-                         check_gather_ragged, make_cache, random_fill)
+                         check_gather_ragged, check_write, make_cache, random_fill)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -306,9 +306,10 @@ ODD_CHUNKS = [(1, 576, DType.BF16), (6, 128, DType.BF16), (3, 80, DType.F16),
 def test_row_major_chunk_counts_not_pow2(shape, spoil):
     """Canonical NHD caches whose rows hold a chunk count that is not a power
     of two (DeepSeek's 576-element MLA rows: 72 chunks; 6 x 128; 3 x 80):
-    the RAGGED row-tile kernel (one-block and per-row paths, with `spoil`
-    ids spoiled) and the KV_OFFSETS flat kernel (per-tile and per-chunk
-    table entries), copies and the FP8 dequantizing gather."""
+    the flat write (decode and prefill rows), the RAGGED row-tile kernel
+    (one-block and per-row paths, with `spoil` ids spoiled) and the
+    KV_OFFSETS flat kernel (per-tile table entries), copies and the FP8
+    quantizing write and dequantizing gather."""
     H, D, dt = shape
     seed = 7500 + ODD_CHUNKS.index(shape) * 2 + (spoil > 0)
     rng = np.random.default_rng(seed)
@@ -318,6 +319,16 @@ def test_row_major_chunk_counts_not_pow2(shape, spoil):
     ks, vs = (0.019, 0.0043) if fp8 else (None, None)
     bs, nb = 16, 40
     pc, kb, vb = make_cache(NHD, NHD, dt, nb, bs, H, D, gen=gen)
+    # writes first (write_flat_kernel with a multiply-high token lookup):
+    # decode rows to scattered slots, then a prefill run
+    T = 37
+    slots = torch.from_numpy(rng.permutation(nb * bs)[:T].astype(np.int64))
+    slots[5] = -1
+    for n, sl in ((T, slots), (64, torch.arange(64) + 3 * bs + 5)):
+        key = (torch.randn((n, H, D), generator=gen) * 2).to(TORCH_DT[io]).to(DEV)
+        val = torch.randn((n, H, D), generator=gen).to(TORCH_DT[io]).to(DEV)
+        check_write(pc, kb, vb, key, val, sl.to(DEV), io_dtype=io, cache_dtype=dt,
+                    k_scale=ks, v_scale=vs)
     S, L = 5, 120
     table = block_run_table(rng, S, L, nb, bs, np.int32, np.int64, spoil=spoil)
     lens = lens_tensor(rng, S, L, np.int32)
