@@ -190,19 +190,21 @@ class Built:
         self.extra = extra or {}
 
 
-def reshape_rows(w, name, heads=None, head_dim=None):
+def reshape_rows(w, name, heads=None, head_dim=None, room=1.0):
     """--heads / --head-dim: give c2's, c3's, c4's or c5's rows another head count or head size
-    (the block table, lengths and slots stay); the row may not outgrow the config's,
-    so the pools fit wherever the config does."""
+    (the block table, lengths and slots stay).  The row may outgrow the config's by at
+    most `room` (the caller's factor of memory to spare, e.g. fewer layers), so the pools
+    fit wherever the config does."""
     if heads is None and head_dim is None:
         return
     h = w.heads if heads is None else heads
     d = w.head_dim if head_dim is None else head_dim
     if name not in ("c2", "c3", "c4", "c5"):
         raise SystemExit("--heads / --head-dim apply to c2, c3, c4 and c5")
-    if h <= 0 or d <= 0 or d % 8 != 0 or h * d > w.heads * w.head_dim:
+    if h <= 0 or d <= 0 or d % 8 != 0 or h * d > w.heads * w.head_dim * room:
         raise SystemExit("--heads and --head-dim: positive, head_dim a multiple of 8, "
-                         f"heads x head_dim at most {w.heads} x {w.head_dim}")
+                         f"heads x head_dim at most {room:g} x {w.heads} x {w.head_dim} "
+                         "(c2 / c4: fewer --layers leave room for larger rows)")
     if heads is not None:
         w.name = f"{w.name}_h{h}"
     if head_dim is not None:
@@ -240,7 +242,13 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
         w.name = w.name.replace("fp8_e4m3", "fp8_e5m2")
     if scales != "tensor":
         w.name = f"{w.name}_scale_{scales}"
-    reshape_rows(w, name, heads, head_dim)
+    # larger rows fit when fewer layers (c2 / c4) or c3's single write leave room
+    room = 1.0
+    if name in ("c2", "c4") and layers_override:
+        room = max(1.0, w.layers / layers_override)
+    elif name == "c3":
+        room = 4.0
+    reshape_rows(w, name, heads, head_dim, room)
     if block_size is not None and name not in ("c2", "c3"):
         raise SystemExit("--block-size applies to c2 and c3")
     if layout is not None:

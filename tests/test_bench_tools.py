@@ -99,6 +99,11 @@ def test_reshape_rows():
     w = W.c3_llama8b_prefill()
     bench.reshape_rows(w, "c3", heads=6)
     assert (w.heads, w.head_dim) == (6, 128)
+    w = W.c2_llama8b_decode()
+    bench.reshape_rows(w, "c2", 8, 256, room=2.0)
+    assert (w.heads, w.head_dim) == (8, 256)
+    with pytest.raises(SystemExit):
+        bench.reshape_rows(W.c2_llama8b_decode(), "c2", 8, 256)
     for name_, h, d in [("c1", 4, None), ("c5", 12, 128), ("c5", None, 84), ("c5", 0, None)]:
         with pytest.raises(SystemExit):
             bench.reshape_rows(W.CONFIGS["c5"](), name_, h, d)
