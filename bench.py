@@ -122,8 +122,8 @@ def parse_args():
                         "config), or ascending as a fresh allocator hands blocks out (the "
                         "gather then reads the pool front to back)")
     p.add_argument("--block-size", type=int, default=None,
-                   help="c2 / c3: tokens per block (a power of two; the configs' is 16), "
-                        "same lengths (c2) or chunks and pool tokens (c3), the pool drawn in "
+                   help="c2 / c3 / c4: tokens per block (a power of two; the configs' is 16), "
+                        "same lengths (c2, c4) or chunks and pool tokens (c3), the pool drawn in "
                         "blocks of this size")
     p.add_argument("--c3-shift", type=int, default=0,
                    help="c3: every chunk starts this many tokens (0-15) into its first "
@@ -230,6 +230,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                                  block_size=block_size or 16)
     elif name == "c2":
         w = W.c2_llama8b_decode(order=c2_order, block_size=block_size or 16)
+    elif name == "c4":
+        w = W.c4_llama8b_fp8(block_size=block_size or 16)
     else:
         w = W.CONFIGS[name]()
     keep = []  # keeps every buffer and descriptor alive
@@ -249,8 +251,8 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     elif name == "c3":
         room = 4.0
     reshape_rows(w, name, heads, head_dim, room)
-    if block_size is not None and name not in ("c2", "c3"):
-        raise SystemExit("--block-size applies to c2 and c3")
+    if block_size is not None and name not in ("c2", "c3", "c4"):
+        raise SystemExit("--block-size applies to c2, c3 and c4")
     if layout is not None:
         if name not in ("c2", "c3", "c5"):
             raise SystemExit("--layout applies to c2, c3 and c5")

@@ -596,6 +596,8 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
   a.split_log2 = 0;
+  a.fold_log2 = 0;
+  a.units_per_seq = 0;
   a.nchunks_log2 = log2_exact(a.nchunks);
   a.nchunks_magic = a.nchunks_log2 < 0 ? magic_for(a.nchunks) : 0;
   a.bs_log2 = log2_exact(p.block_size);
@@ -647,9 +649,14 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
            ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
            a.split_log2 < 16 && grid_fits(blocks << (a.split_log2 + 1), kFlatThreads))
       ++a.split_log2;
-    const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // workgroups
+    const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // units
     if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
-    a.blocks_per_seq = (int32_t)per_seq;
+    // up to 1 << fold_log2 units per workgroup, strided by the workgroups
+    // per sequence (KVX_FLAT_FOLD_LOG2)
+    a.units_per_seq = (int32_t)per_seq;
+    if (per_seq >= KVX_FLAT_FOLD_MIN_UNITS && per_seq <= KVX_FLAT_FOLD_MAX_UNITS)
+      a.fold_log2 = KVX_FLAT_FOLD_LOG2;
+    a.blocks_per_seq = (int32_t)((per_seq + (1 << a.fold_log2) - 1) >> a.fold_log2);
   } else if (a.bs_log2 >= 0) {
     // gather_rows_kernel: a power-of-two block's rows split into
     // 1 << split_log2 equal ranges of at least KVX_ROWS_TILE_BYTES of cache

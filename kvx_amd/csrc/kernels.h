@@ -1412,6 +1412,8 @@ struct GatherArgs {
   uint32_t nchunks_magic;  // nchunks_log2 < 0: div_magic's m for nchunks
   int32_t bs_log2;       // log2(block_size), or -1 when not a power of two
   int32_t ragged_tile;   // RAGGED: gather_ragged_tile_kernel
+  int32_t fold_log2;     // PACKED flat gather: up to 1 << fold_log2 units per workgroup
+  int32_t units_per_seq;  // PACKED flat gather: (block, part) units per sequence
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -1533,39 +1535,81 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
   }
 }
 
+// Units (one 1 << split_log2 share of a block) per workgroup of
+// gather_flat_kernel, at most: 1 << KVX_FLAT_FOLD_LOG2, taken when a
+// sequence has KVX_FLAT_FOLD_MIN_UNITS to KVX_FLAT_FOLD_MAX_UNITS units.
+// The grid covers max_seq_len, so a decode batch's shorter sequences leave
+// workgroups that only load seq_len and exit; on MI355X such workgroups cost
+// wave launches (c2 with max_seq_len doubled at the same lengths: 1573 ->
+// 1699 us per layer).  Two units per workgroup, the second half a sequence
+// further on, measured on three boxes (same-box A/B medians, us per layer):
+// c2 1612.6 -> 1553.9 and 1609.4 -> 1547.7 (8192 units per sequence), c2
+// with every sequence at 8192 tokens 2954.6 -> 2915.2, c4 and c2 with four
+// heads (4096 units) 0.5-0.8% faster; 2048 units or fewer (one or two KV
+// heads) 0-2.8% slower, where the last sequences' two-unit workgroups
+// lengthen a short launch; c5 (32768 units) -3.9%, -1.2% and +1.7%.  Four
+// units were slower at every shape, and ordering the grid unit-major (all
+// sequences' first units first) 15-30% slower.
+#ifndef KVX_FLAT_FOLD_LOG2
+#define KVX_FLAT_FOLD_LOG2 1
+#endif
+#ifndef KVX_FLAT_FOLD_MIN_UNITS
+#define KVX_FLAT_FOLD_MIN_UNITS 4096
+#endif
+#ifndef KVX_FLAT_FOLD_MAX_UNITS
+#define KVX_FLAT_FOLD_MAX_UNITS 16384
+#endif
+constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
+
+// A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J
+// (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
+// below units_per_seq and seq_len; unit u is share u & (2^split_log2 - 1)
+// of logical block u >> split_log2.
 template <class Op, bool I64>
 __global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a) {
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
   const int64_t s = su;
   const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
-  const int32_t lb = w >> a.split_log2;
-  const int32_t part = w & ((1 << a.split_log2) - 1);
-  if (lb >= a.max_blocks_per_seq) return;
-  // seq_len and the block id do not depend on each other: load both at once.
+  // seq_len and the block ids do not depend on each other: load them at once.
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
-  const int64_t bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+  int64_t bid[kFlatFold];
+#pragma unroll
+  for (int i = 0; i < kFlatFold; ++i) {
+    const int32_t u = w + i * a.blocks_per_seq;
+    const int32_t lb = u >> a.split_log2;
+    bid[i] = -1;
+    if (i < (1 << a.fold_log2) && u < a.units_per_seq && lb < a.max_blocks_per_seq)
+      bid[i] = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
+  }
   const int64_t n = seq_len < a.max_seq_len ? seq_len : (int64_t)a.max_seq_len;
-  const int64_t t0 = (int64_t)lb * a.block_size;
-  if (t0 >= n || bid < 0 || bid >= a.num_blocks) return;
-  // The block's valid rows are `valid` consecutive chunks of K (and of V);
-  // this workgroup copies chunks [c0, c0 + per_part) of them.
-  const int64_t rem = n - t0;
-  const int64_t valid = (rem < a.block_size ? rem : (int64_t)a.block_size) * a.nchunks;
-  const int64_t per_part = ((int64_t)a.block_size * a.nchunks) >> a.split_log2;
-  const int64_t c0 = (int64_t)part * per_part;
-  if (c0 >= valid) return;
-  const int64_t cnt = valid - c0 < per_part ? valid - c0 : per_part;
   float ks = 1.0f;  // per-tensor values; indexed scales are looked up per chunk
   float vs = 1.0f;
   if constexpr (Op::kScaled) {
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
   }
-  const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes + c0 * Op::kDst;
-  flat_copy<Op>(a, a.src_k + bid * a.gk.s_block + c0 * Op::kSrc,
-                a.src_v + bid * a.gv.s_block + c0 * Op::kSrc, a.dst_k + out0, a.dst_v + out0,
-                cnt, ks, vs, bid, c0);
+  const int64_t per_part = ((int64_t)a.block_size * a.nchunks) >> a.split_log2;
+#pragma unroll
+  for (int i = 0; i < kFlatFold; ++i) {
+    const int32_t u = w + i * a.blocks_per_seq;
+    const int32_t lb = u >> a.split_log2;
+    const int32_t part = u & ((1 << a.split_log2) - 1);
+    const int64_t t0 = (int64_t)lb * a.block_size;
+    if (t0 >= n) break;  // later units lie further along the sequence
+    if (bid[i] < 0 || bid[i] >= a.num_blocks) continue;
+    // The block's valid rows are `valid` consecutive chunks of K (and of V);
+    // this unit is chunks [c0, c0 + per_part) of them.
+    const int64_t rem = n - t0;
+    const int64_t valid = (rem < a.block_size ? rem : (int64_t)a.block_size) * a.nchunks;
+    const int64_t c0 = (int64_t)part * per_part;
+    if (c0 >= valid) continue;
+    const int64_t cnt = valid - c0 < per_part ? valid - c0 : per_part;
+    const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes + c0 * Op::kDst;
+    flat_copy<Op>(a, a.src_k + bid[i] * a.gk.s_block + c0 * Op::kSrc,
+                  a.src_v + bid[i] * a.gv.s_block + c0 * Op::kSrc, a.dst_k + out0,
+                  a.dst_v + out0, cnt, ks, vs, bid[i], c0);
+  }
 }
 
 // Any other layout: rows go to (wave, lane group), each lane keeps the
@@ -2223,13 +2267,29 @@ constexpr int indexed_flat_threads() {
                                                        : kBlockThreads;
 }
 
-// TILE (KV_OFFSETS only): table entries per workgroup tile.
+// Threads per workgroup of the KV_OFFSETS gather with per-tile table
+// entries: with KVX_OFFSETS_TILE_FIT, enough for one pass of
+// kIndexedUnroll chunks per thread over the tile's K and V chunks, a power
+// of two from kWave to kBlockThreads; otherwise kBlockThreads.
+#ifndef KVX_OFFSETS_TILE_FIT
+#define KVX_OFFSETS_TILE_FIT 1
+#endif
+inline int offsets_tile_threads(const GatherArgs &a) {
+  if (KVX_OFFSETS_TILE_FIT == 0) return kBlockThreads;
+  const int64_t per_pass = 2 * (int64_t)a.rows_per_wg * a.nchunks / kIndexedUnroll;
+  int t = kWave;
+  while (t < kBlockThreads && t < per_pass) t *= 2;
+  return t;
+}
+
+// TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
+// threads as the launch gives (at most kBlockThreads).
 template <class Op, int FMT, bool I64, bool P64,
           bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
 __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
     GatherArgs a) {
-  constexpr int kT = indexed_flat_threads<Op, FMT>();
   constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
+  const uint32_t nt = kTile ? blockDim.x : (uint32_t)indexed_flat_threads<Op, FMT>();
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
   const int64_t s = su;
@@ -2273,14 +2333,14 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
   // Chunk f: K for f < total, V above; row r = index / nchunks.  Each
   // pass resolves kIndexedUnroll chunks' rows, then loads them all, then
   // stores them, so the table and data latencies overlap across chunks.
-  for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * kT) {
+  for (uint32_t base = threadIdx.x; base < both; base += kIndexedUnroll * nt) {
     const char *src[kIndexedUnroll];
     char *dst[kIndexedUnroll];
     bool isv[kIndexedUnroll];
     float sc[kIndexedUnroll];
 #pragma unroll
     for (int u = 0; u < kIndexedUnroll; ++u) {
-      const uint32_t f = base + u * kT;
+      const uint32_t f = base + u * nt;
       src[u] = nullptr;
       dst[u] = nullptr;
       isv[u] = f >= total;
@@ -2504,11 +2564,12 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
       if (a.flat && !Op::kScaled && kOffsetsTile &&
           ((int64_t)a.nchunks * Op::kSrc <= KVX_OFFSETS_TILE_COPY_ROW || a.nchunks_log2 < 0)) {
         hipLaunchKernelGGL(
-            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false, true>), g, b,
-            0, s, a);
+            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false, true>), g,
+            dim3(offsets_tile_threads(a)), 0, s, a);
       } else if (a.flat) {
+        const dim3 bt(Op::kScaled && kOffsetsTile ? offsets_tile_threads(a) : kBlockThreads);
         hipLaunchKernelGGL(
-            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>), g, b, 0,
+            (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>), g, bt, 0,
             s, a);
       } else {
         hipLaunchKernelGGL((gather_indexed_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>),

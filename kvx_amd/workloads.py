@@ -272,9 +272,9 @@ def c3_llama8b_prefill(seed: int = 3, v_layout: Layout = Layout.BLOCK_NHD, seqs:
                     np.full(S, shift + chunk, np.int32), shift + chunk)
 
 
-def c4_llama8b_fp8(seed: int = 4, batch: int = 128) -> Workload:
-    w = c2_llama8b_decode(seed, batch)
-    w.name = "c4_llama3_8b_decode_fp8_e4m3"
+def c4_llama8b_fp8(seed: int = 4, batch: int = 128, block_size: int = 16) -> Workload:
+    w = c2_llama8b_decode(seed, batch, block_size=block_size)
+    w.name = "c4_llama3_8b_decode_fp8_e4m3" + ("" if block_size == 16 else f"_bs{block_size}")
     w.cache_dtype = DType.F8_E4M3
     w.notes["calibration_seed"] = seed + 1000
     w.notes["io_sigma"] = 2.0

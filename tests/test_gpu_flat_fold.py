@@ -1,0 +1,79 @@
+"""GPU parity of the PACKED row-major gather when a workgroup takes two units
+of its sequence (gather_flat_kernel with sequences of 4096 to 16384 units,
+a unit being one power-of-two share of a block): unit w and unit w + J of
+sequence s, J the workgroups per sequence.  Bit-identical to the CPU oracle
+(kernels/kvx_paged_kv.cu:226-267 gather semantics).
+
+Lengths cover both units of a workgroup valid, the second one cut inside
+its block or part, the second one starting exactly at seq_len (the
+boundary J * block_size / parts), the first one cut, an empty sequence, a
+length past max_seq_len, tables narrower than max_seq_len, and block ids
+< 0 or >= num_blocks in either unit.
+"""
+import pytest
+import torch
+
+from kvx_amd.abi import DType, Layout, ScaleGranularity as SG
+
+from gpu_helpers import ScaleArg, TORCH_DT, check_gather, make_cache, random_fill
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+# (cache dtype, io dtype, H, D, block_size, blocks per sequence, table
+#  columns short of them, units per block)
+CASES = [
+    # 16-byte rows, 256-byte blocks: one unit per block, 4096 units
+    (DType.F16, DType.F16, 1, 8, 16, 4096, 0, 1),
+    # 16384 units, the top of the range
+    (DType.F16, DType.F16, 1, 8, 16, 16384, 0, 1),
+    # c2's rows: 32 KiB blocks in 16 units, 515 blocks (8240 units, the
+    # second unit of a workgroup starting half way through a block)
+    (DType.BF16, DType.BF16, 8, 128, 16, 515, 0, 16),
+    # the table three blocks narrower than max_seq_len
+    (DType.BF16, DType.BF16, 8, 128, 16, 515, 3, 16),
+    # FP8 E4M3 -> bf16: 16 KiB blocks of 8-byte chunks in 8 units
+    (DType.F8_E4M3, DType.BF16, 8, 128, 16, 512, 0, 8),
+    # FP8 E5M2 -> f16, 32-token blocks of 64-element rows: 4 units each
+    (DType.F8_E5M2, DType.F16, 4, 64, 32, 1100, 0, 4),
+]
+
+
+def _ids(c):
+    return (f"{c[0].name}-{c[1].name}-H{c[2]}-D{c[3]}-bs{c[4]}-{c[5]}blocks"
+            f"{'-short' + str(c[6]) if c[6] else ''}")
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+@pytest.mark.parametrize("idx64", [False, True])
+def test_two_units_per_workgroup(case, idx64):
+    cdt, iodt, H, D, bs, blocks, short, parts = case
+    assert 4096 <= (blocks - short) * parts <= 16384  # the two-unit range
+    gen = torch.Generator().manual_seed(1200 + CASES.index(case) * 2 + int(idx64))
+    L = blocks * bs
+    mbps = blocks - short
+    nb = max(64, mbps // 2)
+    pc, kb, vb = make_cache(Layout.BLOCK_NHD, Layout.BLOCK_NHD, cdt, nb, bs, H, D, gen=gen)
+    half = L // 2
+    # (table columns) * parts units per sequence in J = half as many
+    # workgroups: unit J begins at token L / 2 when the table covers L
+    lens = torch.tensor([L, half + 3 * bs + 5, half, half - 7, 0, L + 100, half + bs // 2])
+    S = lens.numel()
+    table = torch.randint(0, nb, (S, mbps), generator=gen)
+    # invalid ids in first units and in second units
+    table[0, 3], table[0, mbps // 2 + 1] = -1, nb + 5
+    table[1, mbps // 2 + 2] = -7
+    table[5, 1] = nb
+    itype = torch.int64 if idx64 else torch.int32
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks = vs = None
+    if cdt != iodt:
+        if CASES.index(case) % 2 == 0:
+            ks, vs = 0.0213, 0.0047
+        else:
+            ks, vs = (ScaleArg(SG.PER_BLOCK_HEAD,
+                               torch.empty(nb, H).uniform_(0.002, 0.05, generator=gen).numpy())
+                      for _ in range(2))
+    check_gather(pc, kb, vb, ko, vo, table.to(itype).to(DEV), lens.to(itype).to(DEV), L,
+                 cache_dtype=cdt, io_dtype=iodt, k_scale=ks, v_scale=vs)

@@ -446,8 +446,9 @@ def test_gather_grid_past_hip_limits(kvx_lib):
     # row-major), 256 threads: 4096 x 4096 workgroups = 2^32 work-items
     assert G(kvx_lib, *big_gather(Layout.BLOCK_HND, 4096, 65536, 2, 6, 16)) == UNS
     # gather_flat_kernel (canonical NHD), 128 threads, blocks no longer
-    # split: 8192 x 4096 workgroups = 2^32 work-items
-    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16)) == UNS
+    # split, 4096 blocks per sequence taken two per workgroup: 16384 x 2048
+    # workgroups = 2^32 work-items
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 16384, 65536, 1, 8, 16)) == UNS
     # gather_ragged_tile_kernel, 128 threads, 16 rows per workgroup
     assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16,
                                   fmt="ragged")) == UNS
