@@ -638,6 +638,14 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       a.rows_per_wg = (int32_t)rows;
       a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
     }
+    // the RAGGED tile and flat indexed gathers: up to 1 << fold_log2 tiles
+    // per workgroup, strided as in the PACKED row-major gather
+    a.units_per_seq = a.blocks_per_seq;
+    if (KVX_INDEXED_FOLD && (a.ragged_tile || a.flat) &&
+        a.blocks_per_seq >= KVX_FLAT_FOLD_MIN_UNITS && a.blocks_per_seq <= KVX_FLAT_FOLD_MAX_UNITS) {
+      a.fold_log2 = KVX_FLAT_FOLD_LOG2;
+      a.blocks_per_seq = (a.blocks_per_seq + (1 << a.fold_log2) - 1) >> a.fold_log2;
+    }
   } else if (a.flat) {
     // split a block's chunks into a power-of-two number of equal ranges of
     // about KVX_FLAT_TILE_BYTES of cache per tensor, while the grid stays

@@ -1560,6 +1560,11 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #define KVX_FLAT_FOLD_MAX_UNITS 16384
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
+// The same for the RAGGED tile and flat indexed gathers' row tiles (1), or
+// one tile per workgroup (0).
+#ifndef KVX_INDEXED_FOLD
+#define KVX_INDEXED_FOLD 1
+#endif
 
 // A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J
 // (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
@@ -2282,18 +2287,12 @@ inline int offsets_tile_threads(const GatherArgs &a) {
   return t;
 }
 
-// TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
-// threads as the launch gives (at most kBlockThreads).
-template <class Op, int FMT, bool I64, bool P64,
-          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
-__global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
-    GatherArgs a) {
-  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
-  const uint32_t nt = kTile ? blockDim.x : (uint32_t)indexed_flat_threads<Op, FMT>();
-  const uint32_t wg = blockIdx.x;
-  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
-  const int64_t s = su;
-  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
+// One tile (rows t0 .. t0 + rows_per_wg - 1 of sequence s) of
+// gather_indexed_flat_kernel, nt threads; false when the tile lies past the
+// sequence's end (or its table row), and so does every later one.
+template <class Op, int FMT, bool I64, bool P64, bool kTile>
+__device__ __forceinline__ bool indexed_flat_unit(const GatherArgs &a, int64_t s, int64_t t0,
+                                                  uint32_t nt) {
   // KV_OFFSETS tiles lie inside one block (rows_per_wg divides block_size).
   // kTile: the tile's K and V table entries are two scalar loads, issued with
   // the seq_len load; otherwise every chunk loads its own entry.
@@ -2302,11 +2301,11 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
   uint32_t lb = 0;
   if constexpr (kTile) {
     lb = (uint32_t)t0 >> a.bs_log2;
-    if (lb >= (uint32_t)a.max_blocks_per_seq) return;
+    if (lb >= (uint32_t)a.max_blocks_per_seq) return false;
   }
   int64_t n;
   int64_t start;
-  if (!indexed_extent<FMT, I64, P64, kTile>(a, s, t0, n, start, lb, &ek, &ev)) return;
+  if (!indexed_extent<FMT, I64, P64, kTile>(a, s, t0, n, start, lb, &ek, &ev)) return false;
   const char *tk = nullptr;
   const char *tv = nullptr;
   if constexpr (kTile) {
@@ -2317,7 +2316,7 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
     const int64_t vb = ev & 0x7FFFFFFFu;
     if (pk != nullptr && kb < a.num_blocks) tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
     if (pv != nullptr && vb < a.num_blocks) tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
-    if (tk == nullptr && tv == nullptr) return;
+    if (tk == nullptr && tv == nullptr) return true;
   }
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;
@@ -2381,6 +2380,28 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
         st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
   }
+  return true;
+}
+
+// TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
+// threads as the launch gives (at most kBlockThreads).  Workgroup w of
+// sequence s takes tiles w + i * J (J = blocks_per_seq, i < 1 << fold_log2)
+// below units_per_seq.
+template <class Op, int FMT, bool I64, bool P64,
+          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
+__global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
+    GatherArgs a) {
+  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
+  const uint32_t nt = kTile ? blockDim.x : (uint32_t)indexed_flat_threads<Op, FMT>();
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
+  for (int i = 0; i < (1 << a.fold_log2); ++i) {
+    const int32_t u = w + i * a.blocks_per_seq;
+    if (u >= a.units_per_seq ||
+        !indexed_flat_unit<Op, FMT, I64, P64, kTile>(a, su, (int64_t)u * a.rows_per_wg, nt))
+      return;
+  }
 }
 
 // RAGGED gather of caches whose block rows are contiguous (canonical NHD
@@ -2396,16 +2417,15 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
 // every chunk takes its row's id from the lane that loaded it, and rows
 // whose id is < 0 or >= num_blocks are skipped.  No chunk loads an index of
 // its own.
+// One tile (rows t0 .. t0 + rows_per_wg - 1 of sequence s) of
+// gather_ragged_tile_kernel; false when the tile lies past the sequence's
+// end, and so does every later one.
 template <class Op, bool I64, bool P64>
-__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
+__device__ __forceinline__ bool ragged_tile_unit(const GatherArgs &a, int64_t s, int64_t t0) {
   constexpr int U = Op::kScaled ? kFlatUnrollDequant : kFlatUnroll;
-  const uint32_t wg = blockIdx.x;
-  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
-  const int64_t s = su;
-  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
   int64_t n;
   int64_t start;
-  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return;
+  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return false;
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;  // <= 64
   const int lane = (int)(threadIdx.x & (kWave - 1));
@@ -2430,7 +2450,7 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     flat_copy<Op>(a, a.src_k + first * a.gk.s_block + o0 * a.gk.s_off,
                   a.src_v + first * a.gv.s_block + o0 * a.gv.s_off, a.dst_k + out0,
                   a.dst_v + out0, total, ks, vs, first, 0);
-    return;
+    return true;
   }
   // Rows in several blocks (or skipped): chunk f is K for f < total, V
   // above; row r = index / nchunks takes its id from lane r.  The
@@ -2470,6 +2490,22 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     for (int u = 0; u < U; ++u) {
       if (src[u] != nullptr) st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
+  }
+  return true;
+}
+
+// Workgroup w of sequence s takes tiles w + i * J (J = blocks_per_seq,
+// i < 1 << fold_log2) below units_per_seq.
+template <class Op, bool I64, bool P64>
+__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
+  for (int i = 0; i < (1 << a.fold_log2); ++i) {
+    const int32_t u = w + i * a.blocks_per_seq;
+    if (u >= a.units_per_seq ||
+        !ragged_tile_unit<Op, I64, P64>(a, su, (int64_t)u * a.rows_per_wg))
+      return;
   }
 }
 

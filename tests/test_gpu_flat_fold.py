@@ -1,8 +1,10 @@
-"""GPU parity of the PACKED row-major gather when a workgroup takes two units
-of its sequence (gather_flat_kernel with sequences of 4096 to 16384 units,
-a unit being one power-of-two share of a block): unit w and unit w + J of
-sequence s, J the workgroups per sequence.  Bit-identical to the CPU oracle
-(kernels/kvx_paged_kv.cu:226-267 gather semantics).
+"""GPU parity of the row-major gathers when a workgroup takes two units of
+its sequence: gather_flat_kernel (PACKED) with sequences of 4096 to 16384
+units, a unit being one power-of-two share of a block, and the RAGGED tile
+and flat indexed gathers (RAGGED, KV_OFFSETS) with 4096 to 16384 row tiles:
+unit w and unit w + J of sequence s, J the workgroups per sequence.
+Bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:226-267 gather
+semantics; KVX_SPEC.md:99-122 for the indexed tables).
 
 Lengths cover both units of a workgroup valid, the second one cut inside
 its block or part, the second one starting exactly at seq_len (the
@@ -77,3 +79,78 @@ def test_two_units_per_workgroup(case, idx64):
                       for _ in range(2))
     check_gather(pc, kb, vb, ko, vo, table.to(itype).to(DEV), lens.to(itype).to(DEV), L,
                  cache_dtype=cdt, io_dtype=iodt, k_scale=ks, v_scale=vs)
+
+
+# RAGGED and KV_OFFSETS gathers take two row tiles per workgroup the same
+# way when a sequence has 4096 to 16384 tiles.
+# (path, cache dtype, io dtype, H, D, rows per tile, tiles per sequence)
+INDEXED = [
+    ("ragged_tile", DType.BF16, DType.BF16, 8, 128, 1, 8197),     # one 2 KiB row per tile
+    ("ragged_tile", DType.F16, DType.F16, 1, 8, 16, 4099),        # 16 rows, mixed block ids
+    ("ragged_tile", DType.F8_E4M3, DType.BF16, 8, 128, 2, 4100),  # dequantizing
+    ("ragged_flat", DType.BF16, DType.BF16, 8, 128, 1, 4100),     # padded heads axis
+    ("offsets", DType.BF16, DType.BF16, 8, 128, 2, 4100),         # entries per chunk
+    ("offsets", DType.BF16, DType.BF16, 1, 128, 16, 4100),        # entries per tile (copy)
+    ("offsets", DType.F8_E4M3, DType.BF16, 8, 128, 4, 4100),      # entries per tile (dequant)
+]
+
+
+def _lens(L, r):
+    half = (L // r + 1) // 2 * r  # first row of the second tile of workgroup 0
+    return [L, half + 3 * r + 1, half, half - 1, 0, L + 100, half + r // 2 + 1]
+
+
+@pytest.mark.parametrize("case", INDEXED,
+                         ids=[f"{c[0]}-{c[1].name}-H{c[3]}-D{c[4]}-r{c[5]}" for c in INDEXED])
+def test_two_tiles_per_workgroup_indexed(case):
+    import numpy as np
+
+    from kvx_amd import paged
+
+    from gpu_helpers import (OffsetsPool, check_gather_offsets, check_gather_ragged)
+
+    path, cdt, iodt, H, D, r, tiles = case
+    idx = INDEXED.index(case)
+    rng = np.random.default_rng(1300 + idx)
+    gen = torch.Generator().manual_seed(1300 + idx)
+    bs, nb = 16, 48
+    L = tiles * r - (r // 2)  # a partial last tile
+    assert 4096 <= (L + r - 1) // r <= 16384
+    S = 7
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks, vs = (0.0213, 0.0047) if cdt != iodt else (None, None)
+    if path == "offsets":
+        pool = OffsetsPool(Layout.BLOCK_NHD, Layout.BLOCK_NHD, cdt, nb, bs, H, D,
+                           pitch_pad=64, gen=gen)
+        mbps = (L + bs - 1) // bs
+        raw = rng.integers(0, nb, size=(S, 1, 2, mbps)).astype(np.uint32)
+        raw |= (rng.random(raw.shape) < 0.3).astype(np.uint32) << 31  # secondary pool
+        raw[0, 0, 0, 5] = nb + 3          # invalid K entries in both halves
+        raw[0, 0, 1, mbps // 2 + 1] = 0x7FFFFFFF
+        raw[2, 0, :, mbps // 2] = nb      # both entries of a block invalid
+        offsets = torch.from_numpy(raw.view(np.int32)).to(DEV)
+        lens = torch.tensor(_lens(L, r), dtype=torch.int32, device=DEV)
+        check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=cdt, io_dtype=iodt,
+                             k_scale=ks, v_scale=vs)
+        return
+    pc, kb, vb = make_cache(Layout.BLOCK_NHD, Layout.BLOCK_NHD, cdt, nb, bs, H, D, gen=gen,
+                            k_pad=2 if path == "ragged_flat" else None,
+                            v_pad=2 if path == "ragged_flat" else None)
+    counts = np.array(_lens(L, r))
+    counts[5] = L + 3
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    # each sequence's tokens follow a block table, with corrupted entries
+    parts = []
+    for s in range(S):
+        t = np.arange(counts[s])
+        ids = rng.integers(0, nb, size=(counts[s] + bs - 1) // bs + 1)[t // bs]
+        parts.append(ids)
+    indices = np.concatenate(parts).astype(np.int32)
+    bad = rng.choice(indices.size, size=64, replace=False)
+    indices[bad] = rng.choice([-1, nb, nb + 9, 3], size=64)
+    rt = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    lens = torch.full((S,), L, dtype=torch.int32, device=DEV)
+    lens[3] = L // 3
+    check_gather_ragged(pc, kb, vb, ko, vo, rt, lens, L, cache_dtype=cdt, io_dtype=iodt,
+                        k_scale=ks, v_scale=vs)
