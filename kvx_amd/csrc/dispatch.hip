@@ -641,8 +641,10 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     // the RAGGED tile and flat indexed gathers: up to 1 << fold_log2 tiles
     // per workgroup, strided as in the PACKED row-major gather
     a.units_per_seq = a.blocks_per_seq;
-    if (KVX_INDEXED_FOLD && (a.ragged_tile || a.flat) &&
-        a.blocks_per_seq >= KVX_FLAT_FOLD_MIN_UNITS && a.blocks_per_seq <= KVX_FLAT_FOLD_MAX_UNITS) {
+    const int64_t fold_min = p.format == KVX_BLOCK_TABLE_RAGGED ? KVX_RAGGED_FOLD_MIN_UNITS
+                                                                : KVX_OFFSETS_FOLD_MIN_UNITS;
+    if (KVX_INDEXED_FOLD && (a.ragged_tile || a.flat) && a.blocks_per_seq >= fold_min &&
+        a.blocks_per_seq <= KVX_INDEXED_FOLD_MAX_UNITS) {
       a.fold_log2 = KVX_FLAT_FOLD_LOG2;
       a.blocks_per_seq = (a.blocks_per_seq + (1 << a.fold_log2) - 1) >> a.fold_log2;
     }

@@ -1561,9 +1561,27 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
 // The same for the RAGGED tile and flat indexed gathers' row tiles (1), or
-// one tile per workgroup (0).
+// one tile per workgroup (0), for sequences of KVX_RAGGED_FOLD_MIN_UNITS
+// (RAGGED) or KVX_OFFSETS_FOLD_MIN_UNITS (KV_OFFSETS) to
+// KVX_INDEXED_FOLD_MAX_UNITS tiles.  These workgroups load seq_len and the
+// indptr pair or table entries before any data, so two tiles gain more:
+// on MI355X (same-box A/B medians, us per layer) c2's RAGGED gather 1787
+// -> 1638, c4's 811 -> 744, c5's (32768 tiles) 2198 -> 2073, RAGGED with
+// one or two KV heads (512-2048 tiles) 4-7% faster; c2's KV_OFFSETS gather
+// 1874 -> 1805, c4's (2048 tiles) 662 -> 645, but KV_OFFSETS copies with
+// per-tile entries at 512 and 1024 tiles (one and two bf16 heads) 2-3%
+// slower.
 #ifndef KVX_INDEXED_FOLD
 #define KVX_INDEXED_FOLD 1
+#endif
+#ifndef KVX_RAGGED_FOLD_MIN_UNITS
+#define KVX_RAGGED_FOLD_MIN_UNITS 512
+#endif
+#ifndef KVX_OFFSETS_FOLD_MIN_UNITS
+#define KVX_OFFSETS_FOLD_MIN_UNITS 2048
+#endif
+#ifndef KVX_INDEXED_FOLD_MAX_UNITS
+#define KVX_INDEXED_FOLD_MAX_UNITS 65536
 #endif
 
 // A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J

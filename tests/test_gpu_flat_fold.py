@@ -82,11 +82,14 @@ def test_two_units_per_workgroup(case, idx64):
 
 
 # RAGGED and KV_OFFSETS gathers take two row tiles per workgroup the same
-# way when a sequence has 4096 to 16384 tiles.
+# way when a sequence has 512 (RAGGED) or 2048 (KV_OFFSETS) to 65536 tiles.
 # (path, cache dtype, io dtype, H, D, rows per tile, tiles per sequence)
 INDEXED = [
     ("ragged_tile", DType.BF16, DType.BF16, 8, 128, 1, 8197),     # one 2 KiB row per tile
     ("ragged_tile", DType.F16, DType.F16, 1, 8, 16, 4099),        # 16 rows, mixed block ids
+    ("ragged_tile", DType.F16, DType.F16, 1, 8, 16, 40001),       # 16 rows, 40001 tiles
+    ("ragged_tile", DType.BF16, DType.BF16, 1, 128, 8, 513),      # 513 tiles
+    ("offsets", DType.BF16, DType.BF16, 4, 128, 4, 2049),         # 2049 tiles
     ("ragged_tile", DType.F8_E4M3, DType.BF16, 8, 128, 2, 4100),  # dequantizing
     ("ragged_flat", DType.BF16, DType.BF16, 8, 128, 1, 4100),     # padded heads axis
     ("offsets", DType.BF16, DType.BF16, 8, 128, 2, 4100),         # entries per chunk
@@ -100,8 +103,11 @@ def _lens(L, r):
     return [L, half + 3 * r + 1, half, half - 1, 0, L + 100, half + r // 2 + 1]
 
 
-@pytest.mark.parametrize("case", INDEXED,
-                         ids=[f"{c[0]}-{c[1].name}-H{c[3]}-D{c[4]}-r{c[5]}" for c in INDEXED])
+def _indexed_ids(c):
+    return f"{c[0]}-{c[1].name}-H{c[3]}-D{c[4]}-r{c[5]}-{c[6]}tiles"
+
+
+@pytest.mark.parametrize("case", INDEXED, ids=[_indexed_ids(c) for c in INDEXED])
 def test_two_tiles_per_workgroup_indexed(case):
     import numpy as np
 
@@ -115,7 +121,7 @@ def test_two_tiles_per_workgroup_indexed(case):
     gen = torch.Generator().manual_seed(1300 + idx)
     bs, nb = 16, 48
     L = tiles * r - (r // 2)  # a partial last tile
-    assert 4096 <= (L + r - 1) // r <= 16384
+    assert (512 if path != "offsets" else 2048) <= (L + r - 1) // r <= 65536
     S = 7
     ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
     vo = random_fill(torch.empty_like(ko), gen)
