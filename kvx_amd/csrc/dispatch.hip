@@ -304,7 +304,16 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     t->t[i].run_magic = run_log2[i] == kRunOdd ? magic_for(run_bytes[i]) : 0;
     t->t[i].pad_ = 0;
   }
-  *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
+  // up to 1 << fold_log2 (block, tile) units per workgroup, strided by the
+  // workgroups per sequence
+  const int64_t units = (int64_t)t->blocks_per_seq * t->tiles;
+  if (units > 0x7FFFFFFF) return false;
+  t->units_per_seq = (int32_t)units;
+  t->fold_log2 = 0;
+  if (KVX_TILES_FOLD && units >= KVX_TILES_FOLD_MIN_UNITS && units <= KVX_TILES_FOLD_MAX_UNITS)
+    t->fold_log2 = KVX_FLAT_FOLD_LOG2;
+  t->wg_per_seq = (int32_t)((units + (1 << t->fold_log2) - 1) >> t->fold_log2);
+  *grid = (int64_t)p.seq_count * t->wg_per_seq;
   *lds_bytes = (uint32_t)(bs * pitch);
   return grid_fits(*grid, t->threads);
 }

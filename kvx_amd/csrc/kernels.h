@@ -1574,6 +1574,23 @@ constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
 #ifndef KVX_INDEXED_FOLD
 #define KVX_INDEXED_FOLD 1
 #endif
+// The same for the transposing gather's (block, tile) units
+// (gather_tiles_kernel), from KVX_TILES_FOLD_MIN_UNITS to
+// KVX_TILES_FOLD_MAX_UNITS units per sequence.  On MI355X (same-box A/B
+// medians, us per layer, c2's table in 8 KiB tiles) HND 1853 -> 1704,
+// x-packed 1862 -> 1715, vLLM's pair 1901 -> 1728 (one KV head 241 ->
+// 218), HND RAGGED 2015 -> 1769, c5 in HND blocks 2266 -> 2193; 128-token
+// HND blocks (16 KiB tiles, 1024 units) 1692 -> 1708.  A second unit
+// waits at a barrier for the first's LDS reads.
+#ifndef KVX_TILES_FOLD
+#define KVX_TILES_FOLD 1
+#endif
+#ifndef KVX_TILES_FOLD_MIN_UNITS
+#define KVX_TILES_FOLD_MIN_UNITS 512
+#endif
+#ifndef KVX_TILES_FOLD_MAX_UNITS
+#define KVX_TILES_FOLD_MAX_UNITS 65536
+#endif
 #ifndef KVX_RAGGED_FOLD_MIN_UNITS
 #define KVX_RAGGED_FOLD_MIN_UNITS 512
 #endif
@@ -1773,6 +1790,9 @@ struct TileArgs {
   int32_t bs_log2;
   int32_t cache_es_log2;  // log2 cache element bytes
   int32_t io_es_log2;     // log2 output element bytes
+  int32_t units_per_seq;  // (block, tile) units per sequence: blocks_per_seq * tiles
+  int32_t wg_per_seq;     // workgroups per sequence
+  int32_t fold_log2;      // up to 1 << fold_log2 units per workgroup
 };
 
 // Store piece k (PIECE bytes) of a 16-byte chunk at p.
@@ -1957,22 +1977,14 @@ __device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const Til
   }
 }
 
-// I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
-// indptr dtype.
+// One tile (tile `tile` of logical block lb of sequence s, the tensor of
+// blockIdx.y) of gather_tiles_kernel; false when the block lies past the
+// sequence's end (or its table row), and so does every later one.  s_ids
+// and s_same are the workgroup's shared RAGGED row ids.
 template <class Op, int FMT, bool I64, bool P64>
-__global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char lds[];
-  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
-  __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
-  const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
-  const uint32_t wg = blockIdx.x;
-  const uint32_t per_seq = (uint32_t)a.blocks_per_seq * (uint32_t)a.tiles;
-  const uint32_t su = wg / per_seq;
-  const uint32_t w = wg - su * per_seq;
-  const uint32_t lbu = w / (uint32_t)a.tiles;
-  const int32_t tile = (int32_t)(w - lbu * (uint32_t)a.tiles);
-  const int32_t lb = (int32_t)lbu;
-  const int64_t s = su;
+__device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTensor &tt,
+                                                 char *lds, int64_t *s_ids, int32_t &s_same,
+                                                 int64_t s, int32_t lb, int32_t tile) {
   const int64_t t0 = (int64_t)lb << a.bs_log2;
   const int32_t bs = 1 << a.bs_log2;
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
@@ -1989,7 +2001,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     cnt = left < cnt ? left : cnt;
     n = cnt < n ? cnt : n;
     if (start < 0) n = 0;
-    if (t0 >= n) return;
+    if (t0 >= n) return false;
     const int64_t rem = n - t0;
     const int32_t rws = rem < bs ? (int32_t)rem : bs;
     if (threadIdx.x < kWave) {
@@ -2010,25 +2022,26 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     bid = s_ids[0];
     mixed = !s_same;
     if (!mixed) {
-      if (bid < 0) return;  // every row skipped
+      if (bid < 0) return true;  // every row skipped
       blk = tt.src + bid * tt.s_block;
     }
   } else {
-    if (lb >= a.max_blocks_per_seq) return;
+    if (lb >= a.max_blocks_per_seq) return false;
     if constexpr (FMT == KVX_BLOCK_TABLE_KV_OFFSETS) {
       // table [seq, beam = 1, {K, V}, max_blocks_per_seq] of KVCacheIndex
       const uint32_t ent = reinterpret_cast<const uint32_t *>(
           a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
       const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
       bid = ent & 0x7FFFFFFFu;
-      if (pool == nullptr || bid >= a.num_blocks) return;
+      if (t0 >= n) return false;
+      if (pool == nullptr || bid >= a.num_blocks) return true;
       blk = pool + bid * a.bytes_per_block;
     } else {
       bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
-      if (bid < 0 || bid >= a.num_blocks) return;
+      if (t0 >= n) return false;
+      if (bid < 0 || bid >= a.num_blocks) return true;
       blk = tt.src + bid * tt.s_block;
     }
-    if (t0 >= n) return;
   }
   const int64_t rem = n - t0;
   const int32_t rows = rem < bs ? (int32_t)rem : bs;
@@ -2061,7 +2074,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
       st<Op::kDst, kGatherNtStore>(out + ((int64_t)e << a.io_es_log2),
                                    Op::apply(ld<Op::kSrc, kGatherNtLoad>(b + m), sc));
     }
-    return;
+    return true;
   }
 
   if (mixed) {
@@ -2093,6 +2106,32 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     unstage_gather_tile<Op, FMT, true>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
   else
     unstage_gather_tile<Op, FMT, false>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
+  return true;
+}
+
+// I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
+// indptr dtype.  Workgroup w of sequence s takes units w + i * J (J =
+// wg_per_seq, i < 1 << fold_log2) below units_per_seq; unit u is tile
+// u % tiles of logical block u / tiles.
+template <class Op, int FMT, bool I64, bool P64>
+__global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
+  __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
+  const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
+  const uint32_t wg = blockIdx.x;
+  const uint32_t per_seq = (uint32_t)a.wg_per_seq;
+  const uint32_t su = wg / per_seq;
+  const uint32_t w = wg - su * per_seq;
+  for (int i = 0; i < (1 << a.fold_log2); ++i) {
+    const uint32_t u = w + (uint32_t)i * per_seq;
+    if (u >= (uint32_t)a.units_per_seq) return;
+    if (i > 0) __syncthreads();  // the last unit's reads of lds and s_ids are done
+    const uint32_t lbu = u / (uint32_t)a.tiles;
+    if (!gather_tile_unit<Op, FMT, I64, P64>(a, tt, lds, s_ids, s_same, su, (int32_t)lbu,
+                                             (int32_t)(u - lbu * (uint32_t)a.tiles)))
+      return;
+  }
 }
 
 // Rows of sequence s that exist (t < n) for an indexed-format workgroup,

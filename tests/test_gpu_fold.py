@@ -1,8 +1,10 @@
-"""GPU parity of the row-major gathers when a workgroup takes two units of
-its sequence: gather_flat_kernel (PACKED) with sequences of 4096 to 16384
-units, a unit being one power-of-two share of a block, and the RAGGED tile
-and flat indexed gathers (RAGGED, KV_OFFSETS) with 4096 to 16384 row tiles:
-unit w and unit w + J of sequence s, J the workgroups per sequence.
+"""GPU parity of the gathers when a workgroup takes two units of its
+sequence: gather_flat_kernel (PACKED) with sequences of 4096 to 16384 units,
+a unit being one power-of-two share of a block; the RAGGED tile and flat
+indexed gathers (RAGGED, KV_OFFSETS) with 512 (RAGGED) or 2048 (KV_OFFSETS)
+to 65536 row tiles; the transposing gather (gather_tiles_kernel) with 512 to
+65536 (block, tile) units: unit w and unit w + J of sequence s, J the
+workgroups per sequence.
 Bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:226-267 gather
 semantics; KVX_SPEC.md:99-122 for the indexed tables).
 
@@ -160,3 +162,76 @@ def test_two_tiles_per_workgroup_indexed(case):
     lens[3] = L // 3
     check_gather_ragged(pc, kb, vb, ko, vo, rt, lens, L, cache_dtype=cdt, io_dtype=iodt,
                         k_scale=ks, v_scale=vs)
+
+
+# The transposing gather (gather_tiles_kernel) takes two (block, tile) units
+# per workgroup from 512 to 65536 units per sequence.
+# (K order, K x, V order, V x, table, cache dtype, H, D, blocks per sequence)
+TILED = [
+    ("bhod", None, "bhod", None, "packed", DType.BF16, 8, 128, 130),    # HND, 4 tiles a block
+    ("bhpox", 8, "bhdo", None, "packed", DType.BF16, 8, 128, 130),      # vLLM's pair
+    ("bhod", None, "bohd", None, "packed", DType.F16, 4, 64, 520),       # HND K, row-major V
+    ("bhod", None, "bhod", None, "ragged", DType.BF16, 8, 128, 130),    # RAGGED, mixed ids
+    ("bhod", None, "bhod", None, "offsets", DType.BF16, 8, 128, 130),   # KV_OFFSETS
+    ("bhod", None, "bhod", None, "packed", DType.F8_E4M3, 8, 128, 260),  # dequantizing
+    ("bhod", None, "bhod", None, "packed", DType.BF16, 3, 128, 520),    # 768-byte rows
+]
+
+
+def _tiled_ids(c):
+    return f"{c[0]}{c[1] or ''}-{c[2]}{c[3] or ''}-{c[4]}-{c[5].name}-H{c[6]}-D{c[7]}-{c[8]}blocks"
+
+
+@pytest.mark.parametrize("case", TILED, ids=[_tiled_ids(c) for c in TILED])
+def test_two_tiles_per_workgroup_transposing(case):
+    import numpy as np
+
+    from kvx_amd import paged
+
+    from gpu_helpers import (OffsetsPool, check_gather_offsets, check_gather_ragged,
+                             custom_cache)
+
+    ko_, kx, vo_, vx, fmt, cdt, H, D, blocks = case
+    idx = TILED.index(case)
+    rng = np.random.default_rng(1400 + idx)
+    gen = torch.Generator().manual_seed(1400 + idx)
+    bs, nb, S = 16, 40, 7
+    L = blocks * bs - 5  # a partial last block
+    iodt = DType.BF16 if cdt == DType.F8_E4M3 else cdt
+    ks, vs = (0.0213, 0.0047) if cdt != iodt else (None, None)
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    half = (blocks // 2) * bs  # about where the second units begin
+    lens = [L, half + 2 * bs + 3, half, half - 9, 0, L + 100, half + bs + 1]
+    if fmt == "offsets":
+        pool = OffsetsPool(Layout.BLOCK_HND, Layout.BLOCK_HND, cdt, nb, bs, H, D,
+                           pitch_pad=64, gen=gen)
+        raw = rng.integers(0, nb, size=(S, 1, 2, blocks)).astype(np.uint32)
+        raw |= (rng.random(raw.shape) < 0.3).astype(np.uint32) << 31
+        raw[0, 0, 0, 4] = nb + 3
+        raw[0, 0, 1, blocks // 2 + 1] = 0x7FFFFFFF
+        offsets = torch.from_numpy(raw.view(np.int32)).to(DEV)
+        check_gather_offsets(pool, ko, vo, offsets,
+                             torch.tensor(lens, dtype=torch.int32, device=DEV), L,
+                             cache_dtype=cdt, io_dtype=iodt, k_scale=ks, v_scale=vs)
+        return
+    pc, kb, vb = custom_cache(cdt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    if fmt == "ragged":
+        counts = np.array(lens)
+        counts[5] = L + 3
+        indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        parts = [rng.integers(0, nb, size=blocks + 1)[np.arange(c) // bs] for c in counts]
+        indices = np.concatenate(parts).astype(np.int32)
+        bad = rng.choice(indices.size, size=48, replace=False)
+        indices[bad] = rng.choice([-1, nb, 5], size=48)
+        rt = paged.RaggedTable(torch.from_numpy(indices).to(DEV),
+                               torch.from_numpy(indptr).to(DEV))
+        check_gather_ragged(pc, kb, vb, ko, vo, rt, torch.full((S,), L, dtype=torch.int32,
+                                                               device=DEV), L,
+                            cache_dtype=cdt, io_dtype=iodt, k_scale=ks, v_scale=vs)
+        return
+    table = torch.randint(0, nb, (S, blocks), generator=gen).to(torch.int32)
+    table[0, 2], table[0, blocks // 2 + 1], table[1, blocks // 2 + 2] = -1, nb + 4, nb
+    check_gather(pc, kb, vb, ko, vo, table.to(DEV),
+                 torch.tensor(lens, dtype=torch.int32, device=DEV), L, cache_dtype=cdt,
+                 io_dtype=iodt, k_scale=ks, v_scale=vs)
