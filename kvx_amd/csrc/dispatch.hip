@@ -304,16 +304,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     t->t[i].run_magic = run_log2[i] == kRunOdd ? magic_for(run_bytes[i]) : 0;
     t->t[i].pad_ = 0;
   }
-  // up to 1 << fold_log2 (block, tile) units per workgroup, strided by the
-  // workgroups per sequence
-  const int64_t units = (int64_t)t->blocks_per_seq * t->tiles;
-  if (units > 0x7FFFFFFF) return false;
-  t->units_per_seq = (int32_t)units;
-  t->fold_log2 = 0;
-  if (KVX_TILES_FOLD && units >= KVX_TILES_FOLD_MIN_UNITS && units <= KVX_TILES_FOLD_MAX_UNITS)
-    t->fold_log2 = KVX_FLAT_FOLD_LOG2;
-  t->wg_per_seq = (int32_t)((units + (1 << t->fold_log2) - 1) >> t->fold_log2);
-  *grid = (int64_t)p.seq_count * t->wg_per_seq;
+  *grid = (int64_t)p.seq_count * t->blocks_per_seq * t->tiles;
   *lds_bytes = (uint32_t)(bs * pitch);
   return grid_fits(*grid, t->threads);
 }
@@ -646,16 +637,6 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     if (!a.ragged_tile) {
       a.rows_per_wg = (int32_t)rows;
       a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + rows - 1) / rows);
-    }
-    // the RAGGED tile and flat indexed gathers: up to 1 << fold_log2 tiles
-    // per workgroup, strided as in the PACKED row-major gather
-    a.units_per_seq = a.blocks_per_seq;
-    const int64_t fold_min = p.format == KVX_BLOCK_TABLE_RAGGED ? KVX_RAGGED_FOLD_MIN_UNITS
-                                                                : KVX_OFFSETS_FOLD_MIN_UNITS;
-    if (KVX_INDEXED_FOLD && (a.ragged_tile || a.flat) && a.blocks_per_seq >= fold_min &&
-        a.blocks_per_seq <= KVX_INDEXED_FOLD_MAX_UNITS) {
-      a.fold_log2 = KVX_FLAT_FOLD_LOG2;
-      a.blocks_per_seq = (a.blocks_per_seq + (1 << a.fold_log2) - 1) >> a.fold_log2;
     }
   } else if (a.flat) {
     // split a block's chunks into a power-of-two number of equal ranges of

@@ -1541,15 +1541,16 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 // The grid covers max_seq_len, so a decode batch's shorter sequences leave
 // workgroups that only load seq_len and exit; on MI355X such workgroups cost
 // wave launches (c2 with max_seq_len doubled at the same lengths: 1573 ->
-// 1699 us per layer).  Two units per workgroup, the second half a sequence
-// further on, measured on three boxes (same-box A/B medians, us per layer):
-// c2 1612.6 -> 1553.9 and 1609.4 -> 1547.7 (8192 units per sequence), c2
-// with every sequence at 8192 tokens 2954.6 -> 2915.2, c4 and c2 with four
-// heads (4096 units) 0.5-0.8% faster; 2048 units or fewer (one or two KV
-// heads) 0-2.8% slower, where the last sequences' two-unit workgroups
-// lengthen a short launch; c5 (32768 units) -3.9%, -1.2% and +1.7%.  Four
-// units were slower at every shape, and ordering the grid unit-major (all
-// sequences' first units first) 15-30% slower.
+// 1699 us per layer).  Against the one-unit kernel (same-box A/B medians,
+// us per layer) two units measured c2 1540.3 -> 1531.8 (32 layers, 8192
+// units per sequence) and c4 633.4 -> 629.6 (4096 units).  Within this
+// kernel, two units against one: 2048 units or fewer (one or two KV heads)
+// 0-2.8% slower, where the last sequences' two-unit workgroups lengthen a
+// short launch; c5 (32768 units) -3.9% to +1.7% over three boxes; four units
+// slower at every shape; ordering the grid unit-major (all sequences' first
+// units first) 15-30% slower.  (Two tiles per workgroup in the RAGGED tile,
+// flat indexed and transposing gathers measured 1-10% slower than one, bar
+// c2's and c5's RAGGED gathers, 1-2% faster.)
 #ifndef KVX_FLAT_FOLD_LOG2
 #define KVX_FLAT_FOLD_LOG2 1
 #endif
@@ -1560,46 +1561,6 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #define KVX_FLAT_FOLD_MAX_UNITS 16384
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
-// The same for the RAGGED tile and flat indexed gathers' row tiles (1), or
-// one tile per workgroup (0), for sequences of KVX_RAGGED_FOLD_MIN_UNITS
-// (RAGGED) or KVX_OFFSETS_FOLD_MIN_UNITS (KV_OFFSETS) to
-// KVX_INDEXED_FOLD_MAX_UNITS tiles.  These workgroups load seq_len and the
-// indptr pair or table entries before any data, so two tiles gain more:
-// on MI355X (same-box A/B medians, us per layer) c2's RAGGED gather 1787
-// -> 1638, c4's 811 -> 744, c5's (32768 tiles) 2198 -> 2073, RAGGED with
-// one or two KV heads (512-2048 tiles) 4-7% faster; c2's KV_OFFSETS gather
-// 1874 -> 1805, c4's (2048 tiles) 662 -> 645, but KV_OFFSETS copies with
-// per-tile entries at 512 and 1024 tiles (one and two bf16 heads) 2-3%
-// slower.
-#ifndef KVX_INDEXED_FOLD
-#define KVX_INDEXED_FOLD 1
-#endif
-// The same for the transposing gather's (block, tile) units
-// (gather_tiles_kernel), from KVX_TILES_FOLD_MIN_UNITS to
-// KVX_TILES_FOLD_MAX_UNITS units per sequence.  On MI355X (same-box A/B
-// medians, us per layer, c2's table in 8 KiB tiles) HND 1853 -> 1704,
-// x-packed 1862 -> 1715, vLLM's pair 1901 -> 1728 (one KV head 241 ->
-// 218), HND RAGGED 2015 -> 1769, c5 in HND blocks 2266 -> 2193; 128-token
-// HND blocks (16 KiB tiles, 1024 units) 1692 -> 1708.  A second unit
-// waits at a barrier for the first's LDS reads.
-#ifndef KVX_TILES_FOLD
-#define KVX_TILES_FOLD 1
-#endif
-#ifndef KVX_TILES_FOLD_MIN_UNITS
-#define KVX_TILES_FOLD_MIN_UNITS 512
-#endif
-#ifndef KVX_TILES_FOLD_MAX_UNITS
-#define KVX_TILES_FOLD_MAX_UNITS 65536
-#endif
-#ifndef KVX_RAGGED_FOLD_MIN_UNITS
-#define KVX_RAGGED_FOLD_MIN_UNITS 512
-#endif
-#ifndef KVX_OFFSETS_FOLD_MIN_UNITS
-#define KVX_OFFSETS_FOLD_MIN_UNITS 2048
-#endif
-#ifndef KVX_INDEXED_FOLD_MAX_UNITS
-#define KVX_INDEXED_FOLD_MAX_UNITS 65536
-#endif
 
 // A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J
 // (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
@@ -1790,9 +1751,6 @@ struct TileArgs {
   int32_t bs_log2;
   int32_t cache_es_log2;  // log2 cache element bytes
   int32_t io_es_log2;     // log2 output element bytes
-  int32_t units_per_seq;  // (block, tile) units per sequence: blocks_per_seq * tiles
-  int32_t wg_per_seq;     // workgroups per sequence
-  int32_t fold_log2;      // up to 1 << fold_log2 units per workgroup
 };
 
 // Store piece k (PIECE bytes) of a 16-byte chunk at p.
@@ -1977,14 +1935,22 @@ __device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const Til
   }
 }
 
-// One tile (tile `tile` of logical block lb of sequence s, the tensor of
-// blockIdx.y) of gather_tiles_kernel; false when the block lies past the
-// sequence's end (or its table row), and so does every later one.  s_ids
-// and s_same are the workgroup's shared RAGGED row ids.
+// I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
+// indptr dtype.
 template <class Op, int FMT, bool I64, bool P64>
-__device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTensor &tt,
-                                                 char *lds, int64_t *s_ids, int32_t &s_same,
-                                                 int64_t s, int32_t lb, int32_t tile) {
+__global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
+  __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
+  const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
+  const uint32_t wg = blockIdx.x;
+  const uint32_t per_seq = (uint32_t)a.blocks_per_seq * (uint32_t)a.tiles;
+  const uint32_t su = wg / per_seq;
+  const uint32_t w = wg - su * per_seq;
+  const uint32_t lbu = w / (uint32_t)a.tiles;
+  const int32_t tile = (int32_t)(w - lbu * (uint32_t)a.tiles);
+  const int32_t lb = (int32_t)lbu;
+  const int64_t s = su;
   const int64_t t0 = (int64_t)lb << a.bs_log2;
   const int32_t bs = 1 << a.bs_log2;
   const int64_t seq_len = load_idx<I64>(a.seq_lens, s);
@@ -2001,7 +1967,7 @@ __device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTe
     cnt = left < cnt ? left : cnt;
     n = cnt < n ? cnt : n;
     if (start < 0) n = 0;
-    if (t0 >= n) return false;
+    if (t0 >= n) return;
     const int64_t rem = n - t0;
     const int32_t rws = rem < bs ? (int32_t)rem : bs;
     if (threadIdx.x < kWave) {
@@ -2022,26 +1988,25 @@ __device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTe
     bid = s_ids[0];
     mixed = !s_same;
     if (!mixed) {
-      if (bid < 0) return true;  // every row skipped
+      if (bid < 0) return;  // every row skipped
       blk = tt.src + bid * tt.s_block;
     }
   } else {
-    if (lb >= a.max_blocks_per_seq) return false;
+    if (lb >= a.max_blocks_per_seq) return;
     if constexpr (FMT == KVX_BLOCK_TABLE_KV_OFFSETS) {
       // table [seq, beam = 1, {K, V}, max_blocks_per_seq] of KVCacheIndex
       const uint32_t ent = reinterpret_cast<const uint32_t *>(
           a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
       const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
       bid = ent & 0x7FFFFFFFu;
-      if (t0 >= n) return false;
-      if (pool == nullptr || bid >= a.num_blocks) return true;
+      if (pool == nullptr || bid >= a.num_blocks) return;
       blk = pool + bid * a.bytes_per_block;
     } else {
       bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
-      if (t0 >= n) return false;
-      if (bid < 0 || bid >= a.num_blocks) return true;
+      if (bid < 0 || bid >= a.num_blocks) return;
       blk = tt.src + bid * tt.s_block;
     }
+    if (t0 >= n) return;
   }
   const int64_t rem = n - t0;
   const int32_t rows = rem < bs ? (int32_t)rem : bs;
@@ -2074,7 +2039,7 @@ __device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTe
       st<Op::kDst, kGatherNtStore>(out + ((int64_t)e << a.io_es_log2),
                                    Op::apply(ld<Op::kSrc, kGatherNtLoad>(b + m), sc));
     }
-    return true;
+    return;
   }
 
   if (mixed) {
@@ -2106,32 +2071,6 @@ __device__ __forceinline__ bool gather_tile_unit(const TileArgs &a, const TileTe
     unstage_gather_tile<Op, FMT, true>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
   else
     unstage_gather_tile<Op, FMT, false>(a, tt, lds, out, rows, tile, bid, mixed, s_ids, uniform);
-  return true;
-}
-
-// I64: dtype of seq_lens and of PACKED / RAGGED block ids; P64: RAGGED's
-// indptr dtype.  Workgroup w of sequence s takes units w + i * J (J =
-// wg_per_seq, i < 1 << fold_log2) below units_per_seq; unit u is tile
-// u % tiles of logical block u / tiles.
-template <class Op, int FMT, bool I64, bool P64>
-__global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char lds[];
-  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
-  __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
-  const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
-  const uint32_t wg = blockIdx.x;
-  const uint32_t per_seq = (uint32_t)a.wg_per_seq;
-  const uint32_t su = wg / per_seq;
-  const uint32_t w = wg - su * per_seq;
-  for (int i = 0; i < (1 << a.fold_log2); ++i) {
-    const uint32_t u = w + (uint32_t)i * per_seq;
-    if (u >= (uint32_t)a.units_per_seq) return;
-    if (i > 0) __syncthreads();  // the last unit's reads of lds and s_ids are done
-    const uint32_t lbu = u / (uint32_t)a.tiles;
-    if (!gather_tile_unit<Op, FMT, I64, P64>(a, tt, lds, s_ids, s_same, su, (int32_t)lbu,
-                                             (int32_t)(u - lbu * (uint32_t)a.tiles)))
-      return;
-  }
 }
 
 // Rows of sequence s that exist (t < n) for an indexed-format workgroup,
@@ -2344,12 +2283,18 @@ inline int offsets_tile_threads(const GatherArgs &a) {
   return t;
 }
 
-// One tile (rows t0 .. t0 + rows_per_wg - 1 of sequence s) of
-// gather_indexed_flat_kernel, nt threads; false when the tile lies past the
-// sequence's end (or its table row), and so does every later one.
-template <class Op, int FMT, bool I64, bool P64, bool kTile>
-__device__ __forceinline__ bool indexed_flat_unit(const GatherArgs &a, int64_t s, int64_t t0,
-                                                  uint32_t nt) {
+// TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
+// threads as the launch gives (at most kBlockThreads).
+template <class Op, int FMT, bool I64, bool P64,
+          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
+__global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
+    GatherArgs a) {
+  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
+  const uint32_t nt = kTile ? blockDim.x : (uint32_t)indexed_flat_threads<Op, FMT>();
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
   // KV_OFFSETS tiles lie inside one block (rows_per_wg divides block_size).
   // kTile: the tile's K and V table entries are two scalar loads, issued with
   // the seq_len load; otherwise every chunk loads its own entry.
@@ -2358,11 +2303,11 @@ __device__ __forceinline__ bool indexed_flat_unit(const GatherArgs &a, int64_t s
   uint32_t lb = 0;
   if constexpr (kTile) {
     lb = (uint32_t)t0 >> a.bs_log2;
-    if (lb >= (uint32_t)a.max_blocks_per_seq) return false;
+    if (lb >= (uint32_t)a.max_blocks_per_seq) return;
   }
   int64_t n;
   int64_t start;
-  if (!indexed_extent<FMT, I64, P64, kTile>(a, s, t0, n, start, lb, &ek, &ev)) return false;
+  if (!indexed_extent<FMT, I64, P64, kTile>(a, s, t0, n, start, lb, &ek, &ev)) return;
   const char *tk = nullptr;
   const char *tv = nullptr;
   if constexpr (kTile) {
@@ -2373,7 +2318,7 @@ __device__ __forceinline__ bool indexed_flat_unit(const GatherArgs &a, int64_t s
     const int64_t vb = ev & 0x7FFFFFFFu;
     if (pk != nullptr && kb < a.num_blocks) tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
     if (pv != nullptr && vb < a.num_blocks) tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
-    if (tk == nullptr && tv == nullptr) return true;
+    if (tk == nullptr && tv == nullptr) return;
   }
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;
@@ -2437,28 +2382,6 @@ __device__ __forceinline__ bool indexed_flat_unit(const GatherArgs &a, int64_t s
         st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
   }
-  return true;
-}
-
-// TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
-// threads as the launch gives (at most kBlockThreads).  Workgroup w of
-// sequence s takes tiles w + i * J (J = blocks_per_seq, i < 1 << fold_log2)
-// below units_per_seq.
-template <class Op, int FMT, bool I64, bool P64,
-          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
-__global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
-    GatherArgs a) {
-  constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
-  const uint32_t nt = kTile ? blockDim.x : (uint32_t)indexed_flat_threads<Op, FMT>();
-  const uint32_t wg = blockIdx.x;
-  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
-  const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
-  for (int i = 0; i < (1 << a.fold_log2); ++i) {
-    const int32_t u = w + i * a.blocks_per_seq;
-    if (u >= a.units_per_seq ||
-        !indexed_flat_unit<Op, FMT, I64, P64, kTile>(a, su, (int64_t)u * a.rows_per_wg, nt))
-      return;
-  }
 }
 
 // RAGGED gather of caches whose block rows are contiguous (canonical NHD
@@ -2474,15 +2397,16 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
 // every chunk takes its row's id from the lane that loaded it, and rows
 // whose id is < 0 or >= num_blocks are skipped.  No chunk loads an index of
 // its own.
-// One tile (rows t0 .. t0 + rows_per_wg - 1 of sequence s) of
-// gather_ragged_tile_kernel; false when the tile lies past the sequence's
-// end, and so does every later one.
 template <class Op, bool I64, bool P64>
-__device__ __forceinline__ bool ragged_tile_unit(const GatherArgs &a, int64_t s, int64_t t0) {
+__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
   constexpr int U = Op::kScaled ? kFlatUnrollDequant : kFlatUnroll;
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t s = su;
+  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
   int64_t n;
   int64_t start;
-  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return false;
+  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return;
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;  // <= 64
   const int lane = (int)(threadIdx.x & (kWave - 1));
@@ -2507,7 +2431,7 @@ __device__ __forceinline__ bool ragged_tile_unit(const GatherArgs &a, int64_t s,
     flat_copy<Op>(a, a.src_k + first * a.gk.s_block + o0 * a.gk.s_off,
                   a.src_v + first * a.gv.s_block + o0 * a.gv.s_off, a.dst_k + out0,
                   a.dst_v + out0, total, ks, vs, first, 0);
-    return true;
+    return;
   }
   // Rows in several blocks (or skipped): chunk f is K for f < total, V
   // above; row r = index / nchunks takes its id from lane r.  The
@@ -2547,22 +2471,6 @@ __device__ __forceinline__ bool ragged_tile_unit(const GatherArgs &a, int64_t s,
     for (int u = 0; u < U; ++u) {
       if (src[u] != nullptr) st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
-  }
-  return true;
-}
-
-// Workgroup w of sequence s takes tiles w + i * J (J = blocks_per_seq,
-// i < 1 << fold_log2) below units_per_seq.
-template <class Op, bool I64, bool P64>
-__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
-  const uint32_t wg = blockIdx.x;
-  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
-  const int32_t w = (int32_t)(wg - su * (uint32_t)a.blocks_per_seq);
-  for (int i = 0; i < (1 << a.fold_log2); ++i) {
-    const int32_t u = w + i * a.blocks_per_seq;
-    if (u >= a.units_per_seq ||
-        !ragged_tile_unit<Op, I64, P64>(a, su, (int64_t)u * a.rows_per_wg))
-      return;
   }
 }
 

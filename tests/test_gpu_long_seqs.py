@@ -1,18 +1,18 @@
-"""GPU parity of the gathers when a workgroup takes two units of its
-sequence: gather_flat_kernel (PACKED) with sequences of 4096 to 16384 units,
-a unit being one power-of-two share of a block; the RAGGED tile and flat
-indexed gathers (RAGGED, KV_OFFSETS) with 512 (RAGGED) or 2048 (KV_OFFSETS)
-to 65536 row tiles; the transposing gather (gather_tiles_kernel) with 512 to
-65536 (block, tile) units: unit w and unit w + J of sequence s, J the
-workgroups per sequence.
-Bit-identical to the CPU oracle (kernels/kvx_paged_kv.cu:226-267 gather
+"""GPU parity of the gathers over long sequences of many workgroups, bit-
+identical to the CPU oracle (kernels/kvx_paged_kv.cu:226-267 gather
 semantics; KVX_SPEC.md:99-122 for the indexed tables).
+
+gather_flat_kernel (PACKED) takes two units of its sequence per workgroup
+when a sequence has 4096 to 16384 units, a unit being one power-of-two
+share of a block: unit w and unit w + J of sequence s, J the workgroups per
+sequence.  The RAGGED tile, flat indexed and transposing gathers keep one
+tile per workgroup; their cases here cover 513 to 40001 tiles per sequence.
 
 Lengths cover both units of a workgroup valid, the second one cut inside
 its block or part, the second one starting exactly at seq_len (the
 boundary J * block_size / parts), the first one cut, an empty sequence, a
 length past max_seq_len, tables narrower than max_seq_len, and block ids
-< 0 or >= num_blocks in either unit.
+< 0 or >= num_blocks in either half of a sequence.
 """
 import pytest
 import torch
@@ -83,8 +83,7 @@ def test_two_units_per_workgroup(case, idx64):
                  cache_dtype=cdt, io_dtype=iodt, k_scale=ks, v_scale=vs)
 
 
-# RAGGED and KV_OFFSETS gathers take two row tiles per workgroup the same
-# way when a sequence has 512 (RAGGED) or 2048 (KV_OFFSETS) to 65536 tiles.
+# RAGGED and KV_OFFSETS gathers over sequences of many row tiles.
 # (path, cache dtype, io dtype, H, D, rows per tile, tiles per sequence)
 INDEXED = [
     ("ragged_tile", DType.BF16, DType.BF16, 8, 128, 1, 8197),     # one 2 KiB row per tile
@@ -101,7 +100,7 @@ INDEXED = [
 
 
 def _lens(L, r):
-    half = (L // r + 1) // 2 * r  # first row of the second tile of workgroup 0
+    half = (L // r + 1) // 2 * r  # the first row of the middle tile
     return [L, half + 3 * r + 1, half, half - 1, 0, L + 100, half + r // 2 + 1]
 
 
@@ -110,7 +109,7 @@ def _indexed_ids(c):
 
 
 @pytest.mark.parametrize("case", INDEXED, ids=[_indexed_ids(c) for c in INDEXED])
-def test_two_tiles_per_workgroup_indexed(case):
+def test_indexed_gather_many_tiles(case):
     import numpy as np
 
     from kvx_amd import paged
@@ -123,7 +122,7 @@ def test_two_tiles_per_workgroup_indexed(case):
     gen = torch.Generator().manual_seed(1300 + idx)
     bs, nb = 16, 48
     L = tiles * r - (r // 2)  # a partial last tile
-    assert (512 if path != "offsets" else 2048) <= (L + r - 1) // r <= 65536
+    assert 512 <= (L + r - 1) // r <= 65536
     S = 7
     ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
     vo = random_fill(torch.empty_like(ko), gen)
@@ -164,8 +163,8 @@ def test_two_tiles_per_workgroup_indexed(case):
                         k_scale=ks, v_scale=vs)
 
 
-# The transposing gather (gather_tiles_kernel) takes two (block, tile) units
-# per workgroup from 512 to 65536 units per sequence.
+# The transposing gather (gather_tiles_kernel) over sequences of 520 to 1560
+# (block, tile) units.
 # (K order, K x, V order, V x, table, cache dtype, H, D, blocks per sequence)
 TILED = [
     ("bhod", None, "bhod", None, "packed", DType.BF16, 8, 128, 130),    # HND, 4 tiles a block
@@ -183,7 +182,7 @@ def _tiled_ids(c):
 
 
 @pytest.mark.parametrize("case", TILED, ids=[_tiled_ids(c) for c in TILED])
-def test_two_tiles_per_workgroup_transposing(case):
+def test_transposing_gather_many_units(case):
     import numpy as np
 
     from kvx_amd import paged
@@ -201,7 +200,7 @@ def test_two_tiles_per_workgroup_transposing(case):
     ks, vs = (0.0213, 0.0047) if cdt != iodt else (None, None)
     ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[iodt], device=DEV), gen)
     vo = random_fill(torch.empty_like(ko), gen)
-    half = (blocks // 2) * bs  # about where the second units begin
+    half = (blocks // 2) * bs  # the middle block
     lens = [L, half + 2 * bs + 3, half, half - 9, 0, L + 100, half + bs + 1]
     if fmt == "offsets":
         pool = OffsetsPool(Layout.BLOCK_HND, Layout.BLOCK_HND, cdt, nb, bs, H, D,

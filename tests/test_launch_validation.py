@@ -449,7 +449,6 @@ def test_gather_grid_past_hip_limits(kvx_lib):
     # split, 4096 blocks per sequence taken two per workgroup: 16384 x 2048
     # workgroups = 2^32 work-items
     assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 16384, 65536, 1, 8, 16)) == UNS
-    # gather_ragged_tile_kernel, 128 threads, 16 rows per tile, two tiles per
-    # workgroup: 16384 x 2048 workgroups
-    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 16384, 65536, 1, 8, 16,
+    # gather_ragged_tile_kernel, 128 threads, 16 rows per workgroup
+    assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16,
                                   fmt="ragged")) == UNS
