@@ -621,6 +621,15 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
       a.ragged_tile = 1;
       a.rows_per_wg = (int32_t)r;
       a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + r - 1) / r);
+      // copies of sequences of KVX_RAGGED_FOLD_MIN_UNITS to _MAX_UNITS tiles:
+      // two tiles per workgroup, tile w and w + J (J workgroups per sequence)
+      a.units_per_seq = a.blocks_per_seq;
+      if (p.conv == kConvCopy && KVX_RAGGED_FOLD_MIN_UNITS > 0 &&
+          a.blocks_per_seq >= KVX_RAGGED_FOLD_MIN_UNITS &&
+          a.blocks_per_seq <= KVX_RAGGED_FOLD_MAX_UNITS) {
+        a.fold_log2 = 1;  // the kernel is built for one or two tiles
+        a.blocks_per_seq = (a.blocks_per_seq + 1) >> 1;
+      }
     }
     const bool ragged_copy = a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy;
     int64_t rows = (ragged_copy ? KVX_RAGGED_COPY_TILE_BYTES : KVX_GATHER_TILE_BYTES) /

@@ -1548,9 +1548,9 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 // 0-2.8% slower, where the last sequences' two-unit workgroups lengthen a
 // short launch; c5 (32768 units) -3.9% to +1.7% over three boxes; four units
 // slower at every shape; ordering the grid unit-major (all sequences' first
-// units first) 15-30% slower.  (Two tiles per workgroup in the RAGGED tile,
-// flat indexed and transposing gathers measured 1-10% slower than one, bar
-// c2's and c5's RAGGED gathers, 1-2% faster.)
+// units first) 15-30% slower.  (Two tiles per workgroup in the flat indexed
+// and transposing gathers measured 1-10% slower than one; the RAGGED tile
+// gather takes two for long copies, below.)
 #ifndef KVX_FLAT_FOLD_LOG2
 #define KVX_FLAT_FOLD_LOG2 1
 #endif
@@ -1561,6 +1561,18 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #define KVX_FLAT_FOLD_MAX_UNITS 16384
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
+// RAGGED copies in gather_ragged_tile_kernel: two tiles per workgroup when a
+// sequence has KVX_RAGGED_FOLD_MIN_UNITS to KVX_RAGGED_FOLD_MAX_UNITS tiles
+// (0 disables).  Against one tile per workgroup (same-box A/B, medians of 6
+// rounds, us per layer): c2's RAGGED gather 1563.7 -> 1528.0 (8 layers) and
+// 1468.8 -> 1448.9 (32 layers), c5's 2163.4 -> 2150.3; c4's FP8 RAGGED
+// gather (4096 tiles) measured 6.7% slower with two tiles and keeps one.
+#ifndef KVX_RAGGED_FOLD_MIN_UNITS
+#define KVX_RAGGED_FOLD_MIN_UNITS 8192
+#endif
+#ifndef KVX_RAGGED_FOLD_MAX_UNITS
+#define KVX_RAGGED_FOLD_MAX_UNITS 65536
+#endif
 
 // A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J
 // (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
@@ -1577,8 +1589,8 @@ __global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a)
   int64_t bid[kFlatFold];
 #pragma unroll
   for (int i = 0; i < kFlatFold; ++i) {
-    const int32_t u = w + i * a.blocks_per_seq;
-    const int32_t lb = u >> a.split_log2;
+    const int64_t u = (int64_t)w + (int64_t)i * a.blocks_per_seq;
+    const int64_t lb = u >> a.split_log2;
     bid[i] = -1;
     if (i < (1 << a.fold_log2) && u < a.units_per_seq && lb < a.max_blocks_per_seq)
       bid[i] = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
@@ -1593,10 +1605,10 @@ __global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a)
   const int64_t per_part = ((int64_t)a.block_size * a.nchunks) >> a.split_log2;
 #pragma unroll
   for (int i = 0; i < kFlatFold; ++i) {
-    const int32_t u = w + i * a.blocks_per_seq;
-    const int32_t lb = u >> a.split_log2;
-    const int32_t part = u & ((1 << a.split_log2) - 1);
-    const int64_t t0 = (int64_t)lb * a.block_size;
+    const int64_t u = (int64_t)w + (int64_t)i * a.blocks_per_seq;
+    const int64_t lb = u >> a.split_log2;
+    const int32_t part = (int32_t)(u & ((1 << a.split_log2) - 1));
+    const int64_t t0 = lb * a.block_size;
     if (t0 >= n) break;  // later units lie further along the sequence
     if (bid[i] < 0 || bid[i] >= a.num_blocks) continue;
     // The block's valid rows are `valid` consecutive chunks of K (and of V);
@@ -2397,16 +2409,15 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
 // every chunk takes its row's id from the lane that loaded it, and rows
 // whose id is < 0 or >= num_blocks are skipped.  No chunk loads an index of
 // its own.
+// One tile (rows t0 .. t0 + rows_per_wg - 1 of sequence s) of
+// gather_ragged_tile_kernel; false when the tile lies past the sequence's
+// end, and so does every later one.
 template <class Op, bool I64, bool P64>
-__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
+__device__ __forceinline__ bool ragged_tile_unit(const GatherArgs &a, int64_t s, int64_t t0) {
   constexpr int U = Op::kScaled ? kFlatUnrollDequant : kFlatUnroll;
-  const uint32_t wg = blockIdx.x;
-  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
-  const int64_t s = su;
-  const int64_t t0 = (int64_t)(wg - su * (uint32_t)a.blocks_per_seq) * a.rows_per_wg;
   int64_t n;
   int64_t start;
-  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return;
+  if (!indexed_extent<KVX_BLOCK_TABLE_RAGGED, I64, P64>(a, s, t0, n, start)) return false;
   const int64_t rem = n - t0;
   const int32_t rows = rem < a.rows_per_wg ? (int32_t)rem : a.rows_per_wg;  // <= 64
   const int lane = (int)(threadIdx.x & (kWave - 1));
@@ -2431,7 +2442,7 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     flat_copy<Op>(a, a.src_k + first * a.gk.s_block + o0 * a.gk.s_off,
                   a.src_v + first * a.gv.s_block + o0 * a.gv.s_off, a.dst_k + out0,
                   a.dst_v + out0, total, ks, vs, first, 0);
-    return;
+    return true;
   }
   // Rows in several blocks (or skipped): chunk f is K for f < total, V
   // above; row r = index / nchunks takes its id from lane r.  The
@@ -2471,6 +2482,23 @@ __global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(Gather
     for (int u = 0; u < U; ++u) {
       if (src[u] != nullptr) st<Op::kDst, kGatherNtStore>(dst[u], Op::apply(x[u], sc[u]));
     }
+  }
+  return true;
+}
+
+// Workgroup w of sequence s takes tile w and, with FOLD = 2, tile w + J (J =
+// blocks_per_seq) when that is below units_per_seq.  FOLD is a template
+// parameter: a loop over a run-time count around the tile body measured
+// 3-17% slower than one tile per workgroup.
+template <class Op, bool I64, bool P64, int FOLD>
+__global__ __launch_bounds__(kFlatThreads) void gather_ragged_tile_kernel(GatherArgs a) {
+  const uint32_t wg = blockIdx.x;
+  const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
+  const int64_t w = wg - su * (uint32_t)a.blocks_per_seq;
+  if (!ragged_tile_unit<Op, I64, P64>(a, su, w * a.rows_per_wg)) return;
+  if constexpr (FOLD > 1) {
+    const int64_t u = w + a.blocks_per_seq;
+    if (u < a.units_per_seq) ragged_tile_unit<Op, I64, P64>(a, su, u * a.rows_per_wg);
   }
 }
 
@@ -2551,8 +2579,12 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
   const dim3 b(kBlockThreads);
   if (a.format == KVX_BLOCK_TABLE_RAGGED) {
     if (a.ragged_tile) {
-      hipLaunchKernelGGL((gather_ragged_tile_kernel<Op, I64, P64>), g, dim3(kFlatThreads), 0, s,
-                         a);
+      if (a.fold_log2 > 0)
+        hipLaunchKernelGGL((gather_ragged_tile_kernel<Op, I64, P64, 2>), g, dim3(kFlatThreads),
+                           0, s, a);
+      else
+        hipLaunchKernelGGL((gather_ragged_tile_kernel<Op, I64, P64, 1>), g, dim3(kFlatThreads),
+                           0, s, a);
     } else if (a.flat) {
       hipLaunchKernelGGL((gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_RAGGED, I64, P64>), g,
                          dim3(indexed_flat_threads<Op, KVX_BLOCK_TABLE_RAGGED>()), 0, s, a);

@@ -5,8 +5,11 @@ semantics; KVX_SPEC.md:99-122 for the indexed tables).
 gather_flat_kernel (PACKED) takes two units of its sequence per workgroup
 when a sequence has 4096 to 16384 units, a unit being one power-of-two
 share of a block: unit w and unit w + J of sequence s, J the workgroups per
-sequence.  The RAGGED tile, flat indexed and transposing gathers keep one
-tile per workgroup; their cases here cover 513 to 40001 tiles per sequence.
+sequence.  RAGGED copies in gather_ragged_tile_kernel take two tiles per
+workgroup the same way from 8192 to 65536 tiles per sequence (the 8197- and
+40001-tile cases); the flat indexed and transposing gathers keep one tile
+per workgroup.  The indexed and transposing cases cover 513 to 40001 tiles
+per sequence.
 
 Lengths cover both units of a workgroup valid, the second one cut inside
 its block or part, the second one starting exactly at seq_len (the
