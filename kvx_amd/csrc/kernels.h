@@ -1543,12 +1543,12 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 // wave launches (c2 with max_seq_len doubled at the same lengths: 1573 ->
 // 1699 us per layer).  Against the one-unit kernel (same-box A/B medians,
 // us per layer) two units measured c2 1540.3 -> 1531.8 (32 layers, 8192
-// units per sequence) and c4 633.4 -> 629.6 (4096 units).  Within this
-// kernel, two units against one: 2048 units or fewer (one or two KV heads)
-// 0-2.8% slower, where the last sequences' two-unit workgroups lengthen a
-// short launch; c5 (32768 units) -3.9% to +1.7% over three boxes; four units
-// slower at every shape; ordering the grid unit-major (all sequences' first
-// units first) 15-30% slower.  (Two tiles per workgroup in the flat indexed
+// units per sequence), c4 633.4 -> 629.6 (4096 units) and c5 2032.8 ->
+// 2005.9 (32768 units; 1.1-1.4% in two sessions).  Two units at 2048 units
+// or fewer (one or two KV heads) measured up to 2.8% slower, where the last
+// sequences' two-unit workgroups lengthen a short launch; four units were
+// slower at every shape; ordering the grid unit-major (all sequences'
+// first units first) 15-30% slower.  (Two tiles per workgroup in the flat indexed
 // and transposing gathers measured 1-10% slower than one; the RAGGED tile
 // gather takes two for long copies, below.)
 #ifndef KVX_FLAT_FOLD_LOG2
@@ -1558,7 +1558,7 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #define KVX_FLAT_FOLD_MIN_UNITS 4096
 #endif
 #ifndef KVX_FLAT_FOLD_MAX_UNITS
-#define KVX_FLAT_FOLD_MAX_UNITS 16384
+#define KVX_FLAT_FOLD_MAX_UNITS 65536
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
 // RAGGED copies in gather_ragged_tile_kernel: two tiles per workgroup when a

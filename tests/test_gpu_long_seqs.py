@@ -3,7 +3,7 @@ identical to the CPU oracle (kernels/kvx_paged_kv.cu:226-267 gather
 semantics; KVX_SPEC.md:99-122 for the indexed tables).
 
 gather_flat_kernel (PACKED) takes two units of its sequence per workgroup
-when a sequence has 4096 to 16384 units, a unit being one power-of-two
+when a sequence has 4096 to 65536 units, a unit being one power-of-two
 share of a block: unit w and unit w + J of sequence s, J the workgroups per
 sequence.  RAGGED copies in gather_ragged_tile_kernel take two tiles per
 workgroup the same way from 8192 to 65536 tiles per sequence (the 8197- and
@@ -32,8 +32,9 @@ DEV = "cuda"
 CASES = [
     # 16-byte rows, 256-byte blocks: one unit per block, 4096 units
     (DType.F16, DType.F16, 1, 8, 16, 4096, 0, 1),
-    # 16384 units, the top of the range
+    # 16384 and 32768 units
     (DType.F16, DType.F16, 1, 8, 16, 16384, 0, 1),
+    (DType.F16, DType.F16, 1, 8, 16, 32768, 0, 1),
     # c2's rows: 32 KiB blocks in 16 units, 515 blocks (8240 units, the
     # second unit of a workgroup starting half way through a block)
     (DType.BF16, DType.BF16, 8, 128, 16, 515, 0, 16),
@@ -55,7 +56,7 @@ def _ids(c):
 @pytest.mark.parametrize("idx64", [False, True])
 def test_two_units_per_workgroup(case, idx64):
     cdt, iodt, H, D, bs, blocks, short, parts = case
-    assert 4096 <= (blocks - short) * parts <= 16384  # the two-unit range
+    assert 4096 <= (blocks - short) * parts <= 65536  # the two-unit range
     gen = torch.Generator().manual_seed(1200 + CASES.index(case) * 2 + int(idx64))
     L = blocks * bs
     mbps = blocks - short
