@@ -30,8 +30,10 @@ DEV = "cuda"
 # (cache dtype, io dtype, H, D, block_size, blocks per sequence, table
 #  columns short of them, units per block)
 CASES = [
-    # 16-byte rows, 256-byte blocks: one unit per block, 4096 units
+    # 16-byte rows, 256-byte blocks: one unit per block, 4096 units, and an
+    # odd count (the last workgroup has no second unit)
     (DType.F16, DType.F16, 1, 8, 16, 4096, 0, 1),
+    (DType.F16, DType.F16, 1, 8, 16, 4097, 0, 1),
     # 16384 and 32768 units
     (DType.F16, DType.F16, 1, 8, 16, 16384, 0, 1),
     (DType.F16, DType.F16, 1, 8, 16, 32768, 0, 1),
