@@ -529,7 +529,20 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
         (uintptr_t)p.bytes_per_block);
   }
   hipStream_t s = as_stream(stream);
-  {
+  // PACKED gathers whose heads are contiguous runs of a power-of-two number
+  // of whole 128-byte lines (HND, or HND beside NHD; power-of-two head
+  // counts) take the flat kernel with head-run addressing instead of the LDS
+  // tiles: every 16-byte load and store is then part of a whole line.
+  auto head_runs = [&](const Geom &g) {
+    return g.s_inner == 1 && (g.pack == p.head_dim || g.s_piece == g.pack);
+  };
+  const int64_t head_run_bytes = (int64_t)p.head_dim * cs;
+  const bool head_run_flat =
+      KVX_FLAT_HEAD_RUNS && p.format == KVX_BLOCK_TABLE_PACKED && head_runs(p.gk) &&
+      head_runs(p.gv) && !(rows_contig(p.gk) && rows_contig(p.gv)) &&
+      log2_exact(p.heads) >= 0 && log2_exact(head_run_bytes) >= 0 && head_run_bytes >= 128 &&
+      p.block_size >= KVX_FLAT_HEAD_RUNS_MIN_BS;
+  if (!head_run_flat) {
     // Dense blocks that are not all row-major: the transposing gather.
     TileArgs t;
     int64_t tgrid = 0;
@@ -595,6 +608,11 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
            (g.s_off == row_elems || p.block_size == 1);
   };
   a.flat = rows_contiguous(p.gk) && rows_contiguous(p.gv);
+  a.cph_log2 = -1;
+  if (head_run_flat) {
+    a.flat = 1;
+    a.cph_log2 = log2_exact(p.head_dim / ge);  // ge divides the power-of-two run
+  }
   a.split_log2 = 0;
   a.fold_log2 = 0;
   a.units_per_seq = 0;

@@ -1414,6 +1414,7 @@ struct GatherArgs {
   int32_t ragged_tile;   // RAGGED: gather_ragged_tile_kernel
   int32_t fold_log2;     // PACKED flat gather: up to 1 << fold_log2 units per workgroup
   int32_t units_per_seq;  // PACKED flat gather: (block, part) units per sequence
+  int32_t cph_log2;       // head-run flat gather: log2(chunks per head)
 };
 
 // The (sequence, logical block) job of one workgroup: cache block and
@@ -1490,8 +1491,30 @@ __device__ __forceinline__ float run_scale(const GatherArgs &a, bool v, float ks
   return r.p[bid * r.s_block + (int64_t)h * r.s_head];
 }
 
+// Source of chunk i of a flat run that starts at chunk c0 of a block: with
+// HR (head runs) the block's chunks in output order are (row, head, chunk)
+// triples, each head's D elements contiguous at any row and head strides:
+// base is the block, and chunk c0 + i sits at row t, head h, chunk c of the
+// head (shifts: power-of-two heads and chunks per head).  Otherwise the run
+// is contiguous from base.
+template <class Op, bool HR>
+__device__ __forceinline__ const char *flat_src(const GatherArgs &a, const GeomBytes &g,
+                                                const char *base, int64_t c0, int64_t i) {
+  if constexpr (!HR) {
+    return base + i * Op::kSrc;
+  } else {
+    const uint32_t e = (uint32_t)(c0 + i);  // < block_size * nchunks < 2^31
+    const uint32_t t = e >> a.nchunks_log2;
+    const uint32_t r = e & ((1u << a.nchunks_log2) - 1u);
+    const uint32_t h = r >> a.cph_log2;
+    const uint32_t c = r & ((1u << a.cph_log2) - 1u);
+    return base + (int64_t)t * g.s_off + (int64_t)h * g.s_head + (int64_t)c * Op::kSrc;
+  }
+}
+
 // c0: chunk index of ck / cv counted from a row start (indexed scales).
-template <class Op>
+// HR: ck / cv are the blocks, the run's chunks addressed by flat_src.
+template <class Op, bool HR = false>
 __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, const char *cv,
                                           char *ok, char *ov, int64_t total, float ks, float vs,
                                           int64_t bid, int64_t c0) {
@@ -1514,7 +1537,8 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
     for (int u = 0; u < U; ++u) {
       const int64_t g = f + u * kFlatThreads;
       const bool v = g >= total;
-      x[u] = ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + (g - (v ? total : 0)) * Op::kSrc);
+      x[u] = ld<Op::kSrc, kGatherNtLoad>(
+          flat_src<Op, HR>(a, v ? a.gv : a.gk, v ? cv : ck, c0, g - (v ? total : 0)));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1529,9 +1553,11 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
     const int64_t i = f - (v ? total : 0);
     float sc = v ? vs : ks;
     if constexpr (Op::kScaled) sc = run_scale(a, v, ks, vs, bid, c0 + i);
-    st<Op::kDst, kGatherNtStore>((v ? ov : ok) + i * Op::kDst,
-                                 Op::apply(ld<Op::kSrc, kGatherNtLoad>((v ? cv : ck) + i * Op::kSrc),
-                                           sc));
+    st<Op::kDst, kGatherNtStore>(
+        (v ? ov : ok) + i * Op::kDst,
+        Op::apply(ld<Op::kSrc, kGatherNtLoad>(flat_src<Op, HR>(a, v ? a.gv : a.gk, v ? cv : ck,
+                                                                c0, i)),
+                  sc));
   }
 }
 
@@ -1561,6 +1587,16 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 #define KVX_FLAT_FOLD_MAX_UNITS 65536
 #endif
 constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
+// PACKED gathers of caches whose heads are contiguous runs of a power-of-two
+// number of whole 128-byte lines (HND; a power-of-two head count) in blocks
+// of at least KVX_FLAT_HEAD_RUNS_MIN_BS tokens take gather_flat_kernel with
+// head-run addressing (1) instead of the LDS tiles or the row kernel (0).
+#ifndef KVX_FLAT_HEAD_RUNS
+#define KVX_FLAT_HEAD_RUNS 1
+#endif
+#ifndef KVX_FLAT_HEAD_RUNS_MIN_BS
+#define KVX_FLAT_HEAD_RUNS_MIN_BS 64
+#endif
 // RAGGED copies in gather_ragged_tile_kernel: two tiles per workgroup when a
 // sequence has KVX_RAGGED_FOLD_MIN_UNITS to KVX_RAGGED_FOLD_MAX_UNITS tiles
 // (0 disables).  Against one tile per workgroup (same-box A/B, medians of 6
@@ -1578,7 +1614,7 @@ constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
 // (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
 // below units_per_seq and seq_len; unit u is share u & (2^split_log2 - 1)
 // of logical block u >> split_log2.
-template <class Op, bool I64>
+template <class Op, bool I64, bool HR>
 __global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a) {
   const uint32_t wg = blockIdx.x;
   const uint32_t su = wg / (uint32_t)a.blocks_per_seq;
@@ -1619,9 +1655,10 @@ __global__ __launch_bounds__(kFlatThreads) void gather_flat_kernel(GatherArgs a)
     if (c0 >= valid) continue;
     const int64_t cnt = valid - c0 < per_part ? valid - c0 : per_part;
     const int64_t out0 = (s * a.max_seq_len + t0) * a.out_row_bytes + c0 * Op::kDst;
-    flat_copy<Op>(a, a.src_k + bid[i] * a.gk.s_block + c0 * Op::kSrc,
-                  a.src_v + bid[i] * a.gv.s_block + c0 * Op::kSrc, a.dst_k + out0,
-                  a.dst_v + out0, cnt, ks, vs, bid[i], c0);
+    const int64_t skip = HR ? 0 : c0 * Op::kSrc;  // HR: flat_src addresses from the block
+    flat_copy<Op, HR>(a, a.src_k + bid[i] * a.gk.s_block + skip,
+                      a.src_v + bid[i] * a.gv.s_block + skip, a.dst_k + out0, a.dst_v + out0,
+                      cnt, ks, vs, bid[i], c0);
   }
 }
 
@@ -2609,7 +2646,10 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
                            g, b, 0, s, a);
       }
     } else if (a.flat) {
-      hipLaunchKernelGGL((gather_flat_kernel<Op, I64>), g, dim3(kFlatThreads), 0, s, a);
+      if (a.cph_log2 >= 0)
+        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, true>), g, dim3(kFlatThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, false>), g, dim3(kFlatThreads), 0, s, a);
     } else {
       hipLaunchKernelGGL((gather_rows_kernel<Op, I64>), g, b, 0, s, a);
     }

@@ -210,3 +210,52 @@ def test_one_head(orders, dt):
     vo = random_fill(torch.empty_like(ko), gen)
     check_gather_ragged(pc, kb, vb, ko, vo, rt, lens.to(DEV), L, cache_dtype=dt,
                         io_dtype=DType.BF16, k_scale=ks, v_scale=vs)
+
+
+# PACKED gathers of caches whose heads are contiguous runs of whole 128-byte
+# lines, in blocks of 64 tokens or more, take gather_flat_kernel with
+# head-run addressing (row, head, chunk of the head, any row and head
+# strides).  (cache dtype, K order, V order, block_size, H, D, pad, scales)
+HEAD_RUNS = [
+    (DType.BF16, "bhod", "bhod", 64, 8, 128, 0, None),             # HND
+    (DType.BF16, "bhod", "bohd", 128, 8, 128, 0, None),            # HND K, NHD V
+    (DType.F16, "bhod", "bhod", 256, 4, 64, 3, None),              # padded head runs
+    (DType.F32, "obhd", "bhod", 64, 2, 32, 0, None),               # offset axis outermost
+    (DType.F8_E4M3, "bhod", "bhod", 128, 4, 128, 0, "tensor"),     # dequantizing
+    (DType.F8_E5M2, "bhod", "bhod", 64, 8, 128, 0, SG.PER_HEAD),
+    (DType.F8_E4M3, "bhod", "bohd", 256, 2, 128, 0, SG.PER_BLOCK_HEAD),
+]
+
+
+def _hr_ids(c):
+    return f"{c[0].name}-{c[1]}-{c[2]}-bs{c[3]}-H{c[4]}-D{c[5]}-pad{c[6]}-{getattr(c[7], 'name', c[7])}"
+
+
+@pytest.mark.parametrize("case", HEAD_RUNS, ids=[_hr_ids(c) for c in HEAD_RUNS])
+@pytest.mark.parametrize("idx64", [False, True])
+def test_head_run_flat_gather(case, idx64):
+    dt, ko_, vo_, bs, H, D, pad, kind = case
+    gen = torch.Generator().manual_seed(1500 + HEAD_RUNS.index(case) * 2 + int(idx64))
+    nb = 9
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, None, None, gen, pad=pad)
+    S = 5
+    L = 3 * bs + bs // 2 + 3  # a partial last block
+    mbps = (L + bs - 1) // bs
+    table = torch.randint(0, nb, (S, mbps), generator=gen)
+    table[1, 0], table[2, 2], table[3, 1] = -1, nb + 1, nb
+    lens = torch.tensor([L, L + bs, bs + 5, 2 * bs - 3, 0])
+    itype = torch.int64 if idx64 else torch.int32
+    io = DType.BF16 if dt in (DType.F8_E4M3, DType.F8_E5M2) else dt
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks = vs = None
+    if kind == "tensor":
+        ks, vs = 0.0173, 0.0061
+    elif kind == SG.PER_HEAD:
+        ks, vs = (ScaleArg(kind, torch.empty(H).uniform_(0.002, 0.05, generator=gen).numpy())
+                  for _ in range(2))
+    elif kind is not None:
+        ks, vs = (ScaleArg(kind, torch.empty(nb, H).uniform_(0.002, 0.05, generator=gen).numpy(),
+                           stride=(1, nb)) for _ in range(2))
+    check_gather(pc, kb, vb, ko, vo, table.to(itype).to(DEV), lens.to(itype).to(DEV), L,
+                 cache_dtype=dt, io_dtype=io, k_scale=ks, v_scale=vs)
