@@ -188,7 +188,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
   const bool offsets = p.format == KVX_BLOCK_TABLE_KV_OFFSETS;
   const bool ragged = p.format == KVX_BLOCK_TABLE_RAGGED;
-  if (ragged && p.block_size > kWave) return false;  // one wave compares a tile's ids
+  if (ragged && p.block_size > kTileMaxRows) return false;  // a tile's row ids in LDS
   const int64_t bs = p.block_size;
   const int64_t H = p.heads;
   const int64_t D = p.head_dim;
@@ -229,6 +229,19 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
     if (reinterpret_cast<uintptr_t>(dst[i]) % dst_align != 0) return false;
   }
   if (!transposed) return false;  // row-major pairs: the flat kernels
+  // RAGGED blocks of more rows than a wave has lanes load their row ids with
+  // every thread and one more barrier: taken where a tensor's runs are
+  // narrower than a 128-byte line (x-packed, token axis innermost), which
+  // the row kernel reads piece by piece.  On MI355X (c2's lengths, RAGGED,
+  // 128-token blocks, same-box A/B) x-packed K and V 2715 -> 1720 us,
+  // vLLM's pair 5455 -> 2019 us; HND (256-byte runs) 1640 -> 1718 us, so HND
+  // keeps the row kernel.
+  if (ragged && bs > kWave) {
+    int64_t narrow = -1;
+    for (int i = 0; i < 2; ++i)
+      if (run_bytes[i] > 0 && (narrow < 0 || run_bytes[i] < narrow)) narrow = run_bytes[i];
+    if (narrow >= 128) return false;
+  }
   if ((D * cs) % src_chunk != 0) return false;  // chunks never straddle heads
   // Tile width: a power of two that divides the row and holds whole runs.
   // A row that is not a power of two (6 or 12 heads, say) makes several

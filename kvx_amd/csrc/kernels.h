@@ -1775,6 +1775,10 @@ struct TileTensor {
   int32_t pad_;
 };
 
+// Rows of a tile (block_size) at most: the planner keeps
+// block_size * (tw + 16) within 64 KiB of LDS with tw >= 128.
+constexpr int kTileMaxRows = 256;
+
 struct TileArgs {
   TileTensor t[2];
   const void *table;
@@ -1989,7 +1993,7 @@ __device__ __forceinline__ void unstage_gather_tile(const TileArgs &a, const Til
 template <class Op, int FMT, bool I64, bool P64>
 __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  __shared__ int64_t s_ids[kWave];  // RAGGED: block id of each row, -1 if skipped
+  __shared__ int64_t s_ids[kTileMaxRows];  // RAGGED: block id of each row, -1 if skipped
   __shared__ int32_t s_same;        // RAGGED: every row names block s_ids[0]
   const TileTensor tt = blockIdx.y ? a.t[1] : a.t[0];
   const uint32_t wg = blockIdx.x;
@@ -2019,23 +2023,41 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
     if (t0 >= n) return;
     const int64_t rem = n - t0;
     const int32_t rws = rem < bs ? (int32_t)rem : bs;
-    if (threadIdx.x < kWave) {
-      const int lane = (int)threadIdx.x;
-      int64_t id = -1;
-      if (lane < rws) {
-        id = load_idx<I64>(a.table, start + t0 + lane);
-        if (id < 0 || id >= a.num_blocks) id = -1;
-        s_ids[lane] = id;
+    if (bs <= kWave) {
+      // one wave loads the ids, one per lane, and a ballot compares them
+      if (threadIdx.x < kWave) {
+        const int lane = (int)threadIdx.x;
+        int64_t id = -1;
+        if (lane < rws) {
+          id = load_idx<I64>(a.table, start + t0 + lane);
+          if (id < 0 || id >= a.num_blocks) id = -1;
+          s_ids[lane] = id;
+        }
+        const int64_t first =
+            (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(id >> 32))
+                       << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)id));
+        const uint64_t same = __ballot(lane >= rws || id == first);
+        if (lane == 0) s_same = same == ~0ull;
       }
-      const int64_t first =
-          (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(id >> 32)) << 32) |
-                    (uint32_t)__builtin_amdgcn_readfirstlane((int)id));
-      const uint64_t same = __ballot(lane >= rws || id == first);
-      if (lane == 0) s_same = same == ~0ull;
+      __syncthreads();
+      bid = s_ids[0];
+      mixed = !s_same;
+    } else {
+      // blocks of more rows than a wave has lanes: every thread loads ids,
+      // then a barrier that ORs the threads' mismatches with row 0's id
+      for (int32_t r = (int32_t)threadIdx.x; r < rws; r += (int32_t)blockDim.x) {
+        int64_t id = load_idx<I64>(a.table, start + t0 + r);
+        if (id < 0 || id >= a.num_blocks) id = -1;
+        s_ids[r] = id;
+      }
+      __syncthreads();
+      bid = s_ids[0];
+      int differs = 0;
+      for (int32_t r = (int32_t)threadIdx.x; r < rws; r += (int32_t)blockDim.x)
+        differs |= s_ids[r] != bid;
+      mixed = __syncthreads_or(differs) != 0;
     }
-    __syncthreads();
-    bid = s_ids[0];
-    mixed = !s_same;
     if (!mixed) {
       if (bid < 0) return;  // every row skipped
       blk = tt.src + bid * tt.s_block;

@@ -259,3 +259,48 @@ def test_head_run_flat_gather(case, idx64):
                            stride=(1, nb)) for _ in range(2))
     check_gather(pc, kb, vb, ko, vo, table.to(itype).to(DEV), lens.to(itype).to(DEV), L,
                  cache_dtype=dt, io_dtype=io, k_scale=ks, v_scale=vs)
+
+
+# RAGGED gathers of dense blocks of more than 64 tokens in the LDS tiles:
+# every thread loads row ids, and one barrier tells whether a tile names one
+# block.  (cache dtype, K order, K x, V order, V x, block_size, H, D)
+RAGGED_BIG = [
+    (DType.BF16, "bhpox", 8, "bohd", None, 128, 8, 128),     # x-packed K, NHD V
+    (DType.BF16, "bhpox", 8, "bhdo", None, 256, 4, 64),      # vLLM's pair
+    (DType.BF16, "bhod", None, "bhod", None, 128, 8, 128),   # HND: the row kernel
+    (DType.F8_E4M3, "bhpox", 16, "bhpox", 16, 128, 4, 128),  # FP8, dequantizing
+]
+
+
+@pytest.mark.parametrize("case", RAGGED_BIG, ids=[
+    f"{c[0].name}-{c[1]}{c[2] or ''}-{c[3]}{c[4] or ''}-bs{c[5]}-H{c[6]}-D{c[7]}"
+    for c in RAGGED_BIG])
+@pytest.mark.parametrize("spoil", [False, True])
+def test_ragged_big_block_tiles(case, spoil):
+    dt, ko_, kx, vo_, vx, bs, H, D = case
+    idx = RAGGED_BIG.index(case)
+    rng = np.random.default_rng(1600 + 2 * idx + int(spoil))
+    gen = torch.Generator().manual_seed(1600 + 2 * idx + int(spoil))
+    nb = 7
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    S = 4
+    L = 2 * bs + bs // 2 + 3
+    counts = np.array([L, bs + 7, 0, L + 5])
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    parts = []
+    for c in counts:
+        blocks = rng.integers(0, nb, size=(int(c) + bs - 1) // bs + 1)
+        parts.append(blocks[np.arange(c) // bs])  # each block's tokens in order
+    indices = np.concatenate(parts).astype(np.int32)
+    if spoil:  # tiles whose rows name several blocks, or none
+        bad = rng.choice(indices.size, size=24, replace=False)
+        indices[bad] = rng.choice([-1, nb, nb + 3, 2], size=24)
+        indices[indptr[1]: indptr[1] + bs] = -1  # a whole block's rows skipped
+    rt = paged.RaggedTable(torch.from_numpy(indices).to(DEV), torch.from_numpy(indptr).to(DEV))
+    lens = torch.tensor([L, L, 3, L], dtype=torch.int32, device=DEV)
+    io = DType.BF16 if dt == DType.F8_E4M3 else dt
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks, vs = (0.0213, 0.0047) if dt == DType.F8_E4M3 else (None, None)
+    check_gather_ragged(pc, kb, vb, ko, vo, rt, lens, L, cache_dtype=dt, io_dtype=io,
+                        k_scale=ks, v_scale=vs)
