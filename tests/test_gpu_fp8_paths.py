@@ -139,3 +139,29 @@ def test_dequantizing_kv_offsets_gather_indexed_path(shape, fp8, kind):
     ks, vs = scales(kind, gen, nb, H)
     check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=fp8, io_dtype=io,
                          k_scale=ks, v_scale=vs)
+
+
+@pytest.mark.parametrize("kind", ["tensor", "head"])
+@pytest.mark.parametrize("fp8", FP8)
+@pytest.mark.parametrize("shape", [(1, 128), (1, 64), (2, 64)])
+def test_dequantizing_kv_offsets_tile_sized_workgroups(shape, fp8, kind):
+    """KV_OFFSETS dequantizing gathers of row-major blocks of one or two
+    heads: tiles of 16 rows of 64-256 bytes, in workgroups of 128 or 64
+    threads (one pass of four 8-byte chunks per thread)."""
+    H, D = shape
+    rng = np.random.default_rng(1700 + 4 * FP8.index(fp8) + 8 * H + D)
+    gen = torch.Generator().manual_seed(1700 + len(kind) + D)
+    bs, nb, S, L = 16, 40, 5, 150
+    pool = OffsetsPool(Layout.BLOCK_NHD, Layout.BLOCK_NHD, fp8, nb, bs, H, D, pitch_pad=16,
+                       gen=gen)
+    mbps = (L + bs - 1) // bs
+    raw = rng.integers(0, nb + 2, size=(S, 1, 2, mbps)).astype(np.uint32)
+    raw |= (rng.random(raw.shape) < 0.3).astype(np.uint32) << 31
+    offsets = torch.from_numpy(raw.view(np.int32)).to(DEV)
+    lens = torch.tensor([L, L - 9, bs + 1, 0, L + 7], dtype=torch.int32, device=DEV)
+    io = DType.BF16 if kind == "tensor" else DType.F16
+    ko = random_fill(torch.empty((S, L, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+    vo = random_fill(torch.empty_like(ko), gen)
+    ks, vs = scales(kind, gen, nb, H)
+    check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=fp8, io_dtype=io,
+                         k_scale=ks, v_scale=vs)
