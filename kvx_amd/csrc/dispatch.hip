@@ -116,26 +116,17 @@ int64_t dense_run_elems(const Geom &g, int64_t bs, int64_t H, int64_t D) {
 // dense blocks of which at least one is not row-major, or false.  On MI355X
 // (c2 shapes, bf16) it beats the row kernel for every run length measured:
 // token-innermost 2.45 -> 5.90 TB/s, x-packed 4.66 -> 5.88, HND (256-byte
-// runs) 5.14 -> 5.87.  KVX_TILE_BYTES is the cache bytes per tensor of one
-// tile (8 KiB measured best against 4 and 16 KiB).
-#ifndef KVX_TILE_BYTES
-#define KVX_TILE_BYTES 8192
-#endif
-#ifndef KVX_TILE_BYTES_PER_THREAD
-#define KVX_TILE_BYTES_PER_THREAD 32
-#endif
-// Narrowest tile width (cache bytes per row) the halving above goes to.
-#ifndef KVX_TILE_MIN_WIDTH
-#define KVX_TILE_MIN_WIDTH 128
-#endif
-// Tiles whose width is not a power of two: at most KVX_ODD_TILE_BYTES of
-// cache bytes per tensor, at least KVX_ODD_TILE_MIN.
-#ifndef KVX_ODD_TILE_BYTES
-#define KVX_ODD_TILE_BYTES 12288
-#endif
-#ifndef KVX_ODD_TILE_MIN
-#define KVX_ODD_TILE_MIN 4096
-#endif
+// runs) 5.14 -> 5.87.  kTileBytes is the cache bytes per tensor of one
+// tile (8 KiB measured best against 4 and 16 KiB); workgroups have about
+// one thread per kTileBytesPerThread bytes of tile.
+constexpr int64_t kTileBytes = 8192;
+constexpr int64_t kTileBytesPerThread = 32;
+// Narrowest tile width (cache bytes per row) the halving below goes to.
+constexpr int64_t kTileMinWidth = 128;
+// Tiles whose width is not a power of two: at most kOddTileBytes of cache
+// bytes per tensor, at least kOddTileMin.
+constexpr int64_t kOddTileBytes = 12288;
+constexpr int64_t kOddTileMin = 4096;
 
 int64_t gcd64(int64_t a, int64_t b) {
   while (b != 0) {
@@ -153,8 +144,8 @@ uint32_t magic_for(int64_t d) { return (uint32_t)(((uint64_t(1) << 32) + (uint64
 // rows or runs that are not a power of two, phase 2 dividing by chunks per
 // row with a multiply-high (HND heads of 96 or 80 bf16 elements, three
 // 256-byte heads): widths of whole 128-byte lines first, then the tile
-// nearest `target` bytes, the wider on a tie, within KVX_ODD_TILE_MIN and
-// max(target, KVX_ODD_TILE_BYTES); -1 if none.  On MI355X (c2's table, 4
+// nearest `target` bytes, the wider on a tie, within kOddTileMin and
+// max(target, kOddTileBytes); -1 if none.  On MI355X (c2's table, 4
 // layers) such gathers took 5-8% less time than in gather_rows_kernel;
 // widths that split output lines between two workgroups (320 or 192
 // bytes) measured 7-12% slower than line-multiple ones (640 or 384 bytes),
@@ -162,12 +153,12 @@ uint32_t magic_for(int64_t d) { return (uint32_t)(((uint64_t(1) << 32) + (uint64
 // HND 8 x 96 bf16 3% faster in 6 KiB tiles than in 12 KiB ones.
 int64_t odd_tile_width(int64_t row, int64_t unit, int64_t bs, int64_t target) {
   if (row % unit != 0) return -1;
-  const int64_t cap = target > KVX_ODD_TILE_BYTES ? target : KVX_ODD_TILE_BYTES;
+  const int64_t cap = target > kOddTileBytes ? target : kOddTileBytes;
   int64_t tw = -1, best = 0;
   for (int64_t k = row / unit; k >= 1; --k) {
     if ((row / unit) % k != 0) continue;
     const int64_t w = unit * k, bytes = w * bs;
-    if (bytes < KVX_ODD_TILE_MIN || bytes > cap) continue;
+    if (bytes < kOddTileMin || bytes > cap) continue;
     const int64_t dist = bytes > target ? bytes - target : target - bytes;
     const int64_t score = (w % 128 == 0 ? 0 : (int64_t)1 << 40) + dist;
     if (tw < 0 || score < best) {
@@ -179,10 +170,8 @@ int64_t odd_tile_width(int64_t row, int64_t unit, int64_t bs, int64_t target) {
 }
 
 // gather_rows_kernel: cache row bytes per tensor of one workgroup's share
-// of a block, at least (blocks of up to KVX_ROWS_TILE_BYTES stay whole).
-#ifndef KVX_ROWS_TILE_BYTES
-#define KVX_ROWS_TILE_BYTES 32768
-#endif
+// of a block, at least (blocks of up to kRowsTileBytes stay whole).
+constexpr int64_t kRowsTileBytes = 32768;
 
 bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
                 int64_t *grid, uint32_t *lds_bytes) {
@@ -251,18 +240,18 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   // 3 x 128 heads 0.587 in 4 KiB tiles against 0.623.
   int64_t tw = row_cache & -row_cache;
   if (odd_run || tw < min_tw ||
-      ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_TILE_BYTES)) {
-    tw = odd_tile_width(row_cache, unit, bs, KVX_TILE_BYTES);
+      ((row_cache & (row_cache - 1)) != 0 && tw * bs < kTileBytes)) {
+    tw = odd_tile_width(row_cache, unit, bs, kTileBytes);
     if (tw < 0) return false;
   } else {
-    // halve toward KVX_TILE_BYTES, but not below one 128-byte output line per
+    // halve toward kTileBytes, but not below one 128-byte output line per
     // row (blocks of 128 or 256 tokens then take 16 or 32 KiB tiles): on
     // MI355X (c2's lengths, bf16 x-packed blocks of 128 / 256 tokens) 2315 /
     // 6752 -> 1789 / 1823 us per layer, where narrower rows split output
     // lines between workgroups.  (Runs of whole lines, HND, also gathered
     // faster in these tiles than in gather_rows_kernel at every block size
     // that fits: 16-128 tokens, 4-12% at c2's size.)
-    while (tw * bs > KVX_TILE_BYTES && tw / 2 >= min_tw && tw / 2 >= KVX_TILE_MIN_WIDTH) tw /= 2;
+    while (tw * bs > kTileBytes && tw / 2 >= min_tw && tw / 2 >= kTileMinWidth) tw /= 2;
   }
   const int64_t pitch = tw + kTilePad;
   if (bs * pitch > 64 * 1024) return false;
@@ -287,7 +276,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   t->cpr = (int32_t)(tw / src_chunk);
   t->cpr_magic = t->tw_log2 < 0 ? magic_for(t->cpr) : 0;
   t->pitch = (int32_t)pitch;
-  // Workgroups of about one thread per KVX_TILE_BYTES_PER_THREAD bytes of
+  // Workgroups of about one thread per kTileBytesPerThread bytes of
   // tile (64 to 256 threads): smaller tiles run in smaller workgroups, more
   // of them resident per CU, so that as many bytes are in flight as for the
   // 8 KiB tiles of wider rows.  On MI355X (c2's table, one KV head) 4 KiB
@@ -295,7 +284,7 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   // in 256-thread and 209.7 us in 64-thread ones; HND two-token blocks 1585
   // against 2058 us per layer.
   t->threads = kBlockThreads;
-  while (t->threads > 64 && tw * bs < (int64_t)t->threads * KVX_TILE_BYTES_PER_THREAD)
+  while (t->threads > 64 && tw * bs < (int64_t)t->threads * kTileBytesPerThread)
     t->threads /= 2;
   t->max_seq_len = p.max_seq_len;
   t->num_blocks = p.num_blocks;
@@ -327,20 +316,16 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
 // at least one is not row-major, 16-byte aligned block addresses, io rows
 // aligned to the tile op's source chunk, and (quantizing) heads a whole
 // number of 8-element chunks, so that every chunk has one scale.
-// KVX_WRITE_TILE_BYTES: cache bytes per tensor of one tile of a copying
-// write; KVX_QUANT_TILE_BYTES the same for the FP8 quantizing write (whose
+// kWriteTileBytes: cache bytes per tensor of one tile of a copying write;
+// kQuantTileBytes the same for the FP8 quantizing write (whose
 // io rows are 2-4x its cache bytes).  On MI355X (c3 shapes, inputs not
 // cache-resident) 8 KiB measured 1.5-3% faster than 16 KiB for copies, and
 // 4-5% faster than 32 or 64 KiB; the quantizing write is 4-8% faster with
 // 16 KiB; 4 KiB is 25-30% slower for both.  Tiles are 0-5% faster than
 // staging whole blocks of K and V in one workgroup (x-packed / HND), 5x for
 // the token-innermost value cache.
-#ifndef KVX_WRITE_TILE_BYTES
-#define KVX_WRITE_TILE_BYTES 8192
-#endif
-#ifndef KVX_QUANT_TILE_BYTES
-#define KVX_QUANT_TILE_BYTES 16384
-#endif
+constexpr int64_t kWriteTileBytes = 8192;
+constexpr int64_t kQuantTileBytes = 16384;
 bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int64_t *grid,
                       uint32_t *lds_bytes) {
   const int64_t bs = p.block_size;
@@ -385,7 +370,7 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   }
   if (!transposed) return false;
   const int64_t tile_bytes =
-      p.conv == kConvQuant ? KVX_QUANT_TILE_BYTES : KVX_WRITE_TILE_BYTES;
+      p.conv == kConvQuant ? kQuantTileBytes : kWriteTileBytes;
   // as in plan_tiles: a power-of-two tile width that divides the row, and
   // a full copy tile for a row that is not a power of two (c3's size into
   // HND caches of 6 x 128 or 12 x 64 bf16 heads: 0.527 of peak against 0.43
@@ -395,7 +380,7 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   // 0.50 for HND; HND 8 x 80 0.61 against 0.50, 8 x 96 0.60 against 0.57
   int64_t tw = row_cache & -row_cache;
   if (odd_run || tw < min_tw ||
-      ((row_cache & (row_cache - 1)) != 0 && tw * bs < KVX_WRITE_TILE_BYTES)) {
+      ((row_cache & (row_cache - 1)) != 0 && tw * bs < kWriteTileBytes)) {
     tw = odd_tile_width(row_cache, unit, bs, tile_bytes);
     if (tw < 0) return false;
   } else {
@@ -411,12 +396,12 @@ bool plan_write_tiles(const WritePlan &p, int cs, int is, WriteTileArgs *wt, int
   wt->cpr = (int32_t)(tw / (p.conv == kConvQuant ? 8 : 16));
   wt->cpr_magic = wt->tw_log2 < 0 ? magic_for(wt->cpr) : 0;
   wt->pitch = (int32_t)pitch;
-  // about one thread per KVX_TILE_BYTES_PER_THREAD bytes of tile, as for
+  // about one thread per kTileBytesPerThread bytes of tile, as for
   // the gather: small tiles (one KV head) in smaller workgroups.  On MI355X
   // (c3's bytes in one-head rows) vLLM's pair 61.3 -> 53.4 us, x-packed K
   // and V 58.6 -> 53.1 us; c3's own 8 KiB tiles unchanged.
   wt->threads = kBlockThreads;
-  while (wt->threads > 64 && tw * bs < (int64_t)wt->threads * KVX_TILE_BYTES_PER_THREAD)
+  while (wt->threads > 64 && tw * bs < (int64_t)wt->threads * kTileBytesPerThread)
     wt->threads /= 2;
   wt->bs_log2 = bs_log2;
   wt->cache_es_log2 = log2_exact(cs);
@@ -489,7 +474,7 @@ kvx_status_t enqueue_write(const WritePlan &p, void *stream) {
   const int64_t flat_total = (int64_t)p.num_tokens * a.nchunks;
   const bool flat_div_ok =
       a.nchunks_log2 >= 0 || (flat_total + kFlatThreads) * a.nchunks <= (int64_t(1) << 32);
-  if (kWriteFlat && row_dense(p.gk) && row_dense(p.gv) && flat_div_ok) {
+  if (row_dense(p.gk) && row_dense(p.gv) && flat_div_ok) {
     const int64_t fg = (flat_total + kFlatThreads - 1) / kFlatThreads;
     if (grid_fits(fg, kFlatThreads)) wl.flat_grid = fg;  // else write_kernel's grid-stride loop
   }
@@ -526,12 +511,10 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
            (g.s_off == row_elems_all || p.block_size == 1);
   };
   const bool ragged_tile =
-      p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv) &&
-      (p.conv == kConvDequant ? KVX_RAGGED_TILE_DEQUANT != 0 : KVX_RAGGED_TILE_COPY != 0);
-  const int max_bytes =
-      p.conv != kConvDequant ? 16
-      : p.format == KVX_BLOCK_TABLE_RAGGED && !ragged_tile ? KVX_RAGGED_DEQUANT_CHUNK
-                                                           : KVX_DEQUANT_CHUNK;
+      p.format == KVX_BLOCK_TABLE_RAGGED && rows_contig(p.gk) && rows_contig(p.gv);
+  const int max_bytes = p.conv != kConvDequant                               ? 16
+                        : p.format == KVX_BLOCK_TABLE_RAGGED && !ragged_tile ? kRaggedDequantChunk
+                                                                             : kDequantChunk;
   const void *base_k = p.src_k;
   const void *base_v = p.src_v;
   if (p.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
@@ -551,17 +534,17 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   };
   const int64_t head_run_bytes = (int64_t)p.head_dim * cs;
   const bool head_run_flat =
-      KVX_FLAT_HEAD_RUNS && p.format == KVX_BLOCK_TABLE_PACKED && head_runs(p.gk) &&
+      p.format == KVX_BLOCK_TABLE_PACKED && head_runs(p.gk) &&
       head_runs(p.gv) && !(rows_contig(p.gk) && rows_contig(p.gv)) &&
       log2_exact(p.heads) >= 0 && log2_exact(head_run_bytes) >= 0 && head_run_bytes >= 128 &&
-      p.block_size >= KVX_FLAT_HEAD_RUNS_MIN_BS;
+      p.block_size >= kFlatHeadRunsMinBs;
   if (!head_run_flat) {
     // Dense blocks that are not all row-major: the transposing gather.
     TileArgs t;
     int64_t tgrid = 0;
     uint32_t tlds = 0;
     const bool dq = p.conv == kConvDequant;
-    if (p.seq_count > 0 && plan_tiles(p, cs, is, dq ? KVX_DEQUANT_CHUNK : 16, &t, &tgrid, &tlds)) {
+    if (p.seq_count > 0 && plan_tiles(p, cs, is, dq ? kDequantChunk : 16, &t, &tgrid, &tlds)) {
       if (tgrid == 0) return KVX_STATUS_OK;
       const bool i64 = p.lens_is64 != 0;
       const bool p64 = p.indptr_is64 != 0;
@@ -644,26 +627,26 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     const bool chunks_ok = a.nchunks_log2 >= 0 || a.nchunks <= 1024;
     a.flat = row_dense(p.gk) && row_dense(p.gv) && chunks_ok;
     if (ragged_tile && chunks_ok) {
-      // R rows of about KVX_FLAT_TILE_BYTES of cache per tensor: a power of
+      // R rows of about kFlatTileBytes of cache per tensor: a power of
       // two <= 64 (one block id per lane) that divides block_size
-      int64_t want = KVX_FLAT_TILE_BYTES / (row_elems * cs);
+      int64_t want = kFlatTileBytes / (row_elems * cs);
       int64_t r = 1;
       while (r * 2 <= want && r * 2 <= kWave && p.block_size % (r * 2) == 0) r *= 2;
       a.ragged_tile = 1;
       a.rows_per_wg = (int32_t)r;
       a.blocks_per_seq = (int32_t)(((int64_t)p.max_seq_len + r - 1) / r);
-      // copies of sequences of KVX_RAGGED_FOLD_MIN_UNITS to _MAX_UNITS tiles:
-      // two tiles per workgroup, tile w and w + J (J workgroups per sequence)
+      // copies of sequences of kRaggedFoldMinUnits to kRaggedFoldMaxUnits
+      // tiles: two tiles per workgroup, tile w and w + J (J workgroups per
+      // sequence)
       a.units_per_seq = a.blocks_per_seq;
-      if (p.conv == kConvCopy && KVX_RAGGED_FOLD_MIN_UNITS > 0 &&
-          a.blocks_per_seq >= KVX_RAGGED_FOLD_MIN_UNITS &&
-          a.blocks_per_seq <= KVX_RAGGED_FOLD_MAX_UNITS) {
+      if (p.conv == kConvCopy && a.blocks_per_seq >= kRaggedFoldMinUnits &&
+          a.blocks_per_seq <= kRaggedFoldMaxUnits) {
         a.fold_log2 = 1;  // the kernel is built for one or two tiles
         a.blocks_per_seq = (a.blocks_per_seq + 1) >> 1;
       }
     }
     const bool ragged_copy = a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy;
-    int64_t rows = (ragged_copy ? KVX_RAGGED_COPY_TILE_BYTES : KVX_GATHER_TILE_BYTES) /
+    int64_t rows = (ragged_copy ? kRaggedCopyTileBytes : kGatherTileBytes) /
                    (row_elems * cs);
     const int64_t per_pass = a.flat ? 1 : (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
     rows = rows < per_pass ? per_pass : rows;
@@ -680,31 +663,30 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
     }
   } else if (a.flat) {
     // split a block's chunks into a power-of-two number of equal ranges of
-    // about KVX_FLAT_TILE_BYTES of cache per tensor, while the grid stays
+    // about kFlatTileBytes of cache per tensor, while the grid stays
     // within HIP's limits (larger ranges loop inside a workgroup)
     const int64_t chunks = (int64_t)p.block_size * a.nchunks;
     const int64_t chunk_bytes = (int64_t)ge * cs;
     const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
-    while ((chunks >> a.split_log2) * chunk_bytes > KVX_FLAT_TILE_BYTES &&
+    while ((chunks >> a.split_log2) * chunk_bytes > kFlatTileBytes &&
            ((chunks >> (a.split_log2 + 1)) << (a.split_log2 + 1)) == chunks &&
            a.split_log2 < 16 && grid_fits(blocks << (a.split_log2 + 1), kFlatThreads))
       ++a.split_log2;
     const int64_t per_seq = (int64_t)a.blocks_per_seq << a.split_log2;  // units
     if (per_seq > 0x7FFFFFFF) return KVX_STATUS_UNSUPPORTED;
     // up to 1 << fold_log2 units per workgroup, strided by the workgroups
-    // per sequence (KVX_FLAT_FOLD_LOG2)
+    // per sequence (kFlatFoldLog2)
     a.units_per_seq = (int32_t)per_seq;
-    if (per_seq >= KVX_FLAT_FOLD_MIN_UNITS && per_seq <= KVX_FLAT_FOLD_MAX_UNITS)
-      a.fold_log2 = KVX_FLAT_FOLD_LOG2;
+    if (per_seq >= kFlatFoldMinUnits && per_seq <= kFlatFoldMaxUnits) a.fold_log2 = kFlatFoldLog2;
     a.blocks_per_seq = (int32_t)((per_seq + (1 << a.fold_log2) - 1) >> a.fold_log2);
   } else if (a.bs_log2 >= 0) {
     // gather_rows_kernel: a power-of-two block's rows split into
-    // 1 << split_log2 equal ranges of at least KVX_ROWS_TILE_BYTES of cache
+    // 1 << split_log2 equal ranges of at least kRowsTileBytes of cache
     // rows per tensor (and one full pass of the row groups), so that big
     // blocks still give the grid enough workgroups: on MI355X (c2's lengths
     // in 256-token HND blocks, bf16) 2009 -> 1775 us per layer
     const int64_t per_pass = (int64_t)kWavesPerBlock * (kWave >> a.lpt_log2);
-    int64_t want = KVX_ROWS_TILE_BYTES / (row_elems * cs);
+    int64_t want = kRowsTileBytes / (row_elems * cs);
     if (want < per_pass) want = per_pass;
     const int64_t blocks = (int64_t)p.seq_count * a.blocks_per_seq;
     while ((p.block_size >> (a.split_log2 + 1)) >= want && a.split_log2 < 16 &&
@@ -723,7 +705,7 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   } else if (a.ragged_tile) {
     threads = kFlatThreads;
   } else if (a.flat && p.format == KVX_BLOCK_TABLE_RAGGED && p.conv == kConvCopy) {
-    threads = KVX_RAGGED_COPY_THREADS;
+    threads = kRaggedCopyThreads;
   }
   // one workgroup per (sequence, tile): a batch whose grid exceeds HIP's
   // limits (some 4 x 10^9 work-items) is not launched

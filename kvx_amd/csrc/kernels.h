@@ -51,153 +51,88 @@ constexpr int32_t kRunOdd = 30;
 // the error x * f / 2^32 < 1 / d whenever x * d <= 2^32, so the floor is
 // exact there.  The planners only pass (x, d) pairs that satisfy it.
 __device__ __forceinline__ uint32_t div_magic(uint32_t x, uint32_t m) { return __umulhi(x, m); }
-// Compile-time tuning knobs of the contiguous-block gather (defaults are the
-// measured best on MI355X): chunks per lane in flight for the copy and for
-// the FP8 dequantizing gather, and non-temporal (streaming) loads of the
-// cache / stores of the output.  A lane moves one K and one V chunk;
+// Tuning constants: each value is the measured best on MI355X, and its
+// comment gives the same-box A/B behind it.
+//
+// Chunks per lane in flight in the contiguous-block gathers, for the copy
+// and for the FP8 dequantizing gather.  A lane moves one K and one V chunk;
 // loading both before storing either made the bf16 copy (c2) 7% slower and
 // the dequantizing gather (c4) 2% faster (256-thread, 4 KiB tiles).
-#ifndef KVX_FLAT_UNROLL
-#define KVX_FLAT_UNROLL 1
-#endif
-#ifndef KVX_FLAT_UNROLL_DEQUANT
-#define KVX_FLAT_UNROLL_DEQUANT 2
-#endif
-#ifndef KVX_GATHER_NT_LOAD
-#define KVX_GATHER_NT_LOAD 1
-#endif
-#ifndef KVX_GATHER_NT_STORE
-#define KVX_GATHER_NT_STORE 1
-#endif
+constexpr int kFlatUnroll = 1;
+constexpr int kFlatUnrollDequant = 2;
+// Non-temporal (streaming) cache loads and output stores in every gather:
+// together 4-13% faster than either alone.
+constexpr bool kGatherNtLoad = true;
+constexpr bool kGatherNtStore = true;
 // Contiguous-block gather (gather_flat_kernel): threads per workgroup (also
 // those of the row-dense write, write_flat_kernel) and cache bytes per
 // tensor per workgroup.  A block's valid chunks are split into a
-// power-of-two number of equal ranges of at most this size, so that each
-// lane copies one 16-byte chunk of K and one of V (2 KiB for power-of-two
-// rows).  On MI355X (c2, same box) 128 threads and 2 KiB measured 3.7%
-// faster than 256 threads and 4 KiB, 64 threads and 1 KiB 1% slower (2%
-// faster on c5's 64 KiB blocks); tiles that leave a lane one chunk, or give
-// it more than two, were 5-40% slower.  The 3 KiB bound changes only rows
-// whose chunk count is not a power of two: head_dim 96 or 80 (8 heads, bf16)
-// then splits into 192- or 160-chunk ranges instead of 96 or 80, 0.670 ->
-// 0.697 and 0.657 -> 0.693 of peak at c2's table.
-#ifndef KVX_FLAT_THREADS
-#define KVX_FLAT_THREADS 128
-#endif
-#ifndef KVX_FLAT_TILE_BYTES
-#define KVX_FLAT_TILE_BYTES 3072
-#endif
-// Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about this
-// many cache bytes of each tensor, in 256-thread workgroups.  The RAGGED
-// copy of row-dense caches whose rows are not contiguous in the block
-// (gather_indexed_flat_kernel without a dequant) uses
-// KVX_RAGGED_COPY_THREADS threads and KVX_RAGGED_COPY_TILE_BYTES instead: on
-// MI355X (c2, same box) 64 threads and 2 KiB measured 7% faster than 256
-// threads and 4 KiB, 128 threads and 2 KiB 5%; the same change made
-// KV_OFFSETS copies 1-2% and that kernel's dequantizing gather 2-8% slower.
-#ifndef KVX_GATHER_TILE_BYTES
-#define KVX_GATHER_TILE_BYTES 4096
-#endif
-#ifndef KVX_RAGGED_COPY_THREADS
-#define KVX_RAGGED_COPY_THREADS 64
-#endif
-#ifndef KVX_RAGGED_COPY_TILE_BYTES
-#define KVX_RAGGED_COPY_TILE_BYTES 2048
-#endif
+// power-of-two number of equal ranges of at most kFlatTileBytes, so that
+// each lane copies one 16-byte chunk of K and one of V (2 KiB for
+// power-of-two rows).  On MI355X (c2, same box) 128 threads and 2 KiB
+// measured 3.7% faster than 256 threads and 4 KiB, 64 threads and 1 KiB 1%
+// slower (2% faster on c5's 64 KiB blocks); tiles that leave a lane one
+// chunk, or give it more than two, were 5-40% slower.  The 3 KiB bound
+// changes only rows whose chunk count is not a power of two: head_dim 96 or
+// 80 (8 heads, bf16) then splits into 192- or 160-chunk ranges instead of
+// 96 or 80, 0.670 -> 0.697 and 0.657 -> 0.693 of peak at c2's table.
+constexpr int kFlatThreads = 128;
+constexpr int64_t kFlatTileBytes = 3072;
+// Output rows per workgroup of the RAGGED / KV_OFFSETS gathers: about
+// kGatherTileBytes cache bytes of each tensor, in 256-thread workgroups.
+// The RAGGED copy of row-dense caches whose rows are not contiguous in the
+// block (gather_indexed_flat_kernel without a dequant) uses
+// kRaggedCopyThreads threads and kRaggedCopyTileBytes instead: on MI355X
+// (c2, same box) 64 threads and 2 KiB measured 7% faster than 256 threads
+// and 4 KiB, 128 threads and 2 KiB 5%; the same change made KV_OFFSETS
+// copies 1-2% and that kernel's dequantizing gather 2-8% slower.
+constexpr int64_t kGatherTileBytes = 4096;
+constexpr int kRaggedCopyThreads = 64;
+constexpr int64_t kRaggedCopyTileBytes = 2048;
 // RAGGED gathers of row-contiguous caches (canonical NHD blocks) take
-// gather_ragged_tile_kernel (1) or gather_indexed_flat_kernel (0), for
-// copies and for dequantizing gathers.  On MI355X (same-box A/B, medians of
-// 6 alternating rounds) the tile kernel took c4's FP8 dequantizing gather
-// from 690 to 629 us and c5's copy from 2336 to 2241 us; c2's copy measured
-// 1587 against 1571 us.
-#ifndef KVX_RAGGED_TILE_COPY
-#define KVX_RAGGED_TILE_COPY 1
-#endif
-#ifndef KVX_RAGGED_TILE_DEQUANT
-#define KVX_RAGGED_TILE_DEQUANT 1
-#endif
+// gather_ragged_tile_kernel, for copies and for dequantizing gathers.
+// Against gather_indexed_flat_kernel on MI355X (same-box A/B, medians of 6
+// alternating rounds) it took c4's FP8 dequantizing gather from 690 to
+// 629 us and c5's copy from 2336 to 2241 us; c2's copy measured 1587
+// against 1571 us.
 // Chunks per thread the RAGGED / KV_OFFSETS flat gather resolves and loads
 // together (the table load and the data load of each are dependent).
-#ifndef KVX_INDEXED_UNROLL
-#define KVX_INDEXED_UNROLL 4
-#endif
-// KV_OFFSETS row-dense gather: table entries of the dequantizing gather are
-// loaded once per workgroup tile (1) or by every chunk (0).  The copy gather
-// always loads them per chunk: on MI355X that measures 5% faster for bf16,
-// while per-chunk loads cost the dequantizing gather (8-byte source chunks,
-// twice the table loads per byte) 15%.
-#ifndef KVX_OFFSETS_TILE
-#define KVX_OFFSETS_TILE 1
-#endif
-constexpr bool kOffsetsTile = KVX_OFFSETS_TILE != 0;
-// The copy gather takes per-tile entries for rows of at most this many
-// cache bytes, and for rows whose chunk count is not a power of two: on
-// MI355X (c2's table, bf16) one KV head (256-byte rows) measured 200.8
-// against 211.7 us and two heads 413.9 against 423.0 us, 576-element MLA
-// rows 1050 us against 1185 us per chunk (1142 us in gather_indexed_kernel)
-// and 6 x 128 rows 1290 against 1392 us, while c2's 2 KiB rows measured
-// 1614.7 against 1526.5 us.
-#ifndef KVX_OFFSETS_TILE_COPY_ROW
-#define KVX_OFFSETS_TILE_COPY_ROW 512
-#endif
-// FP8 cache bytes per chunk of the dequantizing gathers (8 or 16): 16-byte
-// chunks measured 3% faster for the RAGGED kernels that load a block id per
-// chunk (gather_indexed_flat_kernel; half the id loads) and 20-40% slower
-// for every other gather, gather_ragged_tile_kernel included (8).
-#ifndef KVX_DEQUANT_CHUNK
-#define KVX_DEQUANT_CHUNK 8
-#endif
-#ifndef KVX_RAGGED_DEQUANT_CHUNK
-#define KVX_RAGGED_DEQUANT_CHUNK 16
-#endif
-// Non-temporal io-row loads of the tiled block write and of the per-token
-// write, and non-temporal cache stores of every write kernel.  On MI355X
-// (c3 shapes) non-temporal stores make the tiled write 2-9% faster and the
-// per-token prefill write 14% faster (decode writes are unchanged);
-// non-temporal loads make the tiled write 10-20% slower and the per-token
-// prefill write 2-5% faster.
-#ifndef KVX_WRITE_NT_LOAD
-#define KVX_WRITE_NT_LOAD 0
-#endif
-// write_flat_kernel: when a row has at least 64 chunks, every lane of a
-// wave belongs to one token; the slot is then one scalar load per wave (1)
-// instead of one vector load per lane (0).  Kernel traces on MI355X: c4's
-// quantizing write 5.11 against 5.45 us, c2's and c5's writes unchanged
-// (3.90 / 3.87 and 4.75 / 4.77 us).
-#ifndef KVX_WRITE_FLAT_UNIFORM_SLOT
-#define KVX_WRITE_FLAT_UNIFORM_SLOT 1
-#endif
-// The row loads of write_flat_kernel and write_kernel are forced ahead of
-// the slot test (1), or left to the compiler (0), which may sink them below
-// it.  On MI355X (kernel traces, same box) forcing them measured no gain:
-// c2's decode write 3.90 against 3.88 us, c4's quantizing write 5.11
-// against 4.86 us, c5's 2048-token write 4.75 against 4.82 us.
-#ifndef KVX_WRITE_KEEP_LOADS
-#define KVX_WRITE_KEEP_LOADS 0
-#endif
-// Row-dense writes take write_flat_kernel (1) or write_kernel (0).
-#ifndef KVX_WRITE_FLAT
-#define KVX_WRITE_FLAT 1
-#endif
-#ifndef KVX_TOKEN_WRITE_NT_LOAD
-#define KVX_TOKEN_WRITE_NT_LOAD 1
-#endif
-#ifndef KVX_WRITE_NT_STORE
-#define KVX_WRITE_NT_STORE 1
-#endif
-constexpr bool kWriteNtLoad = KVX_WRITE_NT_LOAD != 0;
-constexpr bool kTokenWriteNtLoad = KVX_TOKEN_WRITE_NT_LOAD != 0;
-constexpr bool kWriteFlat = KVX_WRITE_FLAT != 0;
-constexpr bool kWriteFlatUniformSlot = KVX_WRITE_FLAT_UNIFORM_SLOT != 0;
-constexpr bool kWriteKeepLoads = KVX_WRITE_KEEP_LOADS != 0;
-
-constexpr bool kWriteNtStore = KVX_WRITE_NT_STORE != 0;
-constexpr int kFlatUnroll = KVX_FLAT_UNROLL;
-constexpr int kFlatThreads = KVX_FLAT_THREADS;
-constexpr int kFlatUnrollDequant = KVX_FLAT_UNROLL_DEQUANT;
-constexpr int kIndexedUnroll = KVX_INDEXED_UNROLL;
-constexpr bool kGatherNtLoad = KVX_GATHER_NT_LOAD != 0;
-constexpr bool kGatherNtStore = KVX_GATHER_NT_STORE != 0;
+constexpr int kIndexedUnroll = 4;
+// KV_OFFSETS row-dense gather: the dequantizing gather loads its table
+// entries once per workgroup tile (per-chunk loads cost it, with 8-byte
+// source chunks and twice the table loads per byte, 15%).  The copy gather
+// takes per-tile entries for rows of at most kOffsetsTileCopyRow cache
+// bytes and for rows whose chunk count is not a power of two, per-chunk
+// entries otherwise: on MI355X (c2's table, bf16) one KV head (256-byte
+// rows) measured 200.8 against 211.7 us and two heads 413.9 against
+// 423.0 us per tile, 576-element MLA rows 1050 us against 1185 us per chunk
+// (1142 us in gather_indexed_kernel) and 6 x 128 rows 1290 against 1392 us,
+// while c2's 2 KiB rows measured 1614.7 per tile against 1526.5 us per
+// chunk.
+constexpr int64_t kOffsetsTileCopyRow = 512;
+// FP8 cache bytes per chunk of the dequantizing gathers: 16-byte chunks
+// measured 3% faster for the RAGGED kernels that load a block id per chunk
+// (gather_indexed_flat_kernel; half the id loads) and 20-40% slower for
+// every other gather, gather_ragged_tile_kernel included (8 bytes).
+constexpr int kDequantChunk = 8;
+constexpr int kRaggedDequantChunk = 16;
+// Non-temporal io-row loads of the tiled block write (off) and of the
+// per-token write (on), and non-temporal cache stores of every write
+// kernel (on).  On MI355X (c3 shapes) non-temporal stores make the tiled
+// write 2-9% faster and the per-token prefill write 14% faster (decode
+// writes are unchanged); non-temporal loads make the tiled write 10-20%
+// slower and the per-token prefill write 2-5% faster.
+constexpr bool kWriteNtLoad = false;
+constexpr bool kTokenWriteNtLoad = true;
+constexpr bool kWriteNtStore = true;
+// Row-dense writes take write_flat_kernel.  When a row has at least 64
+// chunks, every lane of a wave belongs to one token and the slot is one
+// scalar load per wave instead of one vector load per lane.  Kernel traces
+// on MI355X: c4's quantizing write 5.11 against 5.45 us, c2's and c5's
+// writes unchanged (3.90 / 3.87 and 4.75 / 4.77 us).  Forcing the row loads
+// of write_flat_kernel and write_kernel ahead of the slot test with an
+// empty asm measured no gain (c2 3.90 against 3.88 us, c4 5.11 against
+// 4.86 us, c5 4.75 against 4.82 us): the compiler's order is kept.
 
 // Cache geometry with strides pre-multiplied by the cache element size.
 struct GeomBytes {
@@ -297,17 +232,6 @@ __device__ __forceinline__ void st(char *p, const Raw<B> &r) {
 }
 
 // Element i of a chunk (i is a compile-time constant after unrolling).
-// Keep a chunk's load ahead of a branch: the empty asm consumes its
-// registers, so the compiler cannot sink the load into the branch's
-// successor (where it would issue only after the branch condition's own
-// load has returned).  The load and that condition's load are then in
-// flight together.
-template <int B>
-__device__ __forceinline__ void keep_loaded(const Raw<B> &r) {
-#pragma unroll
-  for (int i = 0; i < Raw<B>::kWords; ++i) asm volatile("" ::"v"(r.w[i]));
-}
-
 template <int B>
 __device__ __forceinline__ uint32_t get8(const Raw<B> &r, int i) {
   return (r.w[i >> 2] >> ((i & 3) * 8)) & 0xFFu;
@@ -617,10 +541,6 @@ __global__ __launch_bounds__(kBlockThreads) void write_kernel(WriteArgs a) {
         if (c < a.nchunks) {
           xk[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sk + (int64_t)c * Op::kSrc);
           xv[k] = ld<Op::kSrc, kTokenWriteNtLoad>(sv + (int64_t)c * Op::kSrc);
-          if constexpr (kWriteKeepLoads) {
-            keep_loaded(xk[k]);
-            keep_loaded(xv[k]);
-          }
         }
       }
     }
@@ -699,10 +619,6 @@ __global__ __launch_bounds__(kFlatThreads) void write_flat_kernel(WriteArgs a) {
   if constexpr (Op::kScaled) {
     ks = a.ksc.p[0];
     vs = a.vsc.p[0];
-  }
-  if constexpr (kWriteKeepLoads) {
-    keep_loaded(xk);
-    keep_loaded(xv);
   }
   if (slot < 0) return;
   int64_t b, o;
@@ -1476,7 +1392,7 @@ __device__ __forceinline__ bool gather_job(const GatherArgs &a, BlockJob &j) {
 
 // Canonical-NHD gather: the valid rows of a block are one contiguous run in
 // the cache and in the output, streamed as a flat copy.  A workgroup copies
-// one power-of-two share of the block's chunks (KVX_FLAT_TILE_BYTES).
+// one power-of-two share of the block's chunks (kFlatTileBytes).
 // Copy `total` chunks of K and of V: flat index f < 2 * total, K for
 // f < total, V above, so a tile of kFlatThreads chunks per tensor gives
 // every thread one K chunk and one V chunk.
@@ -1562,8 +1478,8 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 }
 
 // Units (one 1 << split_log2 share of a block) per workgroup of
-// gather_flat_kernel, at most: 1 << KVX_FLAT_FOLD_LOG2, taken when a
-// sequence has KVX_FLAT_FOLD_MIN_UNITS to KVX_FLAT_FOLD_MAX_UNITS units.
+// gather_flat_kernel, at most: kFlatFold, taken when a sequence has
+// kFlatFoldMinUnits to kFlatFoldMaxUnits units.
 // The grid covers max_seq_len, so a decode batch's shorter sequences leave
 // workgroups that only load seq_len and exit; on MI355X such workgroups cost
 // wave launches (c2 with max_seq_len doubled at the same lengths: 1573 ->
@@ -1577,38 +1493,22 @@ __device__ __forceinline__ void flat_copy(const GatherArgs &a, const char *ck, c
 // first units first) 15-30% slower.  (Two tiles per workgroup in the flat indexed
 // and transposing gathers measured 1-10% slower than one; the RAGGED tile
 // gather takes two for long copies, below.)
-#ifndef KVX_FLAT_FOLD_LOG2
-#define KVX_FLAT_FOLD_LOG2 1
-#endif
-#ifndef KVX_FLAT_FOLD_MIN_UNITS
-#define KVX_FLAT_FOLD_MIN_UNITS 4096
-#endif
-#ifndef KVX_FLAT_FOLD_MAX_UNITS
-#define KVX_FLAT_FOLD_MAX_UNITS 65536
-#endif
-constexpr int kFlatFold = 1 << KVX_FLAT_FOLD_LOG2;
+constexpr int kFlatFoldLog2 = 1;
+constexpr int kFlatFold = 1 << kFlatFoldLog2;
+constexpr int64_t kFlatFoldMinUnits = 4096;
+constexpr int64_t kFlatFoldMaxUnits = 65536;
 // PACKED gathers of caches whose heads are contiguous runs of a power-of-two
 // number of whole 128-byte lines (HND; a power-of-two head count) in blocks
-// of at least KVX_FLAT_HEAD_RUNS_MIN_BS tokens take gather_flat_kernel with
-// head-run addressing (1) instead of the LDS tiles or the row kernel (0).
-#ifndef KVX_FLAT_HEAD_RUNS
-#define KVX_FLAT_HEAD_RUNS 1
-#endif
-#ifndef KVX_FLAT_HEAD_RUNS_MIN_BS
-#define KVX_FLAT_HEAD_RUNS_MIN_BS 64
-#endif
+// of at least kFlatHeadRunsMinBs tokens take gather_flat_kernel with
+// head-run addressing instead of the LDS tiles or the row kernel.
+constexpr int kFlatHeadRunsMinBs = 64;
 // RAGGED copies in gather_ragged_tile_kernel: two tiles per workgroup when a
-// sequence has KVX_RAGGED_FOLD_MIN_UNITS to KVX_RAGGED_FOLD_MAX_UNITS tiles
-// (0 disables).  Against one tile per workgroup (same-box A/B, medians of 6
+// sequence has kRaggedFoldMinUnits to kRaggedFoldMaxUnits tiles.  Against one tile per workgroup (same-box A/B, medians of 6
 // rounds, us per layer): c2's RAGGED gather 1563.7 -> 1528.0 (8 layers) and
 // 1468.8 -> 1448.9 (32 layers), c5's 2163.4 -> 2150.3; c4's FP8 RAGGED
 // gather (4096 tiles) measured 6.7% slower with two tiles and keeps one.
-#ifndef KVX_RAGGED_FOLD_MIN_UNITS
-#define KVX_RAGGED_FOLD_MIN_UNITS 8192
-#endif
-#ifndef KVX_RAGGED_FOLD_MAX_UNITS
-#define KVX_RAGGED_FOLD_MAX_UNITS 65536
-#endif
+constexpr int64_t kRaggedFoldMinUnits = 8192;
+constexpr int64_t kRaggedFoldMaxUnits = 65536;
 
 // A workgroup w of sequence s copies units w, w + J, ..., w + (F - 1) * J
 // (J = blocks_per_seq workgroups per sequence, F = 1 << fold_log2) that lie
@@ -2332,22 +2232,16 @@ __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, 
 // in gather_flat_kernel, and each thread resolves the source row of its own
 // chunk (threads of one row load the same table entry).
 // Threads per workgroup of gather_indexed_flat_kernel (see
-// KVX_RAGGED_COPY_THREADS).
+// kRaggedCopyThreads).
 template <class Op, int FMT>
 constexpr int indexed_flat_threads() {
-  return FMT == KVX_BLOCK_TABLE_RAGGED && !Op::kScaled ? KVX_RAGGED_COPY_THREADS
-                                                       : kBlockThreads;
+  return FMT == KVX_BLOCK_TABLE_RAGGED && !Op::kScaled ? kRaggedCopyThreads : kBlockThreads;
 }
 
 // Threads per workgroup of the KV_OFFSETS gather with per-tile table
-// entries: with KVX_OFFSETS_TILE_FIT, enough for one pass of
-// kIndexedUnroll chunks per thread over the tile's K and V chunks, a power
-// of two from kWave to kBlockThreads; otherwise kBlockThreads.
-#ifndef KVX_OFFSETS_TILE_FIT
-#define KVX_OFFSETS_TILE_FIT 1
-#endif
+// entries: enough for one pass of kIndexedUnroll chunks per thread over
+// the tile's K and V chunks, a power of two from kWave to kBlockThreads.
 inline int offsets_tile_threads(const GatherArgs &a) {
-  if (KVX_OFFSETS_TILE_FIT == 0) return kBlockThreads;
   const int64_t per_pass = 2 * (int64_t)a.rows_per_wg * a.nchunks / kIndexedUnroll;
   int t = kWave;
   while (t < kBlockThreads && t < per_pass) t *= 2;
@@ -2357,7 +2251,7 @@ inline int offsets_tile_threads(const GatherArgs &a) {
 // TILE (KV_OFFSETS only): table entries per workgroup tile, and as many
 // threads as the launch gives (at most kBlockThreads).
 template <class Op, int FMT, bool I64, bool P64,
-          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && kOffsetsTile && Op::kScaled>
+          bool TILE = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && Op::kScaled>
 __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_indexed_flat_kernel(
     GatherArgs a) {
   constexpr bool kTile = FMT == KVX_BLOCK_TABLE_KV_OFFSETS && TILE;
@@ -2614,7 +2508,7 @@ void launch_write_op(const WriteArgs &a, const WriteLaunch &w, hipStream_t s) {
                          w.tile_lds, s, a, w.wt);
   } else if (w.flat_grid > 0) {
     const dim3 g((uint32_t)w.flat_grid), b(kFlatThreads);
-    if (kWriteFlatUniformSlot && a.nchunks_log2 >= 6) {
+    if (a.nchunks_log2 >= 6) {
       if (a.slot_is64) {
         hipLaunchKernelGGL((write_flat_kernel<Op, true, true>), g, b, 0, s, a);
       } else {
@@ -2653,13 +2547,13 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
     }
   } else if constexpr (!P64) {
     if (a.format == KVX_BLOCK_TABLE_KV_OFFSETS) {
-      if (a.flat && !Op::kScaled && kOffsetsTile &&
-          ((int64_t)a.nchunks * Op::kSrc <= KVX_OFFSETS_TILE_COPY_ROW || a.nchunks_log2 < 0)) {
+      if (a.flat && !Op::kScaled &&
+          ((int64_t)a.nchunks * Op::kSrc <= kOffsetsTileCopyRow || a.nchunks_log2 < 0)) {
         hipLaunchKernelGGL(
             (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false, true>), g,
             dim3(offsets_tile_threads(a)), 0, s, a);
       } else if (a.flat) {
-        const dim3 bt(Op::kScaled && kOffsetsTile ? offsets_tile_threads(a) : kBlockThreads);
+        const dim3 bt(Op::kScaled ? offsets_tile_threads(a) : kBlockThreads);
         hipLaunchKernelGGL(
             (gather_indexed_flat_kernel<Op, KVX_BLOCK_TABLE_KV_OFFSETS, I64, false>), g, bt, 0,
             s, a);
@@ -2719,15 +2613,15 @@ void launch_tiles_dequant(int io, const TileArgs &t, int fmt, bool i64, bool p64
                           uint32_t lds, hipStream_t s) {
   switch (io) {
     case KVX_DTYPE_F32:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F32, F8>>(t, fmt, i64, p64, grid, lds,
+      launch_tiles<DequantOp<kDequantChunk, KVX_DTYPE_F32, F8>>(t, fmt, i64, p64, grid, lds,
                                                                     s);
       break;
     case KVX_DTYPE_F16:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_F16, F8>>(t, fmt, i64, p64, grid, lds,
+      launch_tiles<DequantOp<kDequantChunk, KVX_DTYPE_F16, F8>>(t, fmt, i64, p64, grid, lds,
                                                                     s);
       break;
     default:
-      launch_tiles<DequantOp<KVX_DEQUANT_CHUNK, KVX_DTYPE_BF16, F8>>(t, fmt, i64, p64, grid, lds,
+      launch_tiles<DequantOp<kDequantChunk, KVX_DTYPE_BF16, F8>>(t, fmt, i64, p64, grid, lds,
                                                                      s);
       break;
   }
