@@ -33,10 +33,13 @@ same run (c1 TinyLlama, c3 chunked prefill write, c4 FP8 E4M3 decode with a
 dequantizing gather, c5 Llama-3-70B bs32 on a ~200 GB pool), each with its
 kernels' mean / median, GB/s, fraction of peak and its own CPU baseline.
 
-stream_ceiling: plain streaming copy / read / write kernels
+stream_ceiling: plain streaming copy / read / write / widen kernels
 (libkvx_amd_probe.so, several launch shapes, the fastest reported) over the
 same byte count as the dominant kernel, on buffers beyond the 256 MB
-Infinity Cache: the best the box sustains with no index work.
+Infinity Cache: the best the box sustains with no index work (widen: the
+FP8 dequantizing gather's 8-byte loads and 16-byte stores).  For c3 also
+block_scatter / block_gather: the write's bytes copied into (and out of)
+the config's own randomly drawn pool blocks, with no slot or layout work.
 
 cpu_baseline: the CPU oracle's OpenMP fast path (row memcpy; table-driven
 casts for FP8) timed on this host's cores, threads pinned, over a bounded
@@ -432,16 +435,27 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
     elif name == "c3":
         # four rotating buffer sets (> the 256 MB Infinity Cache)
         gathers = []
+        sets = []
         for _ in range(4):
             pc, _ = cache_for(w)
             key, val = rows(w), rows(w)
             steps.append([write_launch(pc, key, val)])
+            sets.append((pc.key_cache, pc.value_cache, key, val))
             if c3_gathers:
                 # the PACKED gather of the same table back into this set's
                 # io buffers, [S, 2048, H, D]: it returns the rows just written
                 shape = (w.seq_count, w.max_seq_len, w.heads, w.head_dim)
                 gathers.append(gather_launch(pc, key.view(shape), val.view(shape)))
         extra["gathers"] = gathers
+        # the granule probe's block map: group g of bs tokens fills block
+        # slots[g * bs] / bs (chunks that start on a block boundary)
+        bs = w.block_size
+        grp = w.slots.reshape(-1, bs) if w.num_tokens % bs == 0 else None
+        if (grp is not None and c3_shift == 0 and (grp >= 0).all()
+                and (grp == grp[:, :1] + np.arange(bs)).all() and (grp[:, 0] % bs == 0).all()):
+            blk = torch.tensor(grp[:, 0] // bs, dtype=torch.int64, device=dev)
+            keep.append(blk)
+            extra["granules"] = (sets, blk)
         cfg = {"buffer_sets": 4, "block_order": c3_order}
     else:  # c5
         pc, gc = cache_for(w)
@@ -554,7 +568,7 @@ class Probe:
     """Plain copy / read / write kernels over byte counts beyond the
     Infinity Cache: the best stream of this box, beside the KV kernels."""
 
-    OPS = ("copy", "read", "write", "expand")
+    OPS = ("copy", "read", "write", "widen")
 
     def __init__(self):
         from kvx_amd import build as kbuild
@@ -566,8 +580,9 @@ class Probe:
         L.kvx_probe_copy.argtypes = [vp, vp, i64, i, vp]
         L.kvx_probe_read.argtypes = [vp, i64, vp, i, vp]
         L.kvx_probe_write.argtypes = [vp, i64, C.c_uint32, i, vp]
-        L.kvx_probe_expand.argtypes = [vp, vp, i64, i, vp]
+        L.kvx_probe_widen.argtypes = [vp, vp, i64, i, vp]
         L.kvx_probe_shape.argtypes = [i, C.POINTER(i), C.POINTER(i)]
+        L.kvx_probe_granules.argtypes = [vp, vp, i64, vp, i, i, i, vp]
         self.L = L
         self.shapes = []
         for k in range(L.kvx_probe_shapes()):
@@ -578,14 +593,17 @@ class Probe:
     def ceiling(self, nbytes, stream, reps=4, rotate_bytes=1 << 30):
         """Per op: {bytes moved per launch, GB/s of the fastest shape, that
         shape (threads, chunks per lane), mean us}.  Copy moves 2 * nbytes
-        (read + write); read and write move nbytes; expand 3 * nbytes (read
-        nbytes, write 2 * nbytes).  Launches rotate over buffer pairs
+        (read + write); read and write move nbytes; widen reads w = 2/3 of
+        nbytes (rounded to 16 bytes) as 8-byte chunks and writes each as a
+        16-byte chunk, moving 3 * w (about 2 * nbytes, the copy's bytes) in
+        the FP8 dequantizing gather's 1:2 mix.  Launches rotate over buffer pairs
         covering at least `rotate_bytes` per side, so that each one's data
         has left L2 and the Infinity Cache before it is reused; every pair
         runs at least `reps` times per (op, shape)."""
         import torch
 
         nbytes = max(16, nbytes // 16 * 16)
+        wbytes = max(16, 2 * nbytes // 3 // 16 * 16)  # widen's read bytes
         pairs = max(1, min(1024, -(-rotate_bytes // nbytes)))
         cycles = max(1, -(-reps // pairs))
         src_all = torch.empty(pairs * nbytes, dtype=torch.uint8, device="cuda").fill_(3)
@@ -605,8 +623,8 @@ class Probe:
                     if op == "read":
                         return self.L.kvx_probe_read(s.data_ptr(), nbytes, sink.data_ptr(), k,
                                                      sh)
-                    if op == "expand":
-                        return self.L.kvx_probe_expand(d.data_ptr(), s.data_ptr(), nbytes, k, sh)
+                    if op == "widen":
+                        return self.L.kvx_probe_widen(d.data_ptr(), s.data_ptr(), wbytes, k, sh)
                     return self.L.kvx_probe_write(d.data_ptr(), nbytes, 7, k, sh)
 
                 for d, s in bufs:
@@ -623,7 +641,7 @@ class Probe:
                         evs.append((e0, e1))
                 torch.cuda.synchronize()
                 ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
-                moved = {"copy": 2, "expand": 3}.get(op, 1) * nbytes
+                moved = 3 * wbytes if op == "widen" else {"copy": 2}.get(op, 1) * nbytes
                 gbps = moved / (ms / 1e3) / 1e9
                 every[f"{shape[0]}x{shape[1]}"] = round(gbps, 1)
                 if best is None or gbps > best["GBps"]:
@@ -637,6 +655,57 @@ class Probe:
         del bufs, sink, src_all, dst_all
         torch.cuda.empty_cache()
         return out
+
+    def granules(self, sets, blk, scatter, stream, reps=6):
+        """The data movement of a paged write (scatter) or gather over a
+        config's own block table and pools, with no slot, table or layout
+        work: for every buffer set (K pool, V pool, K rows, V rows), one
+        launch copies the K rows into (or out of) the pool blocks that `blk`
+        names and one the V rows; HIP events time the pair.  Granule = one
+        cache block, whose bytes the pool's block stride gives.  Fastest
+        shape: {bytes per pair, GB/s, frac, shape, mean us, by shape}."""
+        import torch
+
+        kc = sets[0][0]
+        gb = kc.stride(0) * kc.element_size()
+        if gb & (gb - 1) or gb < 16:
+            raise ValueError("granule (block bytes) must be a power of two >= 16")
+        glog = gb.bit_length() - 1
+        nbytes = blk.numel() * gb
+        for kp, vp_, kr, vr in sets:
+            if min(kr.numel() * kr.element_size(), vr.numel() * vr.element_size()) < nbytes:
+                raise ValueError("rows shorter than the mapped blocks")
+            if int(blk.max()) >= kp.shape[0] or int(blk.max()) >= vp_.shape[0]:
+                raise ValueError("block map past a pool")
+        sh = stream.cuda_stream
+        best, every = None, {}
+        for k, shape in enumerate(self.shapes):
+            def one(st):
+                for pool, rows_ in ((st[0], st[2]), (st[1], st[3])):
+                    if self.L.kvx_probe_granules(pool.data_ptr(), rows_.data_ptr(), nbytes,
+                                                 blk.data_ptr(), glog, int(scatter), k, sh):
+                        raise RuntimeError(f"granule probe shape {shape} failed")
+            for st in sets:
+                one(st)
+            evs = []
+            for _ in range(reps):
+                for st in sets:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    one(st)
+                    e1.record(stream)
+                    evs.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
+            gbps = 4 * nbytes / (ms / 1e3) / 1e9
+            every[f"{shape[0]}x{shape[1]}"] = round(gbps, 1)
+            if best is None or gbps > best["GBps"]:
+                best = {"bytes_per_launch": 4 * nbytes, "GBps": round(gbps, 1),
+                        "frac": round(gbps / PEAK_HBM_GBS, 4), "shape": list(shape),
+                        "mean_us": round(ms * 1e3, 2)}
+        best["GBps_by_shape"] = every
+        return best
 
     def pool_copy(self, pools, outs, nbytes, shape, stream, reps=3):
         """A plain copy of each layer's own K and V pools (their first
@@ -922,6 +991,10 @@ def stream_ceilings(b, nbytes, stream):
         pools, outs, n = b.extra["pool_copy"]
         ceiling["pool_copy"] = probe.pool_copy(pools, outs, n, ceiling["copy"]["shape"],
                                                stream)
+    if "granules" in b.extra:
+        sets, blk = b.extra["granules"]
+        ceiling["block_scatter"] = probe.granules(sets, blk, True, stream)
+        ceiling["block_gather"] = probe.granules(sets, blk, False, stream)
     return ceiling
 
 
@@ -1013,6 +1086,9 @@ def compact_ceiling(c):
         pc = c["pool_copy"]
         out["pool_copy"] = {"GBps": pc["GBps"], "frac": pc["frac"], "shape": pc["shape"],
                             "layer_us": [min(pc["by_layer_us"]), max(pc["by_layer_us"])]}
+    for op in ("block_scatter", "block_gather"):
+        if op in c:
+            out[op] = {"GBps": c[op]["GBps"], "frac": c[op]["frac"], "shape": c[op]["shape"]}
     return out
 
 
@@ -1033,7 +1109,8 @@ def compact_config(r):
            "roofline": {x: rf[x] for x in ("kernel", "frac", "frac_median", "traffic")}}
     if r.get("stream_ceiling"):
         out["ceiling_frac"] = {op: r["stream_ceiling"][op]["frac"]
-                               for op in ("copy", "expand", "pool_copy")
+                               for op in ("copy", "widen", "pool_copy", "block_scatter",
+                                          "block_gather")
                                if op in r["stream_ceiling"]}
     c = r.get("cpu_baseline")
     if c:

@@ -2,11 +2,17 @@
 //
 //   copy   reads n bytes and writes them elsewhere (the read/write mix of a
 //          KV write or gather, with no index work);
-//   read   reads n bytes (folded into one word per workgroup that is stored
+//   read   reads n bytes (folded into one word per lane that is stored
 //          only if it equals a value the data never produce);
 //   write  writes n bytes of a constant;
-//   expand reads n bytes and writes each 16-byte chunk twice, to 2n bytes
-//          (the 1:2 read/write mix of an FP8 -> bf16 dequantizing gather).
+//   widen  reads n bytes as 8-byte chunks and writes each as one 16-byte
+//          chunk, to 2n bytes: the access shape of the FP8 -> bf16
+//          dequantizing gather (one contiguous 16-byte store per 8-byte
+//          load, one output stream), with no conversion work;
+//   scatter  copies n contiguous bytes into granules of a pool named by a
+//          granule map (or gathers them back): the data movement of a
+//          paged KV write (or gather) over a given block table, with no
+//          slot, table or layout work.
 //
 // Each kernel is instantiated in a few launch shapes (threads per
 // workgroup x 16-byte chunks per lane, every chunk of a workgroup in flight
@@ -23,6 +29,7 @@
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int T, int U>
 __global__ __launch_bounds__(T) void copy_kernel(const u32x4 *src, u32x4 *dst, int64_t n) {
@@ -53,7 +60,7 @@ __global__ __launch_bounds__(T) void read_kernel(const u32x4 *src, int64_t n, ui
       acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
     }
   }
-  if (acc == never) sink[threadIdx.x] = acc;
+  if (acc == never) sink[threadIdx.x & 255] = acc;  // sink holds 256 words
 }
 
 template <int T, int U>
@@ -68,10 +75,11 @@ __global__ __launch_bounds__(T) void write_kernel(u32x4 *dst, int64_t n, uint32_
   }
 }
 
+// n counts 8-byte source chunks; dst holds n 16-byte chunks.
 template <int T, int U>
-__global__ __launch_bounds__(T) void expand_kernel(const u32x4 *src, u32x4 *dst, int64_t n) {
+__global__ __launch_bounds__(T) void widen_kernel(const u32x2 *src, u32x4 *dst, int64_t n) {
   const int64_t base = (int64_t)blockIdx.x * (T * U) + threadIdx.x;
-  u32x4 v[U];
+  u32x2 v[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = base + (int64_t)u * T;
@@ -81,9 +89,41 @@ __global__ __launch_bounds__(T) void expand_kernel(const u32x4 *src, u32x4 *dst,
   for (int u = 0; u < U; ++u) {
     const int64_t i = base + (int64_t)u * T;
     if (i < n) {
-      __builtin_nontemporal_store(v[u], dst + i);
-      __builtin_nontemporal_store(v[u], dst + n + i);
+      u32x4 w;
+      w[0] = v[u][0];
+      w[1] = v[u][1];
+      w[2] = v[u][0];
+      w[3] = v[u][1];
+      __builtin_nontemporal_store(w, dst + i);
     }
+  }
+}
+
+// Granule copy: 16-byte chunk i of the contiguous side is chunk
+// (map[i >> g16_log2] << g16_log2) + (i & (2^g16_log2 - 1)) of the pool
+// (g16_log2 = log2 of the granule's 16-byte chunks).  SCATTER: contiguous
+// -> pool; else pool -> contiguous.  The caller guarantees that every map
+// entry names a granule inside the pool.
+template <int T, int U, bool SCATTER>
+__global__ __launch_bounds__(T) void granule_kernel(u32x4 *pool, u32x4 *lin, const int64_t *map,
+                                                    int g16_log2, int64_t n) {
+  const int64_t base = (int64_t)blockIdx.x * (T * U) + threadIdx.x;
+  const int64_t mask = ((int64_t)1 << g16_log2) - 1;
+  u32x4 v[U];
+  int64_t at[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    at[u] = 0;
+    if (i < n) {
+      at[u] = (map[i >> g16_log2] << g16_log2) + (i & mask);
+      v[u] = __builtin_nontemporal_load(SCATTER ? lin + i : pool + at[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    if (i < n) __builtin_nontemporal_store(v[u], SCATTER ? pool + at[u] : lin + i);
   }
 }
 
@@ -118,9 +158,51 @@ void launch(int op, void *dst, const void *src, int64_t n, uint32_t value, int64
     hipLaunchKernelGGL((write_kernel<T, U>), grid, block, 0, s, static_cast<u32x4 *>(dst), n,
                        value);
   } else {
-    hipLaunchKernelGGL((expand_kernel<T, U>), grid, block, 0, s,
-                       static_cast<const u32x4 *>(src), static_cast<u32x4 *>(dst), n);
+    hipLaunchKernelGGL((widen_kernel<T, U>), grid, block, 0, s,
+                       static_cast<const u32x2 *>(src), static_cast<u32x4 *>(dst), n);
   }
+}
+
+// bytes: bytes read (copy, read, widen) or written (write).  The grid
+// covers n = bytes / 16 chunks, or bytes / 8 for widen.
+template <int T, int U>
+void launch_granule(bool scatter, void *pool, void *lin, const int64_t *map, int g16_log2,
+                    int64_t n, int64_t g, hipStream_t s) {
+  const dim3 grid((uint32_t)g), block(T);
+  if (scatter)
+    hipLaunchKernelGGL((granule_kernel<T, U, true>), grid, block, 0, s, static_cast<u32x4 *>(pool),
+                       static_cast<u32x4 *>(lin), map, g16_log2, n);
+  else
+    hipLaunchKernelGGL((granule_kernel<T, U, false>), grid, block, 0, s,
+                       static_cast<u32x4 *>(pool), static_cast<u32x4 *>(lin), map, g16_log2, n);
+}
+
+int run_granule(bool scatter, int shape, void *pool, void *lin, int64_t bytes, const int64_t *map,
+                int granule_log2, void *stream) {
+  if (shape < 0 || shape >= kNumShapes || bytes < 0 || granule_log2 < 4 || granule_log2 > 40 ||
+      bytes % ((int64_t)1 << granule_log2) != 0 || (uintptr_t)pool % 16 != 0 ||
+      (uintptr_t)lin % 16 != 0 || (uintptr_t)map % 8 != 0)
+    return 1;
+  const int64_t n = bytes / 16;
+  if (n == 0) return 0;
+  const int64_t g = grid_for(n, kShapes[shape]);
+  if (g == 0) return 1;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int g16 = granule_log2 - 4;
+  switch (shape) {
+    case 0: launch_granule<64, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 1: launch_granule<64, 4>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 2: launch_granule<128, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 3: launch_granule<128, 2>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 4: launch_granule<128, 4>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 5: launch_granule<256, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 6: launch_granule<256, 2>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 7: launch_granule<256, 4>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 8: launch_granule<512, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 9: launch_granule<512, 2>(scatter, pool, lin, map, g16, n, g, s); break;
+    default: launch_granule<1024, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 int run(int op, int shape, void *dst, const void *src, int64_t bytes, uint32_t value,
@@ -128,7 +210,7 @@ int run(int op, int shape, void *dst, const void *src, int64_t bytes, uint32_t v
   if (shape < 0 || shape >= kNumShapes || bytes < 0 || bytes % 16 != 0) return 1;
   if ((op != 1 && ((uintptr_t)dst % 16 != 0)) || (op != 2 && (uintptr_t)src % 16 != 0))
     return 1;
-  const int64_t n = bytes / 16;
+  const int64_t n = op == 3 ? bytes / 8 : bytes / 16;
   if (n == 0) return 0;
   const int64_t g = grid_for(n, kShapes[shape]);
   if (g == 0) return 1;
@@ -170,7 +252,8 @@ int kvx_probe_copy(void *dst, const void *src, int64_t bytes, int shape, void *s
   return run(0, shape, dst, src, bytes, 0, stream);
 }
 
-// sink: 1024 bytes of device memory, written only in the never-taken case.
+// sink: at least 1024 bytes of device memory, written only in the
+// never-taken case (one of its 256 words per lane).
 int kvx_probe_read(const void *src, int64_t bytes, void *sink, int shape, void *stream) {
   return run(1, shape, sink, src, bytes, 0x9E3779B9u, stream);
 }
@@ -179,9 +262,19 @@ int kvx_probe_write(void *dst, int64_t bytes, uint32_t value, int shape, void *s
   return run(2, shape, dst, nullptr, bytes, value, stream);
 }
 
-// dst: 2 * bytes of device memory.
-int kvx_probe_expand(void *dst, const void *src, int64_t bytes, int shape, void *stream) {
+// Reads `bytes` (a multiple of 16) from src, writes 2 * bytes to dst.
+int kvx_probe_widen(void *dst, const void *src, int64_t bytes, int shape, void *stream) {
   return run(3, shape, dst, src, bytes, 0, stream);
+}
+
+// Copies `bytes` (a multiple of the granule, 2^granule_log2 bytes, at
+// least 16) between the contiguous buffer lin and the granules of pool
+// that map (bytes >> granule_log2 int64 entries, device memory) names:
+// lin -> pool when scatter is nonzero, pool -> lin otherwise.  Every map
+// entry must name a granule inside the pool; it is not checked.
+int kvx_probe_granules(void *pool, void *lin, int64_t bytes, const int64_t *map,
+                       int granule_log2, int scatter, int shape, void *stream) {
+  return run_granule(scatter != 0, shape, pool, lin, bytes, map, granule_log2, stream);
 }
 
 }  // extern "C"

@@ -131,3 +131,86 @@ def test_c3_block_size_keeps_chunks():
     assert len(set(b.slots.tolist())) == b.slots.size and (b.slots // 128 < 1024).all()
     with pytest.raises(ValueError):
         W.c3_llama8b_prefill(block_size=24)
+
+
+@pytest.mark.gpu
+def test_probe_kernels_move_the_right_bytes():
+    """Every launch shape of the streaming probes: copy reproduces its
+    source, write fills its range with the value, widen stores each 8-byte
+    source chunk twice in one 16-byte chunk, read leaves its sink untouched
+    (the sink word is written only for a sentinel the data never produce);
+    bytes past each range stay as they were."""
+    import torch
+
+    from kvx_amd import build as kbuild
+
+    if not kbuild.PROBE_LIB.exists():
+        pytest.skip("libkvx_amd_probe.so is not built")
+    p = bench.Probe()
+    n = 3 * 4096 + 48  # not a multiple of any workgroup's chunks
+    g = torch.Generator().manual_seed(5)
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, generator=g).cuda()
+    sh = torch.cuda.current_stream().cuda_stream
+    for k, shape in enumerate(p.shapes):
+        dst = torch.full((2 * n + 64,), 0xAB, dtype=torch.uint8, device="cuda")
+        assert p.L.kvx_probe_copy(dst.data_ptr(), src.data_ptr(), n, k, sh) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(dst[:n], src), shape
+        assert bool((dst[n:] == 0xAB).all()), shape
+
+        dst.fill_(0xAB)
+        assert p.L.kvx_probe_widen(dst.data_ptr(), src.data_ptr(), n, k, sh) == 0
+        torch.cuda.synchronize()
+        pairs = src.view(-1, 8)
+        assert torch.equal(dst[:2 * n].view(-1, 16), torch.cat([pairs, pairs], dim=1)), shape
+        assert bool((dst[2 * n:] == 0xAB).all()), shape
+
+        dst.fill_(0xAB)
+        assert p.L.kvx_probe_write(dst.data_ptr(), n, 0x01020304, k, sh) == 0
+        torch.cuda.synchronize()
+        want = torch.tensor([4, 3, 2, 1], dtype=torch.uint8, device="cuda").repeat(n // 4)
+        assert torch.equal(dst[:n], want) and bool((dst[n:] == 0xAB).all()), shape
+
+        sink = torch.full((1024,), 0x5A, dtype=torch.uint8, device="cuda")
+        assert p.L.kvx_probe_read(src.data_ptr(), n, sink.data_ptr(), k, sh) == 0
+        torch.cuda.synchronize()
+        assert bool((sink == 0x5A).all()), shape
+    # sizes that are not a multiple of 16 bytes are refused
+    assert p.L.kvx_probe_widen(dst.data_ptr(), src.data_ptr(), 24, 0, sh) == 1
+
+
+@pytest.mark.gpu
+def test_granule_probe_moves_the_mapped_blocks():
+    """kvx_probe_granules in every shape: scatter puts granule g of the
+    contiguous rows into pool granule map[g] and leaves the other pool
+    granules as they were; gather brings them back; sizes that are not a
+    whole number of granules are refused."""
+    import torch
+
+    from kvx_amd import build as kbuild
+
+    if not kbuild.PROBE_LIB.exists():
+        pytest.skip("libkvx_amd_probe.so is not built")
+    p = bench.Probe()
+    glog, ng, npool = 10, 24, 64  # 1 KiB granules, 24 of a 64-granule pool
+    gb = 1 << glog
+    g = torch.Generator().manual_seed(9)
+    blk = torch.randperm(npool, generator=g)[:ng].to(torch.int64)
+    rows = torch.randint(0, 256, (ng * gb,), dtype=torch.uint8, generator=g)
+    sh = torch.cuda.current_stream().cuda_stream
+    for k, shape in enumerate(p.shapes):
+        pool = torch.full((npool * gb,), 0xCD, dtype=torch.uint8, device="cuda")
+        lin, m = rows.cuda(), blk.cuda()
+        assert p.L.kvx_probe_granules(pool.data_ptr(), lin.data_ptr(), ng * gb, m.data_ptr(),
+                                      glog, 1, k, sh) == 0
+        torch.cuda.synchronize()
+        want = torch.full((npool, gb), 0xCD, dtype=torch.uint8)
+        want[blk] = rows.view(ng, gb)
+        assert torch.equal(pool.cpu().view(npool, gb), want), shape
+        back = torch.zeros_like(lin)
+        assert p.L.kvx_probe_granules(pool.data_ptr(), back.data_ptr(), ng * gb, m.data_ptr(),
+                                      glog, 0, k, sh) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(back.cpu(), rows), shape
+    assert p.L.kvx_probe_granules(pool.data_ptr(), lin.data_ptr(), gb + 16, m.data_ptr(), glog,
+                                  1, 0, sh) == 1
