@@ -1497,6 +1497,19 @@ constexpr int kFlatFoldLog2 = 1;
 constexpr int kFlatFold = 1 << kFlatFoldLog2;
 constexpr int64_t kFlatFoldMinUnits = 4096;
 constexpr int64_t kFlatFoldMaxUnits = 65536;
+// Sequences of at least kFlatLongUnits units (long contexts: Llama-3-70B's
+// 16K-32K tokens in 32-token blocks give 32768) launch gather_flat_kernel
+// with kFlatLongLds bytes of dynamic LDS, which the kernel does not use:
+// it holds a CU to 12 of its 128-thread workgroups (12 * 12800 bytes fit
+// the 160 KiB of LDS, 13 do not, at any allocation granule up to 1 KiB)
+// instead of 16.  Same-process A/B on MI355X, us per gather, 16 -> 12
+// workgroups: c5 2341 -> 2149, 2000 -> 1983 and 2061 -> 2037 on three
+// boxes; c5's lengths over pools of 100000 / 200000 / 400000 blocks 2126 ->
+// 2053, 2154 -> 2066, 2146 -> 2062.  Shorter sequences lose: c2 (8192
+// units) 1438 -> 1464, c2's lengths in 32-token blocks 1450 -> 1467, c4
+// (4096 units) 578 -> 589; 8 workgroups cost c2 9% and c4 16%.
+constexpr int64_t kFlatLongUnits = 16384;
+constexpr uint32_t kFlatLongLds = 12800;
 // PACKED gathers of caches whose heads are contiguous runs of a power-of-two
 // number of whole 128-byte lines (HND; a power-of-two head count) in blocks
 // of at least kFlatHeadRunsMinBs tokens take gather_flat_kernel with
@@ -2562,10 +2575,12 @@ void launch_gather_typed(const GatherArgs &a, int64_t grid, hipStream_t s) {
                            g, b, 0, s, a);
       }
     } else if (a.flat) {
+      const uint32_t lds = a.units_per_seq >= kFlatLongUnits ? kFlatLongLds : 0;
       if (a.cph_log2 >= 0)
-        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, true>), g, dim3(kFlatThreads), 0, s, a);
+        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, true>), g, dim3(kFlatThreads), lds, s, a);
       else
-        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, false>), g, dim3(kFlatThreads), 0, s, a);
+        hipLaunchKernelGGL((gather_flat_kernel<Op, I64, false>), g, dim3(kFlatThreads), lds, s,
+                           a);
     } else {
       hipLaunchKernelGGL((gather_rows_kernel<Op, I64>), g, b, 0, s, a);
     }

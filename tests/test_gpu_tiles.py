@@ -506,3 +506,35 @@ def test_tiles_write_row_major_ownership(seed):
     entry = "abi" if ko_ == vo_ and seed % 2 == 0 else "launch"  # seeds 4 and 14
     check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=dt,
                 entry=entry, **scales)
+
+
+@pytest.mark.parametrize("layouts", [("bhpox", 8, "bhdo", None),   # vLLM's pair
+                                     ("bhdo", None, "bhpox", 8),   # the pair swapped
+                                     ("bhpox", 8, "bhpox", 8),     # x-packed K and V
+                                     ("bhod", None, "bhdo", None)],  # HND / token-innermost
+                         ids=["vllm", "swapped", "xpacked", "hnd-tokinner"])
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F8_E4M3, DType.F32])
+def test_tiles_decode_write_mixed_layouts(layouts, dt):
+    """A decode batch (one new token per sequence, each in a block of its
+    own, at any offset; some slots -1 or past the pool) into K / V pairs of
+    different piece sizes (16-byte x-packed or HND pieces beside one-element
+    token-innermost ones): write_tiles_kernel's groups fill no block, so
+    every token goes through its per-token fallback."""
+    ko_, kx, vo_, vx = layouts
+    gen = torch.Generator().manual_seed(520 + int(dt) * 8 + ["bhpox", "bhdo", "bhod"].index(ko_))
+    H, D, bs, nb, T = 8, 128, 16, 96, 70
+    pc, kb, vb = custom_cache(dt, nb, bs, H, D, ko_, vo_, kx, vx, gen)
+    blocks = torch.randperm(nb, generator=gen)[:T]
+    offs = torch.randint(0, bs, (T,), generator=gen)
+    slots = blocks * bs + offs
+    slots[torch.randperm(T, generator=gen)[:4]] = -1
+    slots[7] = nb * bs + 3  # block == num_blocks: skipped
+    io = DType.BF16 if dt == DType.F8_E4M3 else dt
+    if dt == DType.F8_E4M3:
+        key = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+        val = (torch.randn((T, H, D), generator=gen) * 3).to(TORCH_DT[io]).to(DEV)
+    else:
+        key = random_fill(torch.empty((T, H, D), dtype=TORCH_DT[io], device=DEV), gen)
+        val = random_fill(torch.empty_like(key), gen)
+    scales = dict(k_scale=0.013, v_scale=0.007) if dt == DType.F8_E4M3 else {}
+    check_write(pc, kb, vb, key, val, slots.to(DEV), io_dtype=io, cache_dtype=dt, **scales)
