@@ -45,10 +45,12 @@
  *               block; the block's address is pool + index * bytes_per_block.
  *               An entry is skipped when its index is >= num_blocks or its
  *               pool is NULL.  kvx_pool_desc_t carries no pool sizes, so
- *               BOTH pools must hold at least num_blocks blocks of
- *               bytes_per_block bytes: a smaller secondary pool (an offload
+ *               through kvx_launch_gather_kv, kvx_launch_gather_kv_dequant and
+ *               kvx_gather_kv BOTH pools must hold at least num_blocks blocks
+ *               of bytes_per_block bytes: a smaller secondary pool (an offload
  *               pool, say) is read out of bounds by indices between its size
- *               and num_blocks.
+ *               and num_blocks.  kvx_launch_gather_kv_pools below takes each
+ *               pool's block count and skips the entries past it.
  */
 #ifndef KVX_EXT_H
 #define KVX_EXT_H
@@ -70,6 +72,32 @@ KVX_API kvx_status_t kvx_launch_gather_kv_dequant(
     const kvx_cache_desc_t *cache, const kvx_gather_desc_t *gather,
     const kvx_scale_desc_t *k_scale, const kvx_scale_desc_t *v_scale,
     void *stream);
+
+/* Block counts of the two pools of a KV_OFFSETS table (kvx_pool_desc_t,
+ * reference kvx_abi.h:84-90, has none).  A count of 0, or one of
+ * num_blocks or more, means num_blocks. */
+typedef struct kvx_pool_blocks_t {
+  uint32_t size; /* sizeof(kvx_pool_blocks_t) */
+  uint32_t reserved;
+  int64_t primary;   /* blocks in cache->pool.primary */
+  int64_t secondary; /* blocks in cache->pool.secondary */
+} kvx_pool_blocks_t;
+
+/* kvx_launch_gather_kv (k_scale and v_scale NULL) or
+ * kvx_launch_gather_kv_dequant (both non-NULL), with a KV_OFFSETS entry also
+ * skipped when its index is at or past its pool's count in pool_blocks, so
+ * that a secondary pool smaller than num_blocks is never read past its end.
+ * pool_blocks may be NULL (no narrowing); it is not read for PACKED and
+ * RAGGED tables.  KVX_STATUS_INVALID_ARGUMENT for a pool_blocks->size below
+ * sizeof(kvx_pool_blocks_t), a negative count, or one scale descriptor
+ * without the other; otherwise the same validation order and codes as the
+ * gather it stands for.  No reference counterpart: an extension for callers
+ * whose KV_OFFSETS pools differ in size (an offload pool beside the
+ * primary one). */
+KVX_API kvx_status_t kvx_launch_gather_kv_pools(
+    const kvx_cache_desc_t *cache, const kvx_gather_desc_t *gather,
+    const kvx_pool_blocks_t *pool_blocks, const kvx_scale_desc_t *k_scale,
+    const kvx_scale_desc_t *v_scale, void *stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

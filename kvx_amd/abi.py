@@ -142,6 +142,11 @@ class ScaleDesc(C.Structure):
                 ("data", C.c_void_p)]
 
 
+class PoolBlocks(C.Structure):  # kvx_ext.h: kvx_pool_blocks_t (no reference counterpart)
+    _fields_ = [("size", C.c_uint32), ("reserved", C.c_uint32), ("primary", C.c_int64),
+                ("secondary", C.c_int64)]
+
+
 class WriteDesc(C.Structure):
     _fields_ = [("size", C.c_uint32), ("io", KvIoDesc), ("slots", SlotMapping),
                 ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
@@ -165,6 +170,8 @@ _SIGS = {
     "kvx_launch_gather_kv": [_P(CacheDesc), _P(GatherDesc), C.c_void_p],
     "kvx_launch_gather_kv_dequant": [_P(CacheDesc), _P(GatherDesc), _P(ScaleDesc),
                                      _P(ScaleDesc), C.c_void_p],
+    "kvx_launch_gather_kv_pools": [_P(CacheDesc), _P(GatherDesc), _P(PoolBlocks), _P(ScaleDesc),
+                                   _P(ScaleDesc), C.c_void_p],
 }
 for _t in ("f32", "f16", "bf16"):
     _SIGS[f"kvx_launch_write_kv_{_t}"] = [_P(CacheDesc), _P(WriteDesc), C.c_void_p]

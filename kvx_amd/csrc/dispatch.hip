@@ -262,6 +262,8 @@ bool plan_tiles(const GatherPlan &p, int cs, int is, int src_chunk, TileArgs *t,
   t->pool[0] = p.pool[0];
   t->pool[1] = p.pool[1];
   t->bytes_per_block = p.bytes_per_block;
+  t->pool_blocks[0] = p.pool_blocks[0];
+  t->pool_blocks[1] = p.pool_blocks[1];
   t->out_row_bytes = H * D * is;
   t->max_blocks_per_seq = p.max_blocks_per_seq;
   const int64_t by_len = ((int64_t)p.max_seq_len + bs - 1) / bs;
@@ -582,6 +584,8 @@ kvx_status_t enqueue_gather(const GatherPlan &p, void *stream) {
   a.pool[0] = p.pool[0];
   a.pool[1] = p.pool[1];
   a.bytes_per_block = p.bytes_per_block;
+  a.pool_blocks[0] = p.pool_blocks[0];
+  a.pool_blocks[1] = p.pool_blocks[1];
   a.format = p.format;
   a.rows_per_wg = 0;
   a.ragged_tile = 0;

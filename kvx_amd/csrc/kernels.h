@@ -1305,6 +1305,7 @@ struct GatherArgs {
   int64_t table_count;       // RAGGED: entries of `table`
   const char *pool[2];       // KV_OFFSETS primary / secondary
   int64_t bytes_per_block;   // KV_OFFSETS
+  int32_t pool_blocks[2];    // KV_OFFSETS: entries of pool i at or past pool_blocks[i] are skipped
   GeomBytes gk;
   GeomBytes gv;
   int64_t out_row_bytes;  // bytes of one output row (H * D * io size)
@@ -1700,6 +1701,7 @@ struct TileArgs {
   int64_t table_count;      // RAGGED: entries of `table`
   const char *pool[2];      // KV_OFFSETS primary / secondary
   int64_t bytes_per_block;  // KV_OFFSETS
+  int32_t pool_blocks[2];   // KV_OFFSETS: entries of pool i at or past pool_blocks[i] are skipped
   int64_t out_row_bytes;
   int32_t max_blocks_per_seq;
   int32_t blocks_per_seq;
@@ -1983,7 +1985,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
           a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
       const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
       bid = ent & 0x7FFFFFFFu;
-      if (pool == nullptr || bid >= a.num_blocks) return;
+      if (pool == nullptr || bid >= a.pool_blocks[ent >> 31]) return;
       blk = pool + bid * a.bytes_per_block;
     } else {
       bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
@@ -2176,8 +2178,10 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
       const char *vp = a.pool[vidx >> 31];
       const int64_t kb = kidx & 0x7FFFFFFFu;
       const int64_t vb = vidx & 0x7FFFFFFFu;
-      if (kp != nullptr && kb < a.num_blocks) rk = kp + kb * a.bytes_per_block + o * a.gk.s_off;
-      if (vp != nullptr && vb < a.num_blocks) rv = vp + vb * a.bytes_per_block + o * a.gv.s_off;
+      if (kp != nullptr && kb < a.pool_blocks[kidx >> 31])
+        rk = kp + kb * a.bytes_per_block + o * a.gk.s_off;
+      if (vp != nullptr && vb < a.pool_blocks[vidx >> 31])
+        rv = vp + vb * a.bytes_per_block + o * a.gv.s_off;
     }
     char *wk = a.dst_k + (s * a.max_seq_len + t) * a.out_row_bytes;
     char *wv = a.dst_v + (s * a.max_seq_len + t) * a.out_row_bytes;
@@ -2234,7 +2238,7 @@ __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, 
         a.table)[(s * 2 + (v ? 1 : 0)) * (int64_t)a.max_blocks_per_seq + lb];
     const char *pool = a.pool[e >> 31];
     const int64_t idx = e & 0x7FFFFFFFu;
-    if (pool == nullptr || idx >= a.num_blocks) return nullptr;
+    if (pool == nullptr || idx >= a.pool_blocks[e >> 31]) return nullptr;
     return pool + idx * a.bytes_per_block + (int64_t)o * g.s_off;
   }
 }
@@ -2294,8 +2298,10 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
     const char *pv = (ev >> 31) ? a.pool[1] : a.pool[0];
     const int64_t kb = ek & 0x7FFFFFFFu;
     const int64_t vb = ev & 0x7FFFFFFFu;
-    if (pk != nullptr && kb < a.num_blocks) tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
-    if (pv != nullptr && vb < a.num_blocks) tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
+    if (pk != nullptr && kb < a.pool_blocks[ek >> 31])
+      tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
+    if (pv != nullptr && vb < a.pool_blocks[ev >> 31])
+      tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
     if (tk == nullptr && tv == nullptr) return;
   }
   const int64_t rem = n - t0;

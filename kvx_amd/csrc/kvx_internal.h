@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "kvx_abi.h"
+#include "kvx_ext.h"
 
 namespace kvx {
 
@@ -82,6 +83,8 @@ struct GatherPlan {
   int64_t table_count;      // entries of block_table
   const char *pool[2];      // KV_OFFSETS: primary / secondary pool bases
   int64_t bytes_per_block;  // KV_OFFSETS
+  int32_t pool_blocks[2];   // KV_OFFSETS: blocks of each pool (<= num_blocks); entries
+                            // at or past their pool's count are skipped
   Geom gk;
   Geom gv;
   int32_t format;      // kvx_block_table_format_t
@@ -110,7 +113,9 @@ kvx_status_t enqueue_gather(const GatherPlan &plan, void *stream);
 
 // Shared launch-path implementations behind the exported entry points.
 // `expected` is the dtype the per-dtype helper requires of cache and io
-// (KVX_DTYPE_INVALID = any dtype the dispatcher accepts).
+// (KVX_DTYPE_INVALID = any dtype the dispatcher accepts).  `pools`
+// (kvx_launch_gather_kv_pools only, else NULL): block counts that narrow a
+// KV_OFFSETS table's pools below num_blocks, already checked by the caller.
 kvx_status_t launch_write(const kvx_cache_desc_t *cache,
                           const kvx_write_desc_t *write, int32_t tokens_per_seq,
                           bool prefill, kvx_dtype_t expected, void *stream);
@@ -118,6 +123,7 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
                            const kvx_gather_desc_t *gather,
                            const kvx_scale_desc_t *k_scale,
                            const kvx_scale_desc_t *v_scale, bool dequant,
-                           kvx_dtype_t expected, void *stream);
+                           kvx_dtype_t expected, void *stream,
+                           const kvx_pool_blocks_t *pools = nullptr);
 
 }  // namespace kvx

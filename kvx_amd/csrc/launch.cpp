@@ -276,7 +276,8 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
                            const kvx_gather_desc_t *gather,
                            const kvx_scale_desc_t *k_scale,
                            const kvx_scale_desc_t *v_scale, bool dequant,
-                           kvx_dtype_t expected, void *stream) {
+                           kvx_dtype_t expected, void *stream,
+                           const kvx_pool_blocks_t *pools) {
   if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
   if (dequant && (k_scale == nullptr || v_scale == nullptr))
     return KVX_STATUS_INVALID_ARGUMENT;
@@ -395,6 +396,10 @@ kvx_status_t launch_gather(const kvx_cache_desc_t *cache,
   p.pool[0] = static_cast<const char *>(cache->pool.primary);
   p.pool[1] = static_cast<const char *>(cache->pool.secondary);
   p.bytes_per_block = cache->pool.bytes_per_block;
+  const int64_t nb = cache->num_blocks;
+  const int64_t counts[2] = {pools ? pools->primary : 0, pools ? pools->secondary : 0};
+  for (int i = 0; i < 2; ++i)
+    p.pool_blocks[i] = (int32_t)(counts[i] > 0 && counts[i] < nb ? counts[i] : nb);
   p.seq_count = seq_count;
   p.max_blocks_per_seq = (int32_t)gather->block_table.max_blocks_per_seq;
   p.max_seq_len = max_seq_len;
@@ -539,6 +544,42 @@ KVX_API kvx_status_t kvx_launch_gather_kv_dequant(
   if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
   if (!kvx::is_fp8(cache->k.dtype)) return KVX_STATUS_UNSUPPORTED;
   return launch_gather(cache, gather, k_scale, v_scale, true, cache->k.dtype, stream);
+}
+
+// kvx_ext.h's own struct (no reference counterpart), LP64.
+static_assert(sizeof(kvx_pool_blocks_t) == 24, "abi");
+static_assert(offsetof(kvx_pool_blocks_t, primary) == 8, "abi");
+static_assert(offsetof(kvx_pool_blocks_t, secondary) == 16, "abi");
+
+KVX_API kvx_status_t kvx_launch_gather_kv_pools(const kvx_cache_desc_t *cache,
+                                                const kvx_gather_desc_t *gather,
+                                                const kvx_pool_blocks_t *pool_blocks,
+                                                const kvx_scale_desc_t *k_scale,
+                                                const kvx_scale_desc_t *v_scale,
+                                                void *stream) {
+  if (cache == nullptr || gather == nullptr) return KVX_STATUS_INVALID_ARGUMENT;
+  if (pool_blocks != nullptr &&
+      (pool_blocks->size < sizeof(kvx_pool_blocks_t) || pool_blocks->primary < 0 ||
+       pool_blocks->secondary < 0))
+    return KVX_STATUS_INVALID_ARGUMENT;
+  if ((k_scale == nullptr) != (v_scale == nullptr)) return KVX_STATUS_INVALID_ARGUMENT;
+  if (cache->k.dtype != cache->v.dtype) return KVX_STATUS_INVALID_ARGUMENT;
+  if (k_scale != nullptr) {
+    if (!kvx::is_fp8(cache->k.dtype)) return KVX_STATUS_UNSUPPORTED;
+    return launch_gather(cache, gather, k_scale, v_scale, true, cache->k.dtype, stream,
+                         pool_blocks);
+  }
+  switch (cache->k.dtype) {
+    case KVX_DTYPE_F16:
+    case KVX_DTYPE_BF16:
+    case KVX_DTYPE_F32:
+    case KVX_DTYPE_F8_E4M3:
+    case KVX_DTYPE_F8_E5M2:
+      return launch_gather(cache, gather, nullptr, nullptr, false, cache->k.dtype, stream,
+                           pool_blocks);
+    default:
+      return KVX_STATUS_UNSUPPORTED;
+  }
 }
 
 }  // extern "C"

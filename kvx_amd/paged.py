@@ -337,18 +337,27 @@ def write_kv(cache: PagedCache, key: torch.Tensor, value: torch.Tensor,
 def gather_kv(cache: PagedCache, key_out: torch.Tensor, value_out: torch.Tensor,
               block_table, seq_lens: torch.Tensor, max_seq_len: int, *,
               k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
-              stream=None, entry: str = "launch") -> Status:
+              stream=None, entry: str = "launch",
+              pool_blocks: tuple[int, int] | None = None) -> Status:
     """Gather sequences into contiguous [S, max_seq_len, H, D] buffers.
     `block_table` is a PACKED [S, max_blocks_per_seq] tensor, a RaggedTable
     or an OffsetsTable (whose pool replaces the cache tensors' data).
     With k_scale/v_scale the FP8 cache is dequantized
-    (kvx_launch_gather_kv_dequant)."""
+    (kvx_launch_gather_kv_dequant).  pool_blocks = (primary, secondary)
+    block counts go through kvx_launch_gather_kv_pools instead."""
     lib = abi.load()
     cd = gather_cache_desc(cache, block_table)
     gd = build_gather(key_out, value_out, block_table, seq_lens, max_seq_len)
     s = _stream_handle(stream)
     if entry == "abi":
         return Status(lib.kvx_gather_kv(C.byref(cd), C.byref(gd), s))
+    if pool_blocks is not None:
+        pb = abi.PoolBlocks(C.sizeof(abi.PoolBlocks), 0, pool_blocks[0], pool_blocks[1])
+        ks = vs = None
+        if k_scale is not None or v_scale is not None:
+            ks, vs = C.byref(scale_desc_of(k_scale)), C.byref(scale_desc_of(v_scale))
+        return Status(lib.kvx_launch_gather_kv_pools(C.byref(cd), C.byref(gd), C.byref(pb), ks,
+                                                     vs, s))
     if k_scale is not None or v_scale is not None:
         ks = scale_desc_of(k_scale)
         vs = scale_desc_of(v_scale)

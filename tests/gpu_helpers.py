@@ -240,22 +240,40 @@ class OffsetsPool:
         return paged.OffsetsTable(offsets, self.primary, self.secondary, self.bytes_per_block)
 
 
+def bound_offsets(offsets: np.ndarray, num_blocks: int, pool_blocks) -> np.ndarray:
+    """The KV_OFFSETS table that kvx_launch_gather_kv_pools gathers like:
+    an int32 KVCacheIndex entry whose index is at or past its pool's count
+    (0 or >= num_blocks: num_blocks) becomes an index past every pool, which
+    the gather skips as it skips indices >= num_blocks."""
+    u = offsets.view(np.uint32)
+    sec = (u >> 31).astype(bool)
+    idx = (u & 0x7FFFFFFF).astype(np.int64)
+    lim = [c if 0 < c < num_blocks else num_blocks for c in pool_blocks]
+    cut = np.where(sec, idx >= lim[1], idx >= lim[0])
+    return np.where(cut, np.uint32(0x7FFFFFFF), u).astype(np.uint32).view(np.int32)
+
+
 def check_gather_offsets(pool: OffsetsPool, key_out, value_out, offsets, lens, max_seq_len,
                          *, cache_dtype, io_dtype, k_scale=None, v_scale=None,
-                         entry="launch"):
+                         entry="launch", pool_blocks=None):
     """KV_OFFSETS-table gather on the GPU and in the oracle; bit-identical
-    outputs."""
+    outputs.  pool_blocks = (primary, secondary): the GPU takes
+    kvx_launch_gather_kv_pools, the oracle the table with the entries past
+    each pool's count skipped (bound_offsets)."""
     pc = pool.pc
     ko0, vo0 = np_bytes(key_out), np_bytes(value_out)
     ks, k_or = _dev_scale(k_scale, key_out.device)
     vs, v_or = _dev_scale(v_scale, key_out.device)
     st = paged.gather_kv(pc, key_out, value_out, pool.table(offsets), lens, max_seq_len,
-                         k_scale=ks, v_scale=vs, entry=entry)
+                         k_scale=ks, v_scale=vs, entry=entry, pool_blocks=pool_blocks)
     assert st == Status.OK, st
     torch.cuda.synchronize()
     sec = None if pool.secondary is None else np_bytes(pool.secondary)
+    table = offsets.cpu().numpy()
+    if pool_blocks is not None:
+        table = bound_offsets(table, pc.num_blocks, pool_blocks)
     oracle.gather_kv_offsets(pool.geoms[0], pool.geoms[1], np_bytes(pool.primary), sec,
-                             pool.bytes_per_block, ko0, vo0, offsets.cpu().numpy(),
+                             pool.bytes_per_block, ko0, vo0, table,
                              lens.cpu().numpy(), max_blocks_per_seq=offsets.shape[3],
                              max_seq_len=max_seq_len, heads=pc.heads, head_dim=pc.head_dim,
                              block_size=pc.block_size, num_blocks=pc.num_blocks,

@@ -16,6 +16,7 @@ SIZES = {
     abi.Version: 16, abi.TensorDesc: 112, abi.PoolDesc: 32, abi.CacheDesc: 280,
     abi.BlockTable: 64, abi.SlotMapping: 32, abi.SeqLens: 24, abi.KvIoDesc: 248,
     abi.ScaleDesc: 104, abi.WriteDesc: 512, abi.GatherDesc: 352,
+    abi.PoolBlocks: 24,  # kvx_ext.h
 }
 
 OFFSETS = [
@@ -25,6 +26,7 @@ OFFSETS = [
     (abi.GatherDesc, "seq_lens", 320), (abi.GatherDesc, "max_seq_len", 344),
     (abi.TensorDesc, "shape", 24), (abi.TensorDesc, "stride", 64),
     (abi.TensorDesc, "data", 104),
+    (abi.PoolBlocks, "primary", 8), (abi.PoolBlocks, "secondary", 16),
 ]
 
 

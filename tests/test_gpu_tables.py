@@ -281,6 +281,39 @@ def test_kv_offsets_abi_entry(dt):
                              entry="abi")
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_kv_offsets_pool_blocks(seed):
+    """kvx_launch_gather_kv_pools: entries at or past their pool's block
+    count are skipped.  Both pools are allocated with num_blocks blocks, so
+    an entry the kernel should skip but reads would show up as gathered
+    bytes, not as an access outside the buffers.  Layouts, dtypes, FP8
+    dequantizing gathers, narrow rows (per-tile table entries) and counts of
+    0, 1, below and above num_blocks."""
+    rng = np.random.default_rng(7000 + seed)
+    gen = torch.Generator().manual_seed(700 + seed)
+    dt = [DType.BF16, DType.F16, DType.F32, DType.F8_E4M3][seed % 4]
+    kl, vl = LAYOUTS[seed % 3], LAYOUTS[(seed // 3) % 3]
+    H = [1, 2, 8][seed % 3]
+    D = [64, 128, 32][(seed // 2) % 3]
+    bs = [16, 4, 32, 1][(seed // 4) % 4]
+    nb = int(rng.integers(12, 40))
+    pool = OffsetsPool(kl, vl, dt, nb, bs, H, D, pitch_pad=[0, 64][seed % 2], gen=gen)
+    S, L = int(rng.integers(2, 6)), int(rng.integers(bs, 200))
+    mbps = (L + bs - 1) // bs
+    offsets = offsets_table(rng, S, mbps, nb, secondary_frac=0.5)
+    lens = lens_tensor(rng, S, L, [np.int32, np.int64][seed % 2])
+    counts = [(0, nb // 3), (nb // 2, 0), (nb - 1, 1), (nb + 5, 2)][seed % 4]
+    if dt == DType.F8_E4M3:
+        io = [DType.BF16, DType.F16, DType.F32][seed % 3]
+        ko, vo = out_pair(S, L, H, D, io, gen)
+        check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=io,
+                             k_scale=0.031, v_scale=1.25, pool_blocks=counts)
+    else:
+        ko, vo = out_pair(S, L, H, D, dt, gen)
+        check_gather_offsets(pool, ko, vo, offsets, lens, L, cache_dtype=dt, io_dtype=dt,
+                             pool_blocks=counts)
+
+
 def test_kv_offsets_trtllm_pairs():
     """TensorRT-LLM's pairing: the V block of a K block is the next pool
     block; all tokens of every sequence valid, no secondary pool."""

@@ -452,3 +452,50 @@ def test_gather_grid_past_hip_limits(kvx_lib):
     # gather_ragged_tile_kernel, 128 threads, 16 rows per workgroup
     assert G(kvx_lib, *big_gather(Layout.BLOCK_NHD, 8192, 65536, 1, 8, 16,
                                   fmt="ragged")) == UNS
+
+
+def test_pool_blocks_gather_validation(kvx_lib):
+    """kvx_launch_gather_kv_pools (kvx_ext.h): its own argument checks come
+    first (NULL cache / gather, a short or negative kvx_pool_blocks_t, one
+    scale descriptor without the other); then it is the copy gather (no
+    scales) or the dequantizing gather (both), with their codes; empty
+    batches return OK without a launch."""
+    f = kvx_lib.kvx_launch_gather_kv_pools
+    ks, vs = abi.scale_desc(FAKE), abi.scale_desc(FAKE)
+
+    def pb(primary=0, secondary=0, size=None):
+        return abi.PoolBlocks(C.sizeof(abi.PoolBlocks) if size is None else size, 0, primary,
+                              secondary)
+
+    def call(c, g, p=None, k=None, v=None):
+        return Status(f(abi.ref(c) if c is not None else None, abi.ref(g) if g is not None else None,
+                        abi.ref(p) if p is not None else None, abi.ref(k) if k is not None else None,
+                        abi.ref(v) if v is not None else None, None))
+
+    assert C.sizeof(abi.PoolBlocks) == 24
+    c, g = offsets_gather(L=0)
+    assert call(c, g) == OK
+    assert call(c, g, pb(5, 3)) == OK
+    assert call(c, g, pb(0, 0)) == OK
+    assert call(None, g, pb()) == INV
+    assert call(c, None, pb()) == INV
+    assert call(c, g, pb(size=8)) == INV
+    assert call(c, g, pb(-1, 0)) == INV
+    assert call(c, g, pb(0, -2)) == INV
+    # copy-gather codes: a dtype the copy does not take, mismatched K / V
+    c, g = offsets_gather()
+    c.k.dtype = c.v.dtype = DType.S32
+    assert call(c, g, pb(1, 1)) == UNS
+    c, g = offsets_gather()
+    c.v.dtype = DType.F16 if c.k.dtype != DType.F16 else DType.BF16
+    assert call(c, g, pb(1, 1)) == INV
+    # dequantizing: both scales or neither; FP8 caches only
+    c, g = offsets_gather(dt=DType.F8_E4M3, io_dt=DType.BF16, L=0)
+    assert call(c, g, pb(4, 2), ks, vs) == OK
+    assert call(c, g, pb(4, 2), ks, None) == INV
+    assert call(c, g, pb(4, 2), None, vs) == INV
+    c, g = offsets_gather(dt=DType.BF16, L=0)
+    assert call(c, g, pb(4, 2), ks, vs) == UNS
+    # PACKED tables take the entry too (the counts are not read)
+    c, g = base_gather(L=0)
+    assert call(c, g, pb(1, 1)) == OK

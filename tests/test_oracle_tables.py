@@ -254,3 +254,22 @@ def test_workload_tables_match_packed():
     assert np.array_equal(ok, pk) and np.array_equal(ov, pv)
     assert W.gather_bytes(w, "ragged") - W.gather_bytes(w) == \
         (indices.size - w.block_table.size) * 4 + (S + 1) * 4
+
+
+def test_bound_offsets_marks_entries_past_their_pool():
+    """The KV_OFFSETS table the pool-bounded gather is checked against:
+    entries at or past their pool's count become an index past every pool;
+    a count of 0, or one above num_blocks, means num_blocks."""
+    from gpu_helpers import bound_offsets
+
+    S = np.uint32(1 << 31)
+    X = np.uint32(0x7FFFFFFF)
+    raw = np.array([[3, 7 | S, 9, 2 | S], [X, 12, 4 | S, 5 | S]], dtype=np.uint32)
+    got = bound_offsets(raw.view(np.int32), 10, (0, 5)).view(np.uint32)
+    want = np.array([[3, X, 9, 2 | S], [X, X, 4 | S, X]], dtype=np.uint32)
+    assert np.array_equal(got, want)
+    got = bound_offsets(raw.view(np.int32), 10, (4, 50)).view(np.uint32)
+    want = np.array([[3, 7 | S, X, 2 | S], [X, X, 4 | S, 5 | S]], dtype=np.uint32)
+    assert np.array_equal(got, want)
+    # no narrowing leaves the table as it is
+    assert np.array_equal(bound_offsets(raw.view(np.int32), 13, (0, 0)).view(np.uint32), raw)
