@@ -1985,7 +1985,7 @@ __global__ __launch_bounds__(kBlockThreads) void gather_tiles_kernel(TileArgs a)
           a.table)[(s * 2 + blockIdx.y) * a.max_blocks_per_seq + lb];
       const char *pool = (ent >> 31) ? a.pool[1] : a.pool[0];
       bid = ent & 0x7FFFFFFFu;
-      if (pool == nullptr || bid >= a.pool_blocks[ent >> 31]) return;
+      if (pool == nullptr || bid >= ((ent >> 31) ? a.pool_blocks[1] : a.pool_blocks[0])) return;
       blk = pool + bid * a.bytes_per_block;
     } else {
       bid = load_idx<I64>(a.table, s * a.max_blocks_per_seq + lb);
@@ -2174,13 +2174,13 @@ __global__ __launch_bounds__(kBlockThreads) void gather_indexed_kernel(GatherArg
                            s * 2 * (int64_t)a.max_blocks_per_seq;
       const uint32_t kidx = (uint32_t)row[lb];
       const uint32_t vidx = (uint32_t)row[a.max_blocks_per_seq + lb];
-      const char *kp = a.pool[kidx >> 31];
-      const char *vp = a.pool[vidx >> 31];
+      const char *kp = (kidx >> 31) ? a.pool[1] : a.pool[0];
+      const char *vp = (vidx >> 31) ? a.pool[1] : a.pool[0];
       const int64_t kb = kidx & 0x7FFFFFFFu;
       const int64_t vb = vidx & 0x7FFFFFFFu;
-      if (kp != nullptr && kb < a.pool_blocks[kidx >> 31])
+      if (kp != nullptr && kb < ((kidx >> 31) ? a.pool_blocks[1] : a.pool_blocks[0]))
         rk = kp + kb * a.bytes_per_block + o * a.gk.s_off;
-      if (vp != nullptr && vb < a.pool_blocks[vidx >> 31])
+      if (vp != nullptr && vb < ((vidx >> 31) ? a.pool_blocks[1] : a.pool_blocks[0]))
         rv = vp + vb * a.bytes_per_block + o * a.gv.s_off;
     }
     char *wk = a.dst_k + (s * a.max_seq_len + t) * a.out_row_bytes;
@@ -2236,9 +2236,9 @@ __device__ __forceinline__ const char *indexed_row(const GatherArgs &a, bool v, 
   } else {
     const uint32_t e = (uint32_t)reinterpret_cast<const int32_t *>(
         a.table)[(s * 2 + (v ? 1 : 0)) * (int64_t)a.max_blocks_per_seq + lb];
-    const char *pool = a.pool[e >> 31];
+    const char *pool = (e >> 31) ? a.pool[1] : a.pool[0];
     const int64_t idx = e & 0x7FFFFFFFu;
-    if (pool == nullptr || idx >= a.pool_blocks[e >> 31]) return nullptr;
+    if (pool == nullptr || idx >= ((e >> 31) ? a.pool_blocks[1] : a.pool_blocks[0])) return nullptr;
     return pool + idx * a.bytes_per_block + (int64_t)o * g.s_off;
   }
 }
@@ -2298,9 +2298,9 @@ __global__ __launch_bounds__((indexed_flat_threads<Op, FMT>())) void gather_inde
     const char *pv = (ev >> 31) ? a.pool[1] : a.pool[0];
     const int64_t kb = ek & 0x7FFFFFFFu;
     const int64_t vb = ev & 0x7FFFFFFFu;
-    if (pk != nullptr && kb < a.pool_blocks[ek >> 31])
+    if (pk != nullptr && kb < ((ek >> 31) ? a.pool_blocks[1] : a.pool_blocks[0]))
       tk = pk + kb * a.bytes_per_block + o0 * a.gk.s_off;
-    if (pv != nullptr && vb < a.pool_blocks[ev >> 31])
+    if (pv != nullptr && vb < ((ev >> 31) ? a.pool_blocks[1] : a.pool_blocks[0]))
       tv = pv + vb * a.bytes_per_block + o0 * a.gv.s_off;
     if (tk == nullptr && tv == nullptr) return;
   }
