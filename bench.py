@@ -37,9 +37,13 @@ stream_ceiling: plain streaming copy / read / write / widen kernels
 (libkvx_amd_probe.so, several launch shapes, the fastest reported) over the
 same byte count as the dominant kernel, on buffers beyond the 256 MB
 Infinity Cache: the best the box sustains with no index work (widen: the
-FP8 dequantizing gather's 8-byte loads and 16-byte stores).  For c3 also
-block_scatter / block_gather: the write's bytes copied into (and out of)
-the config's own randomly drawn pool blocks, with no slot or layout work.
+FP8 dequantizing gather's 8-byte loads and 16-byte stores).  Over each
+config's own pools and block table, with no slot, table, layout or
+conversion work: c3's block_scatter / block_gather (the write's bytes
+copied into, and out of, its randomly drawn blocks), and for the PACKED
+gathers of NHD caches block_gather (c1, c2, c5: the blocks the gather
+reads, in table order, copied to contiguous rows) or block_widen (c4: the
+same with 8-byte reads stored as 16-byte chunks).
 
 cpu_baseline: the CPU oracle's OpenMP fast path (row memcpy; table-driven
 casts for FP8) timed on this host's cores, threads pinned, over a bounded
@@ -213,6 +217,33 @@ def reshape_rows(w, name, heads=None, head_dim=None, room=1.0):
     if head_dim is not None:
         w.name = f"{w.name}_d{d}"
     w.heads, w.head_dim = h, d
+
+
+def gather_granules(w, pools, outs, dev):
+    """The granule probe's inputs for a PACKED gather of contiguous NHD
+    blocks: every buffer set is one layer's (K pool, V pool) with the shared
+    (K, V) outputs, and the map lists, sequence by sequence, the blocks that
+    hold its first min(seq_len, max_seq_len) rows; "gather" (copy) or
+    "widen" (FP8 cache, 16-bit outputs).  None when a listed id is outside
+    the pool or the outputs are too short."""
+    import numpy as np
+    import torch
+
+    bs = w.block_size
+    n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
+    ids = np.concatenate([w.block_table[s, :(int(n[s]) + bs - 1) // bs]
+                          for s in range(w.seq_count)]).astype(np.int64)
+    if ids.size == 0 or ids.min() < 0 or ids.max() >= w.num_blocks:
+        return None
+    widen = w.cache_dtype != w.io_dtype
+    kc = pools[0][0]
+    gb = kc.stride(0) * kc.element_size()
+    ko = outs[0]
+    if ids.size * gb * (2 if widen else 1) > ko.numel() * ko.element_size():
+        return None
+    blk = torch.tensor(ids, dtype=torch.int64, device=dev)
+    sets = [(k, v, outs[0].view(-1), outs[1].view(-1)) for k, v in pools]
+    return sets, blk, ("widen",) if widen else ("gather",)
 
 
 def build_config(name: str, dev, layers_override=None, table_fmt="packed",
@@ -431,6 +462,11 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
             n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
             extra["pool_copy"] = (pools, (ko, vo), int(n.sum()) * w.heads * w.head_dim
                                   * W.dtype_bytes(w.cache_dtype))
+        if table_fmt == "packed" and w.k_layout == w.v_layout == Layout.BLOCK_NHD:
+            gran = gather_granules(w, pools[:4], (ko, vo), dev)
+            if gran is not None:
+                keep.append(gran[1])
+                extra["granules"] = gran
         cfg = {"layers": layers}
     elif name == "c3":
         # four rotating buffer sets (> the 256 MB Infinity Cache)
@@ -455,7 +491,7 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
                 and (grp == grp[:, :1] + np.arange(bs)).all() and (grp[:, 0] % bs == 0).all()):
             blk = torch.tensor(grp[:, 0] // bs, dtype=torch.int64, device=dev)
             keep.append(blk)
-            extra["granules"] = (sets, blk)
+            extra["granules"] = (sets, blk, ("scatter", "gather"))
         cfg = {"buffer_sets": 4, "block_order": c3_order}
     else:  # c5
         pc, gc = cache_for(w)
@@ -469,6 +505,10 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
             n = np.minimum(np.maximum(w.seq_lens.astype(np.int64), 0), w.max_seq_len)
             extra["pool_copy"] = ([(gc.key_cache, gc.value_cache)], (ko, vo),
                                   int(n.sum()) * w.heads * w.head_dim * 2)
+            gran = gather_granules(w, [(gc.key_cache, gc.value_cache)], (ko, vo), dev)
+            if gran is not None:
+                keep.append(gran[1])
+                extra["granules"] = gran
     torch.cuda.synchronize()
     if table_fmt != "packed":
         w.name = f"{w.name}_{table_fmt}"
@@ -583,6 +623,7 @@ class Probe:
         L.kvx_probe_widen.argtypes = [vp, vp, i64, i, vp]
         L.kvx_probe_shape.argtypes = [i, C.POINTER(i), C.POINTER(i)]
         L.kvx_probe_granules.argtypes = [vp, vp, i64, vp, i, i, i, vp]
+        L.kvx_probe_granules_widen.argtypes = [vp, vp, i64, vp, i, i, vp]
         self.L = L
         self.shapes = []
         for k in range(L.kvx_probe_shapes()):
@@ -656,14 +697,16 @@ class Probe:
         torch.cuda.empty_cache()
         return out
 
-    def granules(self, sets, blk, scatter, stream, reps=6):
-        """The data movement of a paged write (scatter) or gather over a
-        config's own block table and pools, with no slot, table or layout
-        work: for every buffer set (K pool, V pool, K rows, V rows), one
-        launch copies the K rows into (or out of) the pool blocks that `blk`
-        names and one the V rows; HIP events time the pair.  Granule = one
-        cache block, whose bytes the pool's block stride gives.  Fastest
-        shape: {bytes per pair, GB/s, frac, shape, mean us, by shape}."""
+    def granules(self, sets, blk, mode, stream, reps=6):
+        """The data movement of a paged write ("scatter"), gather ("gather")
+        or FP8 -> 16-bit dequantizing gather ("widen": 8-byte reads, each
+        stored as one 16-byte chunk) over a config's own block table and
+        pools, with no slot, table, layout or conversion work: for every
+        buffer set (K pool, V pool, K rows, V rows), one launch moves the K
+        rows into (or out of) the pool blocks that `blk` names and one the V
+        rows; HIP events time the pair.  Granule = one cache block, whose
+        bytes the pool's block stride gives.  Fastest shape: {bytes per
+        pair, GB/s, frac, shape, mean us, by shape}."""
         import torch
 
         kc = sets[0][0]
@@ -671,9 +714,10 @@ class Probe:
         if gb & (gb - 1) or gb < 16:
             raise ValueError("granule (block bytes) must be a power of two >= 16")
         glog = gb.bit_length() - 1
-        nbytes = blk.numel() * gb
+        nbytes = blk.numel() * gb  # pool bytes per tensor
+        rows_bytes = 2 * nbytes if mode == "widen" else nbytes
         for kp, vp_, kr, vr in sets:
-            if min(kr.numel() * kr.element_size(), vr.numel() * vr.element_size()) < nbytes:
+            if min(kr.numel() * kr.element_size(), vr.numel() * vr.element_size()) < rows_bytes:
                 raise ValueError("rows shorter than the mapped blocks")
             if int(blk.max()) >= kp.shape[0] or int(blk.max()) >= vp_.shape[0]:
                 raise ValueError("block map past a pool")
@@ -682,9 +726,15 @@ class Probe:
         for k, shape in enumerate(self.shapes):
             def one(st):
                 for pool, rows_ in ((st[0], st[2]), (st[1], st[3])):
-                    if self.L.kvx_probe_granules(pool.data_ptr(), rows_.data_ptr(), nbytes,
-                                                 blk.data_ptr(), glog, int(scatter), k, sh):
-                        raise RuntimeError(f"granule probe shape {shape} failed")
+                    if mode == "widen":
+                        rc = self.L.kvx_probe_granules_widen(rows_.data_ptr(), pool.data_ptr(),
+                                                             nbytes, blk.data_ptr(), glog, k, sh)
+                    else:
+                        rc = self.L.kvx_probe_granules(pool.data_ptr(), rows_.data_ptr(), nbytes,
+                                                       blk.data_ptr(), glog,
+                                                       int(mode == "scatter"), k, sh)
+                    if rc:
+                        raise RuntimeError(f"granule probe {mode} shape {shape} failed")
             for st in sets:
                 one(st)
             evs = []
@@ -698,10 +748,11 @@ class Probe:
                     evs.append((e0, e1))
             torch.cuda.synchronize()
             ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
-            gbps = 4 * nbytes / (ms / 1e3) / 1e9
+            moved = 2 * (nbytes + rows_bytes)  # K and V: pool side + rows side
+            gbps = moved / (ms / 1e3) / 1e9
             every[f"{shape[0]}x{shape[1]}"] = round(gbps, 1)
             if best is None or gbps > best["GBps"]:
-                best = {"bytes_per_launch": 4 * nbytes, "GBps": round(gbps, 1),
+                best = {"bytes_per_launch": moved, "GBps": round(gbps, 1),
                         "frac": round(gbps / PEAK_HBM_GBS, 4), "shape": list(shape),
                         "mean_us": round(ms * 1e3, 2)}
         best["GBps_by_shape"] = every
@@ -992,9 +1043,9 @@ def stream_ceilings(b, nbytes, stream):
         ceiling["pool_copy"] = probe.pool_copy(pools, outs, n, ceiling["copy"]["shape"],
                                                stream)
     if "granules" in b.extra:
-        sets, blk = b.extra["granules"]
-        ceiling["block_scatter"] = probe.granules(sets, blk, True, stream)
-        ceiling["block_gather"] = probe.granules(sets, blk, False, stream)
+        sets, blk, modes = b.extra["granules"]
+        for mode in modes:
+            ceiling[f"block_{mode}"] = probe.granules(sets, blk, mode, stream)
     return ceiling
 
 
@@ -1086,7 +1137,7 @@ def compact_ceiling(c):
         pc = c["pool_copy"]
         out["pool_copy"] = {"GBps": pc["GBps"], "frac": pc["frac"], "shape": pc["shape"],
                             "layer_us": [min(pc["by_layer_us"]), max(pc["by_layer_us"])]}
-    for op in ("block_scatter", "block_gather"):
+    for op in ("block_scatter", "block_gather", "block_widen"):
         if op in c:
             out[op] = {"GBps": c[op]["GBps"], "frac": c[op]["frac"], "shape": c[op]["shape"]}
     return out
@@ -1110,7 +1161,7 @@ def compact_config(r):
     if r.get("stream_ceiling"):
         out["ceiling_frac"] = {op: r["stream_ceiling"][op]["frac"]
                                for op in ("copy", "widen", "pool_copy", "block_scatter",
-                                          "block_gather")
+                                          "block_gather", "block_widen")
                                if op in r["stream_ceiling"]}
     c = r.get("cpu_baseline")
     if c:

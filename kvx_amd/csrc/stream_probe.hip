@@ -12,7 +12,10 @@
 //   scatter  copies n contiguous bytes into granules of a pool named by a
 //          granule map (or gathers them back): the data movement of a
 //          paged KV write (or gather) over a given block table, with no
-//          slot, table or layout work.
+//          slot, table or layout work;
+//   granule widen  reads n bytes from the mapped granules as 8-byte chunks
+//          and writes each as one 16-byte chunk of a contiguous buffer: the
+//          FP8 dequantizing gather's access pattern over a given table.
 //
 // Each kernel is instantiated in a few launch shapes (threads per
 // workgroup x 16-byte chunks per lane, every chunk of a workgroup in flight
@@ -127,6 +130,35 @@ __global__ __launch_bounds__(T) void granule_kernel(u32x4 *pool, u32x4 *lin, con
   }
 }
 
+// Granule widen: 8-byte chunk i of the read side is chunk
+// (map[i >> g8_log2] << g8_log2) + (i & (2^g8_log2 - 1)) of the pool, and
+// is stored twice over as 16-byte chunk i of out.
+template <int T, int U>
+__global__ __launch_bounds__(T) void granule_widen_kernel(const u32x2 *pool, u32x4 *out,
+                                                          const int64_t *map, int g8_log2,
+                                                          int64_t n) {
+  const int64_t base = (int64_t)blockIdx.x * (T * U) + threadIdx.x;
+  const int64_t mask = ((int64_t)1 << g8_log2) - 1;
+  u32x2 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    if (i < n) v[u] = __builtin_nontemporal_load(pool + (map[i >> g8_log2] << g8_log2) + (i & mask));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + (int64_t)u * T;
+    if (i < n) {
+      u32x4 w;
+      w[0] = v[u][0];
+      w[1] = v[u][1];
+      w[2] = v[u][0];
+      w[3] = v[u][1];
+      __builtin_nontemporal_store(w, out + i);
+    }
+  }
+}
+
 struct Shape {
   int threads;
   int unroll;
@@ -165,42 +197,50 @@ void launch(int op, void *dst, const void *src, int64_t n, uint32_t value, int64
 
 // bytes: bytes read (copy, read, widen) or written (write).  The grid
 // covers n = bytes / 16 chunks, or bytes / 8 for widen.
+// mode 0 scatter, 1 gather (16-byte chunks, n of them, gran_log2 = log2 of
+// a granule's 16-byte chunks); 2 widen (8-byte chunks, n of them, the
+// granule's log2 in 8-byte chunks passed the same way).
 template <int T, int U>
-void launch_granule(bool scatter, void *pool, void *lin, const int64_t *map, int g16_log2,
+void launch_granule(int mode, void *pool, void *lin, const int64_t *map, int gran_log2,
                     int64_t n, int64_t g, hipStream_t s) {
   const dim3 grid((uint32_t)g), block(T);
-  if (scatter)
+  if (mode == 2)
+    hipLaunchKernelGGL((granule_widen_kernel<T, U>), grid, block, 0, s,
+                       static_cast<const u32x2 *>(pool), static_cast<u32x4 *>(lin), map,
+                       gran_log2, n);
+  else if (mode == 0)
     hipLaunchKernelGGL((granule_kernel<T, U, true>), grid, block, 0, s, static_cast<u32x4 *>(pool),
-                       static_cast<u32x4 *>(lin), map, g16_log2, n);
+                       static_cast<u32x4 *>(lin), map, gran_log2, n);
   else
     hipLaunchKernelGGL((granule_kernel<T, U, false>), grid, block, 0, s,
-                       static_cast<u32x4 *>(pool), static_cast<u32x4 *>(lin), map, g16_log2, n);
+                       static_cast<u32x4 *>(pool), static_cast<u32x4 *>(lin), map, gran_log2, n);
 }
 
-int run_granule(bool scatter, int shape, void *pool, void *lin, int64_t bytes, const int64_t *map,
+int run_granule(int mode, int shape, void *pool, void *lin, int64_t bytes, const int64_t *map,
                 int granule_log2, void *stream) {
   if (shape < 0 || shape >= kNumShapes || bytes < 0 || granule_log2 < 4 || granule_log2 > 40 ||
       bytes % ((int64_t)1 << granule_log2) != 0 || (uintptr_t)pool % 16 != 0 ||
       (uintptr_t)lin % 16 != 0 || (uintptr_t)map % 8 != 0)
     return 1;
-  const int64_t n = bytes / 16;
+  const int chunk_log2 = mode == 2 ? 3 : 4;  // bytes per chunk of the pool side
+  const int64_t n = bytes >> chunk_log2;
   if (n == 0) return 0;
   const int64_t g = grid_for(n, kShapes[shape]);
   if (g == 0) return 1;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int g16 = granule_log2 - 4;
+  const int gl = granule_log2 - chunk_log2;
   switch (shape) {
-    case 0: launch_granule<64, 1>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 1: launch_granule<64, 4>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 2: launch_granule<128, 1>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 3: launch_granule<128, 2>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 4: launch_granule<128, 4>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 5: launch_granule<256, 1>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 6: launch_granule<256, 2>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 7: launch_granule<256, 4>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 8: launch_granule<512, 1>(scatter, pool, lin, map, g16, n, g, s); break;
-    case 9: launch_granule<512, 2>(scatter, pool, lin, map, g16, n, g, s); break;
-    default: launch_granule<1024, 1>(scatter, pool, lin, map, g16, n, g, s); break;
+    case 0: launch_granule<64, 1>(mode, pool, lin, map, gl, n, g, s); break;
+    case 1: launch_granule<64, 4>(mode, pool, lin, map, gl, n, g, s); break;
+    case 2: launch_granule<128, 1>(mode, pool, lin, map, gl, n, g, s); break;
+    case 3: launch_granule<128, 2>(mode, pool, lin, map, gl, n, g, s); break;
+    case 4: launch_granule<128, 4>(mode, pool, lin, map, gl, n, g, s); break;
+    case 5: launch_granule<256, 1>(mode, pool, lin, map, gl, n, g, s); break;
+    case 6: launch_granule<256, 2>(mode, pool, lin, map, gl, n, g, s); break;
+    case 7: launch_granule<256, 4>(mode, pool, lin, map, gl, n, g, s); break;
+    case 8: launch_granule<512, 1>(mode, pool, lin, map, gl, n, g, s); break;
+    case 9: launch_granule<512, 2>(mode, pool, lin, map, gl, n, g, s); break;
+    default: launch_granule<1024, 1>(mode, pool, lin, map, gl, n, g, s); break;
   }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
@@ -274,7 +314,17 @@ int kvx_probe_widen(void *dst, const void *src, int64_t bytes, int shape, void *
 // entry must name a granule inside the pool; it is not checked.
 int kvx_probe_granules(void *pool, void *lin, int64_t bytes, const int64_t *map,
                        int granule_log2, int scatter, int shape, void *stream) {
-  return run_granule(scatter != 0, shape, pool, lin, bytes, map, granule_log2, stream);
+  return run_granule(scatter != 0 ? 0 : 1, shape, pool, lin, bytes, map, granule_log2, stream);
+}
+
+// Reads `bytes` (a whole number of granules, 2^granule_log2 >= 16 bytes
+// each) from the pool granules that map names, 8 bytes at a time, and
+// writes 2 * bytes to out: 8-byte chunk i of the read side, stored twice
+// over, is 16-byte chunk i of out.  Every map entry must name a granule
+// inside the pool; it is not checked.
+int kvx_probe_granules_widen(void *out, const void *pool, int64_t bytes, const int64_t *map,
+                             int granule_log2, int shape, void *stream) {
+  return run_granule(2, shape, const_cast<void *>(pool), out, bytes, map, granule_log2, stream);
 }
 
 }  // extern "C"

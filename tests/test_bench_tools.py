@@ -214,3 +214,35 @@ def test_granule_probe_moves_the_mapped_blocks():
         assert torch.equal(back.cpu(), rows), shape
     assert p.L.kvx_probe_granules(pool.data_ptr(), lin.data_ptr(), gb + 16, m.data_ptr(), glog,
                                   1, 0, sh) == 1
+
+
+@pytest.mark.gpu
+def test_granule_widen_probe_reads_the_mapped_blocks():
+    """kvx_probe_granules_widen in every shape: 8-byte chunk i of the mapped
+    pool granules is 16-byte chunk i of the output, stored twice over; bytes
+    past the output's end stay as they were."""
+    import torch
+
+    from kvx_amd import build as kbuild
+
+    if not kbuild.PROBE_LIB.exists():
+        pytest.skip("libkvx_amd_probe.so is not built")
+    p = bench.Probe()
+    glog, ng, npool = 9, 20, 48  # 512-byte granules, 20 of a 48-granule pool
+    gb = 1 << glog
+    g = torch.Generator().manual_seed(11)
+    blk = torch.randperm(npool, generator=g)[:ng].to(torch.int64)
+    pool_h = torch.randint(0, 256, (npool * gb,), dtype=torch.uint8, generator=g)
+    read = pool_h.view(npool, gb)[blk].reshape(-1, 8)
+    want = torch.cat([read, read], dim=1).reshape(-1)
+    pool, m = pool_h.cuda(), blk.cuda()
+    sh = torch.cuda.current_stream().cuda_stream
+    for k, shape in enumerate(p.shapes):
+        out = torch.full((2 * ng * gb + 64,), 0xEE, dtype=torch.uint8, device="cuda")
+        assert p.L.kvx_probe_granules_widen(out.data_ptr(), pool.data_ptr(), ng * gb, m.data_ptr(),
+                                            glog, k, sh) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out[:2 * ng * gb].cpu(), want), shape
+        assert bool((out[2 * ng * gb:] == 0xEE).all()), shape
+    assert p.L.kvx_probe_granules_widen(out.data_ptr(), pool.data_ptr(), gb + 8, m.data_ptr(),
+                                        glog, 0, sh) == 1
