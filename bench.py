@@ -22,7 +22,8 @@ valid K/V row read once and written once, plus the index arrays used
 
 roofline: the dominant kernel (the gather): its algorithmic bytes per
 launch / its mean launch duration, measured with HIP events recorded on the
-launch stream around every launch inside the timed region.  `traffic` is
+launch stream after every launch inside the timed region (a launch runs from
+the event before it to its own).  `traffic` is
 the HBM bytes per launch of the committed rocprofv3 counter summary
 (profiles/traffic_<kind>_<workload>.json), used only when that summary was
 taken of the same algorithmic bytes and of the kernel sources now in the
@@ -528,9 +529,14 @@ def build_config(name: str, dev, layers_override=None, table_fmt="packed",
 # Timing.
 
 def time_launches(steps, K, W, stream):
-    """W untimed warmup steps, then K steps with HIP events around every
-    launch and around the whole region.  Returns (total ms, [(ms, launch)],
-    wall seconds)."""
+    """W untimed warmup steps, then K steps with one HIP event after every
+    launch: a launch's time runs from the event before it (the previous
+    launch's, or the region's start) to its own, so it includes the gap
+    after the previous kernel.  One event per launch instead of a pair
+    around each: every event record on the stream costs the timed region
+    time of its own (c2, same process: 49.58 ms per step with a pair around
+    every launch, 49.25 with a pair around each gather only, 49.05 with
+    none).  Returns (total ms, [(ms, launch)], wall seconds)."""
     import torch
 
     sh = stream.cuda_stream
@@ -539,10 +545,8 @@ def time_launches(steps, K, W, stream):
             launch(sh)
     torch.cuda.synchronize()
     per_step = [steps[i % len(steps)] for i in range(K)]
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(sum(len(s) for s in per_step))]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(sum(len(s) for s in per_step))]
     t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(stream)
@@ -550,17 +554,17 @@ def time_launches(steps, K, W, stream):
     order = []
     for s in per_step:
         for launch in s:
-            e0, e1 = evs[k]
-            e0.record(stream)
             launch(sh)
-            e1.record(stream)
+            evs[k].record(stream)
             order.append(launch)
             k += 1
-    t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    return (t_start.elapsed_time(t_end),
-            [(e0.elapsed_time(e1), l) for (e0, e1), l in zip(evs, order)], wall)
+    timed, prev = [], t_start
+    for e, l in zip(evs, order):
+        timed.append((prev.elapsed_time(e), l))
+        prev = e
+    return t_start.elapsed_time(evs[-1]), timed, wall
 
 
 def summarize(ms_total, timed, K):
