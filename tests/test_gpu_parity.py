@@ -5,8 +5,8 @@ Covers the reference's own kernel-test cases (tests/kvx_kernel_test.cu),
 every layout (NHD, HND, HND_PACKED, mixed K/V), F32/F16/BF16/FP8 payloads,
 S32/S64 indices, -1 slots, out-of-range blocks, padded strides, odd head
 dims and misaligned buffers (narrower chunk widths), the prefill entry, the
-kvx_abi.h entry points, non-default streams, and reduced versions of the five
-BASELINE configurations.
+kvx_abi.h entry points, non-default and concurrent streams, and reduced
+versions of the five BASELINE configurations.
 """
 import numpy as np
 import pytest
@@ -15,7 +15,7 @@ import torch
 from kvx_amd import paged, workloads
 from kvx_amd.abi import DType, Layout, Status
 
-from gpu_helpers import TORCH_DT, check_gather, check_write, make_cache, random_fill
+from gpu_helpers import TORCH_DT, check_gather, check_write, make_cache, np_bytes, random_fill
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -148,6 +148,57 @@ def test_non_default_stream():
     torch.cuda.synchronize()
     check_write(pc, kb, vb, key, val, slots, io_dtype=DType.BF16, cache_dtype=DType.BF16,
                 stream=s)
+
+
+def test_two_streams_interleaved_on_separate_caches():
+    """Writes and gathers on two streams, enqueued alternately with no
+    synchronization between the streams, each on its own cache (NHD, and
+    x-packed K with NHD V, so different kernels run side by side): the
+    library keeps no state between calls, so each cache and each gather
+    output must equal the oracle applying that stream's calls in order."""
+    import oracle
+
+    gen = torch.Generator().manual_seed(61)
+    H, D, bs, nb, S, mbps = 8, 128, 16, 384, 12, 32
+    dt = DType.BF16
+    caches = [make_cache(NHD, NHD, dt, nb, bs, H, D, gen=gen),
+              make_cache(PK, NHD, dt, nb, bs, H, D, gen=gen)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    expect = [[np_bytes(kb.base), np_bytes(vb.base)] for _, kb, vb in caches]
+    launched = []
+    torch.cuda.synchronize()
+    for rnd in range(3):
+        for c, ((pc, kb, vb), s) in enumerate(zip(caches, streams)):
+            slots = torch.randperm(nb * bs, generator=gen)[:700].to(DEV)
+            key, val = rows(700, H, D, dt, gen), rows(700, H, D, dt, gen)
+            table = torch.randperm(nb, generator=gen)[:S * mbps].reshape(S, mbps)
+            table = table.to(torch.int32).to(DEV)
+            lens = torch.randint(0, mbps * bs + 1, (S,), generator=gen).to(torch.int32).to(DEV)
+            ko = random_fill(torch.empty((S, mbps * bs, H, D), dtype=TORCH_DT[dt], device=DEV), gen)
+            vo = random_fill(torch.empty_like(ko), gen)
+            ko0, vo0 = np_bytes(ko), np_bytes(vo)
+            # inputs are ready on the default stream before the side streams use them
+            s.wait_stream(torch.cuda.current_stream())
+            assert paged.write_kv(pc, key, val, slots, stream=s) == Status.OK
+            assert paged.gather_kv(pc, ko, vo, table, lens, mbps * bs, stream=s) == Status.OK
+            launched.append((c, key, val, slots, table, lens, ko, vo, ko0, vo0))
+    torch.cuda.synchronize()
+    for c, key, val, slots, table, lens, ko, vo, ko0, vo0 in launched:
+        pc, kb, vb = caches[c]
+        kexp, vexp = expect[c]
+        oracle.write_kv(kb.geometry(), vb.geometry(), np_bytes(key), np_bytes(val), kexp, vexp,
+                        slots.cpu().numpy(), heads=H, head_dim=D, block_size=bs,
+                        num_blocks=nb, io_dtype=dt, cache_dtype=dt)
+        oracle.gather_kv(kb.geometry(), vb.geometry(), kexp, vexp, ko0, vo0,
+                         table.cpu().numpy(), lens.cpu().numpy(), seq_count=S,
+                         max_blocks_per_seq=mbps, max_seq_len=mbps * bs, heads=H,
+                         head_dim=D, block_size=bs, num_blocks=nb, cache_dtype=dt,
+                         io_dtype=dt)
+        assert np.array_equal(np_bytes(ko), ko0)
+        assert np.array_equal(np_bytes(vo), vo0)
+    for c, (pc, kb, vb) in enumerate(caches):
+        assert np.array_equal(np_bytes(kb.base), expect[c][0])
+        assert np.array_equal(np_bytes(vb.base), expect[c][1])
 
 
 def test_empty_and_all_invalid_batches_leave_cache_untouched():
