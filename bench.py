@@ -6,7 +6,7 @@
     python bench.py --sweep c3 [--sweep-scales 1,2,4,8]  size sweep of c3
     python bench.py --copy-probe                       rocprofv3 calibration
 
-Headline: Llama-3-8B-shaped decode, bf16, 32 layers,
+Headline (benchmark configuration c2): Llama-3-8B-shaped decode, bf16, 32 layers,
 8 KV heads x 128, block_size 16, batch 256, contexts U[512, 8192], 5% of
 slots -1.  One step = for each of the 32 layers (each with its own ~4.6 GB
 paged K+V pool): the decode write of 256 new tokens, then the gather of
@@ -29,7 +29,7 @@ the HBM bytes per launch of the committed rocprofv3 counter summary
 taken of the same algorithmic bytes and of the kernel sources now in the
 tree (sha256 of kvx_amd/csrc's kernel files); otherwise null.
 
-configs: the other BASELINE configurations, each timed the same way in the
+configs: the other benchmark configurations, each timed the same way in the
 same run (c1 TinyLlama, c3 chunked prefill write, c4 FP8 E4M3 decode with a
 dequantizing gather, c5 Llama-3-70B bs32 on a ~200 GB pool), each with its
 kernels' mean / median, GB/s, fraction of peak and its own CPU baseline.

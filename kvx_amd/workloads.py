@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads for the five BASELINE configurations.
+"""Seeded synthetic workloads for the five benchmark configurations (c1-c5).
 
 Each function returns a `Workload` that holds only the index metadata
 (slot mapping, block table, sequence lengths) as numpy arrays plus the shapes

@@ -1,4 +1,4 @@
-"""Full-size BASELINE configurations on the GPU, checked through properties
+"""Full-size benchmark configurations (c1-c5) on the GPU, checked through properties
 that do not need the CPU oracle to run at that size:
 
   - write -> gather round trip: every written row comes back bit-exact at its

@@ -6,7 +6,7 @@ every layout (NHD, HND, HND_PACKED, mixed K/V), F32/F16/BF16/FP8 payloads,
 S32/S64 indices, -1 slots, out-of-range blocks, padded strides, odd head
 dims and misaligned buffers (narrower chunk widths), the prefill entry, the
 kvx_abi.h entry points, non-default and concurrent streams, and reduced
-versions of the five BASELINE configurations.
+versions of the five benchmark configurations (c1-c5).
 """
 import numpy as np
 import pytest
@@ -287,7 +287,7 @@ def test_fp8_scale_from_raw_pointer_and_byte_copies():
 
 
 # ---------------------------------------------------------------------------
-# Reduced BASELINE configurations, oracle-checked end to end.
+# Reduced benchmark configurations (c1-c5), oracle-checked end to end.
 
 def _run_workload(w, gen, v_layout=None, scale_k=None, scale_v=None, sigma=1.0):
     vl = w.v_layout if v_layout is None else v_layout
